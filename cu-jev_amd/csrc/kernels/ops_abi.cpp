@@ -1,0 +1,60 @@
+/* libcujev_ops.so: the operator-level C ABI (include/cujev_ops.h). Thin
+ * argument checks around the launchers of kernels.h. */
+#include "../../../include/cujev_ops.h"
+#include "kernels.h"
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#define EXPORT extern "C" __attribute__((visibility("default")))
+
+static thread_local char g_err[512];
+
+static int fail(int status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+static int launched(hipError_t e, const char *what) {
+    if (e == hipErrorInvalidValue)
+        return fail(1, "%s: unsupported shape", what);
+    if (e != hipSuccess)
+        return fail(4, "%s: %s", what, hipGetErrorString(e));
+    g_err[0] = 0;
+    return 0;
+}
+
+EXPORT int cujev_ops_kv_stride(int max_tokens) { return cujev_kv_stride(max_tokens); }
+EXPORT const char *cujev_ops_last_error(void) { return g_err; }
+
+EXPORT int cujev_op_attn_prep(const void *proj, int proj_stride, const float *q_norm_w,
+                              const float *k_norm_w, const int32_t *pos, int N, int Hq, int Hkv,
+                              int rot, double theta, float eps, float q_scale, void *q_out,
+                              void *k_cache, void *vt_cache, int cache_stride, void *stream) {
+    if (N < 0 || Hkv <= 0 || rot <= 0 || rot > 64 || cache_stride % 64)
+        return fail(1, "attn_prep: bad arguments");
+    float inv[32];
+    for (int i = 0; i < rot / 2; i++)
+        inv[i] = (float)(1.0 / pow(theta, 2.0 * i / rot));
+    return launched(k_attn_prep((const bf16_t *)proj, proj_stride, q_norm_w, k_norm_w, pos, N, Hq,
+                                Hkv, rot, inv, eps, q_scale, (bf16_t *)q_out, (bf16_t *)k_cache,
+                                (bf16_t *)vt_cache, cache_stride, (hipStream_t)stream),
+                    "attn_prep");
+}
+
+EXPORT int cujev_op_attention(const void *q, const void *gate, int gate_tok_stride,
+                              int gate_head_stride, const void *pk, const void *pvt, int P,
+                              int p_stride, const void *ok, const void *ovt, int o_stride,
+                              const int32_t *own_base, int N, int Hq, int Hkv, void *out,
+                              void *stream) {
+    if (N < 0 || P < 0 || Hkv <= 0)
+        return fail(1, "attention: bad arguments");
+    return launched(k_attention((const bf16_t *)q, (const bf16_t *)gate, gate_tok_stride,
+                                gate_head_stride, (const bf16_t *)pk, (const bf16_t *)pvt, P,
+                                p_stride, (const bf16_t *)ok, (const bf16_t *)ovt, o_stride,
+                                own_base, N, Hq, Hkv, (bf16_t *)out, (hipStream_t)stream),
+                    "attention");
+}

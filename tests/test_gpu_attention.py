@@ -1,0 +1,221 @@
+"""GPU parity of the shared-prefix gated GQA attention and its prep kernel.
+
+Calls the kernels through the operator C ABI (libcujev_ops.so) and compares
+with the CPU oracle (oracle/qwen35.py) on the same seeded bf16 inputs.
+Tolerance: max |gpu - oracle| / max |oracle| <= 1e-2 on the bf16 outputs
+(the target bar for bf16 layer outputs is 2e-2).
+"""
+import math
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import qwen35 as orc  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+D = 256
+
+
+def ops():
+    from cujev import ops as o
+    o.load()
+    return o
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def bf(x):
+    return torch.as_tensor(np.asarray(x, np.float32)).to(torch.bfloat16)
+
+
+def np32(t):
+    return t.float().cpu().numpy()
+
+
+def make_case(seed, Hq, Hkv, P, seg_lens, stride_tokens=None):
+    rng = np.random.default_rng(seed)
+    N = int(sum(seg_lens))
+    q = orc.bf16_round(rng.standard_normal((N, Hq, D)).astype(np.float32) * 0.6)
+    gate = orc.bf16_round(rng.standard_normal((N, Hq, D)).astype(np.float32))
+    ks = orc.bf16_round(rng.standard_normal((P, Hkv, D)).astype(np.float32))
+    vs = orc.bf16_round(rng.standard_normal((P, Hkv, D)).astype(np.float32))
+    ko = orc.bf16_round(rng.standard_normal((N, Hkv, D)).astype(np.float32))
+    vo = orc.bf16_round(rng.standard_normal((N, Hkv, D)).astype(np.float32))
+    own_base = np.zeros(N, np.int32)
+    s = 0
+    for L in seg_lens:
+        own_base[s: s + L] = s
+        s += L
+    return q, gate, ks, vs, ko, vo, own_base
+
+
+def run_attention(o, q, gate, ks, vs, ko, vo, own_base, Hq, Hkv):
+    dev = "cuda"
+    N, P = q.shape[0], ks.shape[0]
+    ps = o.kv_stride(max(P, 1))
+    os_ = o.kv_stride(N)
+    pk = torch.zeros(Hkv, ps, D, dtype=torch.bfloat16, device=dev)
+    pvt = torch.zeros(Hkv, D, ps, dtype=torch.bfloat16, device=dev)
+    if P:
+        pk[:, :P] = bf(ks.transpose(1, 0, 2)).to(dev)
+        pvt[:, :, :P] = bf(vs.transpose(1, 2, 0)).to(dev)
+    ok = torch.zeros(Hkv, os_, D, dtype=torch.bfloat16, device=dev)
+    ovt = torch.zeros(Hkv, D, os_, dtype=torch.bfloat16, device=dev)
+    ok[:, :N] = bf(ko.transpose(1, 0, 2)).to(dev)
+    ovt[:, :, :N] = bf(vo.transpose(1, 2, 0)).to(dev)
+    # the gate lives in the second half of a fused [q | gate] row per head
+    qg = torch.zeros(N, Hq, 2 * D, dtype=torch.bfloat16, device=dev)
+    qg[:, :, D:] = bf(gate).to(dev)
+    qd = bf(q * orc.LOG2E / 16.0).to(dev)  # the prep kernel's prescaling
+    out = torch.empty(N, Hq * D, dtype=torch.bfloat16, device=dev)
+    ob = torch.as_tensor(own_base).to(dev)
+    o.attention(qd, qg[:, :, D:], Hq * 2 * D, 2 * D, pk, pvt, P, ps, ok, ovt, os_, ob, Hq, Hkv, out)
+    torch.cuda.synchronize()
+    return np32(out).reshape(N, Hq, D), np32(qd)
+
+
+def oracle_attention(qd_scaled, gate, ks, vs, ko, vo, own_base):
+    # qd_scaled holds bf16(q * log2e / 16); scores in natural-log units are
+    # qd.k * ln 2, so the same probabilities as the kernel's exp2.
+    return orc.shared_prefix_attention(qd_scaled.astype(np.float64), gate, ks, vs, ko, vo,
+                                       own_base, scale=math.log(2.0), bf16_p=True)
+
+
+CASES = [
+    # (seed, Hq, Hkv, P, seg_lens)
+    (1, 8, 2, 100, [1, 17, 33]),
+    (2, 8, 2, 0, [300]),                  # prefill: P = 0, one causal segment
+    (3, 8, 2, 512, [32, 32, 32, 32]),     # config 1 shape (4 branches x 32)
+    (4, 16, 4, 64, [16] * 10),            # many short branches, P on a tile edge
+    (5, 4, 1, 65, [1] * 40 + [70]),       # one-token branches then a long one
+    (6, 8, 2, 1, [5, 64, 2]),
+]
+
+
+@pytest.mark.parametrize("seed,Hq,Hkv,P,seg_lens", CASES)
+def test_attention_matches_oracle(seed, Hq, Hkv, P, seg_lens):
+    o = ops()
+    print(f"case seed={seed} Hq={Hq} Hkv={Hkv} P={P} segs={seg_lens}", flush=True)
+    q, gate, ks, vs, ko, vo, ob = make_case(seed, Hq, Hkv, P, seg_lens)
+    got, qd = run_attention(o, q, gate, ks, vs, ko, vo, ob, Hq, Hkv)
+    ref = oracle_attention(qd, gate, ks, vs, ko, vo, ob)
+    err = rel_err(got, ref)
+    print(f"rel err {err:.3e}")
+    assert err <= TOL
+
+
+def test_attention_branch_isolation():
+    """A branch's output does not depend on its siblings (bit-exact: the
+    kernel's per-row arithmetic does not depend on which rows share a tile
+    only through the visible keys)."""
+    o = ops()
+    Hq, Hkv, P = 8, 2, 130
+    q, gate, ks, vs, ko, vo, ob = make_case(11, Hq, Hkv, P, [7, 20, 9])
+    both, _ = run_attention(o, q, gate, ks, vs, ko, vo, ob, Hq, Hkv)
+    # the middle branch alone
+    sl = slice(7, 27)
+    alone, _ = run_attention(o, q[sl], gate[sl], ks, vs, ko[sl], vo[sl],
+                             np.zeros(20, np.int32), Hq, Hkv)
+    assert rel_err(alone, both[sl]) <= 1e-2
+
+
+def test_attn_prep_matches_oracle():
+    o = ops()
+    rng = np.random.default_rng(21)
+    Hq, Hkv, N, rot, theta, eps = 8, 2, 150, 64, 1e7, 1e-6
+    W = Hq * 2 * D + 2 * Hkv * D
+    proj = orc.bf16_round(rng.standard_normal((N, W)).astype(np.float32))
+    qn = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kn = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    pos = (np.arange(N) + 500).astype(np.int32)
+    stride = o.kv_stride(N)
+    dev = "cuda"
+    qs = orc.LOG2E / 16.0
+    q_out = torch.empty(N, Hq, D, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(Hkv, stride, D, dtype=torch.bfloat16, device=dev)
+    vtc = torch.zeros(Hkv, D, stride, dtype=torch.bfloat16, device=dev)
+    o.attn_prep(bf(proj).to(dev), torch.as_tensor(qn).to(dev), torch.as_tensor(kn).to(dev),
+                torch.as_tensor(pos).to(dev), Hq, Hkv, rot, theta, eps, qs, q_out, kc, vtc, stride)
+    torch.cuda.synchronize()
+    rq, rg, rk, rv = orc.attn_prep(proj, qn, kn, pos, Hq, Hkv, rot, theta, eps)
+    assert rel_err(np32(q_out), rq * qs) <= 1e-2
+    assert rel_err(np32(kc)[:, :N].transpose(1, 0, 2), rk) <= 1e-2
+    # V is copied bit-exactly, transposed
+    np.testing.assert_array_equal(np32(vtc)[:, :, :N].transpose(2, 0, 1), rv.astype(np.float32))
+
+
+@pytest.mark.parametrize("rows", [64])
+def test_attention_capacity_shape(rows):
+    """Config 3 shape (Hq 16 / Hkv 4, state 8192, 256 branches x 16) against a
+    torch fp32 reference on the device, plus the CPU oracle on a row sample."""
+    o = ops()
+    Hq, Hkv, P = 16, 4, 8192
+    segs = [16] * 256
+    N = sum(segs)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    dev = "cuda"
+    ps, os_ = o.kv_stride(P), o.kv_stride(N)
+    pk = torch.zeros(Hkv, ps, D, dtype=torch.bfloat16, device=dev)
+    pvt = torch.zeros(Hkv, D, ps, dtype=torch.bfloat16, device=dev)
+    ok = torch.zeros(Hkv, os_, D, dtype=torch.bfloat16, device=dev)
+    ovt = torch.zeros(Hkv, D, os_, dtype=torch.bfloat16, device=dev)
+    ks = torch.randn(Hkv, P, D, generator=g).to(torch.bfloat16)
+    vs = torch.randn(Hkv, P, D, generator=g).to(torch.bfloat16)
+    ko = torch.randn(Hkv, N, D, generator=g).to(torch.bfloat16)
+    vo = torch.randn(Hkv, N, D, generator=g).to(torch.bfloat16)
+    qd = (torch.randn(N, Hq, D, generator=g) * (orc.LOG2E / 16.0)).to(torch.bfloat16)
+    gate = torch.randn(N, Hq, D, generator=g).to(torch.bfloat16)
+    pk[:, :P] = ks.to(dev)
+    pvt[:, :, :P] = vs.transpose(1, 2).to(dev)
+    ok[:, :N] = ko.to(dev)
+    ovt[:, :, :N] = vo.transpose(1, 2).to(dev)
+    ob = torch.as_tensor(np.repeat(np.arange(0, N, 16), 16).astype(np.int32)).to(dev)
+    out = torch.empty(N, Hq * D, dtype=torch.bfloat16, device=dev)
+    gd = gate.to(dev)
+    o.attention(qd.to(dev), gd, Hq * D, D, pk, pvt, P, ps, ok, ovt, os_, ob, Hq, Hkv, out)
+    torch.cuda.synchronize()
+    got = out.float().view(N, Hq, D)
+    # torch fp32 reference on the device, per kv-head, chunked over tokens
+    ref = torch.empty(N, Hq, D, device=dev)
+    kst, vst = ks.float().to(dev), vs.float().to(dev)
+    kof, vof = ko.float().to(dev), vo.float().to(dev)
+    qf = qd.float().to(dev) * math.log(2.0)
+    own_mask = torch.full((16, 16), float("-inf"), device=dev).triu(1)
+    for kh in range(Hkv):
+        for b in range(256):
+            sl = slice(16 * b, 16 * b + 16)
+            kk = torch.cat([kst[kh], kof[kh, sl]], 0)
+            vv = torch.cat([vst[kh], vof[kh, sl]], 0)
+            qq = qf[sl, 4 * kh: 4 * kh + 4]  # [16, 4, D]
+            s = torch.einsum("thd,kd->htk", qq, kk)
+            s[:, :, P:] += own_mask
+            p = torch.softmax(s, -1)
+            ref[sl, 4 * kh: 4 * kh + 4] = torch.einsum("htk,kd->thd", p, vv)
+    ref = ref * torch.sigmoid(gd.float())
+    err = float((got - ref).abs().max() / ref.abs().max())
+    print(f"capacity rel err vs torch fp32: {err:.3e}")
+    assert err <= TOL
+    # oracle on a sample of rows
+    rng = np.random.default_rng(0)
+    rows_idx = np.sort(rng.choice(N, rows, replace=False))
+    ksn, vsn = np32(ks).transpose(1, 0, 2), np32(vs).transpose(1, 0, 2)
+    kon, von = np32(ko).transpose(1, 0, 2), np32(vo).transpose(1, 0, 2)
+    qn, gn, obn = np32(qd), np32(gate), ob.cpu().numpy()
+    worst = 0.0
+    for n in rows_idx:
+        b = int(obn[n])
+        # the branch's tokens b..n, own keys b..n; keep the last row
+        r = orc.shared_prefix_attention(qn[b:n + 1].astype(np.float64), gn[b:n + 1], ksn, vsn,
+                                        kon[b:n + 1], von[b:n + 1],
+                                        np.zeros(n + 1 - b, np.int32),
+                                        scale=math.log(2.0), bf16_p=True)[-1:]
+        worst = max(worst, rel_err(got[n:n + 1].cpu().numpy(), r))
+    print(f"capacity rel err vs oracle sample: {worst:.3e}")
+    assert worst <= TOL
