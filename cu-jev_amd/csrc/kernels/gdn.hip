@@ -1,0 +1,522 @@
+/* Gated DeltaNet for gfx950: fused conv/gates, chunked WY/UT delta rule on
+ * bf16 MFMA with an fp32 recurrent state, gated RMSNorm fused into the scan.
+ *
+ * Semantics: REF src/kernels/gdn.cu:4-24 (conv), :26-43 (conv tail), :57-96
+ * (prep), :111-182 (scan, recurrent form), :193-216 (gated norm); math of
+ * transformers' torch_chunk_gated_delta_rule (modeling_qwen3_5.py:249-327).
+ *
+ * Pipeline per layer (all tokens of all segments in one launch each):
+ *   gdn_conv_prep  conv(4) + SiLU, l2norm(q,k) with q * 128^-1/2, g, beta
+ *                  -> bf16 q,k [N][Hk][128], v [N][Hv][128]; fp32 g, beta.
+ *   gdn_chunk_a    per (64-token chunk, v-head), fully parallel:
+ *                  G = cumsum g, A = tril(beta_i k_i.k_j e^{G_i-G_j}, -1),
+ *                  T = (I+A)^-1 by blocked forward substitution (fp32),
+ *                  W = T diag(beta e^G) K, U = T diag(beta) V (bf16 MFMA),
+ *                  QKm = tril(q_i.k_j e^{G_i-G_j})           -> bf16 in HBM.
+ *   gdn_chunk_b    per (segment, v-head), sequential over the segment's
+ *                  chunks; wave w owns 32 columns of S (fp32, registers):
+ *                  V' = U - W S;  O = (Q e^G) S + QKm V';
+ *                  S = e^{G_last} S + (K e^{G_last-G})^T V'  (bf16 MFMA),
+ *                  then y = w * bf16(rmsnorm(O)) * silu(z) straight to bf16.
+ * Every segment starts from S_in (the state's S, read-only) or 0 and the
+ * conv taps before a segment come from the state's conv tail (or 0): branches
+ * never copy the state.
+ *
+ * MFMA operand layouts (v_mfma_f32_32x32x16_bf16): A lane l = row l%32,
+ * k 8(l/32)..+8; B lane l = col l%32, same k; C lane l = col l%32, rows
+ * 8(r/4) + 4(l/32) + r%4. An accumulator used again as a B operand supplies
+ * its k values in that row order, so the matching A operand is read as two
+ * 4-element pieces at k offsets 4h and 8+4h of each 16-wide step. */
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int DK = 128; /* key head dim   */
+constexpr int DV = 128; /* value head dim */
+constexpr int CH = 64;  /* chunk length   */
+
+/* ---------------------------------------------------------------------- */
+/* conv + gates                                                            */
+/* ---------------------------------------------------------------------- */
+/* grid (N, ceil((2Hk+Hv)/4)), 256 threads: wave = one 128-channel head slice
+ * of one token; lane holds 2 channels. */
+__global__ __launch_bounds__(256) void gdn_conv_prep_kernel(
+    const bf16 *__restrict__ proj, int ps, const float *__restrict__ conv_w,
+    const float *__restrict__ conv_in, const int32_t *__restrict__ own_base,
+    const float *__restrict__ A_neg_exp, const float *__restrict__ dt_bias, int Hk, int Hv,
+    bf16 *__restrict__ qo, bf16 *__restrict__ ko, bf16 *__restrict__ vo, float *__restrict__ go,
+    float *__restrict__ bo) {
+    const int n = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nheads = 2 * Hk + Hv;
+    const int head = blockIdx.y * 4 + wave;
+    const int C = nheads * DK;
+    const int local = n - own_base[n];
+    if (head < nheads) {
+        const int c0 = head * DK + 2 * lane;
+        const float4 wa = *(const float4 *)(conv_w + (size_t)c0 * 4);
+        const float4 wb = *(const float4 *)(conv_w + (size_t)(c0 + 1) * 4);
+        const float w0[4] = {wa.x, wa.y, wa.z, wa.w}, w1[4] = {wb.x, wb.y, wb.z, wb.w};
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int tau = local - 3 + j; /* local index of the tap */
+            float x0, x1;
+            if (tau >= 0) {
+                const bf16 *src = proj + (size_t)(n - 3 + j) * ps + c0;
+                x0 = bf2f(src[0]);
+                x1 = bf2f(src[1]);
+            } else if (conv_in) {
+                x0 = conv_in[(size_t)c0 * 3 + tau + 3];
+                x1 = conv_in[(size_t)(c0 + 1) * 3 + tau + 3];
+            } else {
+                x0 = x1 = 0.f;
+            }
+            a0 += w0[j] * x0;
+            a1 += w1[j] * x1;
+        }
+        float y0 = silu_f(a0), y1 = silu_f(a1);
+        bf16 *dst;
+        if (head < 2 * Hk) {
+            const float ss = wave_sum(y0 * y0 + y1 * y1);
+            float inv = rsqrtf(ss + 1e-6f);
+            if (head < Hk) {
+                inv *= 0.08838834764831845f; /* 128^-1/2 */
+                dst = qo + ((size_t)n * Hk + head) * DK;
+            } else {
+                dst = ko + ((size_t)n * Hk + head - Hk) * DK;
+            }
+            y0 *= inv;
+            y1 *= inv;
+        } else {
+            dst = vo + ((size_t)n * Hv + head - 2 * Hk) * DV;
+        }
+        dst[2 * lane] = f2bf(y0);
+        dst[2 * lane + 1] = f2bf(y1);
+    }
+    if (blockIdx.y == 0) {
+        const bf16 *ab = proj + (size_t)n * ps + C + Hv * DV; /* b then a */
+        for (int t = threadIdx.x; t < Hv; t += blockDim.x) {
+            const float b = bf2f(ab[t]), a = bf2f(ab[Hv + t]);
+            bo[(size_t)n * Hv + t] = sigmoid_f(b);
+            go[(size_t)n * Hv + t] = A_neg_exp[t] * softplus_f(a + dt_bias[t]);
+        }
+    }
+}
+
+/* Last three pre-conv inputs of segment 0 -> conv_out[C][3] (prefill). */
+__global__ void gdn_conv_tail_kernel(const bf16 *__restrict__ proj, int ps,
+                                     const float *__restrict__ conv_in, float *__restrict__ conv_out,
+                                     int seg_len, int C) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= C)
+        return;
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const int t = seg_len - 3 + j;
+        float x;
+        if (t >= 0)
+            x = bf2f(proj[(size_t)t * ps + c]);
+        else
+            x = conv_in ? conv_in[(size_t)c * 3 + t + 3] : 0.f;
+        conv_out[(size_t)c * 3 + j] = x;
+    }
+}
+
+/* ---------------------------------------------------------------------- */
+/* phase A: intra-chunk WY/UT factors                                       */
+/* ---------------------------------------------------------------------- */
+struct __attribute__((aligned(16))) ChunkA_Smem {
+    bf16 K[CH][DK + 8];    /* k rows                       */
+    bf16 Q[CH][DK + 8];    /* q rows                       */
+    bf16 Kt[DK][CH + 8];   /* (beta e^G k)^T               */
+    bf16 Vt[DV][CH + 8];   /* (beta v)^T                   */
+    float A[CH][CH + 1];   /* strictly lower A             */
+    float T[CH][CH + 1];   /* (I + A)^-1                   */
+    float M[3][16][17];    /* block products               */
+    float G[CH], B[CH];
+};
+
+DEV bf16x8 ld8(const bf16 *p) { return *(const bf16x8 *)p; }
+
+__global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
+    const bf16 *__restrict__ qh, const bf16 *__restrict__ kh_, const bf16 *__restrict__ vh,
+    const float *__restrict__ g, const float *__restrict__ beta,
+    const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len, int Hk, int Hv,
+    bf16 *__restrict__ Wo, bf16 *__restrict__ Uo, bf16 *__restrict__ QKo, float *__restrict__ Go) {
+    __shared__ ChunkA_Smem sm;
+    const int ch = blockIdx.x, hv = blockIdx.y;
+    const int hk = hv / (Hv / Hk);
+    const int t0 = chunk_tok0[ch], L = chunk_len[ch];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, col = lane & 31;
+
+    /* gates and cumulative log-decay */
+    if (wave == 0) {
+        float gv = lane < L ? g[(size_t)(t0 + lane) * Hv + hv] : 0.f;
+        const float bv = lane < L ? beta[(size_t)(t0 + lane) * Hv + hv] : 0.f;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float up = __shfl_up(gv, o, 64);
+            if (lane >= o)
+                gv += up;
+        }
+        sm.G[lane] = gv;
+        sm.B[lane] = bv;
+    }
+    /* q, k rows (zero past L) */
+    for (int i = tid; i < CH * (DK / 8); i += 256) {
+        const int t = i / (DK / 8), c8 = (i % (DK / 8)) * 8;
+        bf16x8 kv = {}, qv = {};
+        if (t < L) {
+            kv = ld8(kh_ + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
+            qv = ld8(qh + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
+        }
+        *(bf16x8 *)&sm.K[t][c8] = kv;
+        *(bf16x8 *)&sm.Q[t][c8] = qv;
+    }
+    __syncthreads();
+    /* scaled, transposed k and v */
+    for (int i = tid; i < CH * (DK / 8); i += 256) {
+        const int t = i / (DK / 8), c8 = (i % (DK / 8)) * 8;
+        const float sk = sm.B[t] * fast_exp(sm.G[t]), sv = sm.B[t];
+        bf16x8 kv = *(const bf16x8 *)&sm.K[t][c8];
+        bf16x8 vv = {};
+        if (t < L)
+            vv = ld8(vh + ((size_t)(t0 + t) * Hv + hv) * DV + c8);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            sm.Kt[c8 + e][t] = f2bf(bf2f(kv[e]) * sk);
+            sm.Vt[c8 + e][t] = f2bf(bf2f(vv[e]) * sv);
+        }
+    }
+
+    /* K K^T and Q K^T: wave w owns the 32x32 tile (w>>1, w&1) of both */
+    {
+        const int ti = wave >> 1, tj = wave & 1;
+        floatx16 kk = {}, qk = {};
+#pragma unroll
+        for (int ks = 0; ks < DK / 16; ks++) {
+            const int c = 16 * ks + 8 * h;
+            bf16x8 ak = *(const bf16x8 *)&sm.K[32 * ti + col][c];
+            bf16x8 aq = *(const bf16x8 *)&sm.Q[32 * ti + col][c];
+            bf16x8 bk = *(const bf16x8 *)&sm.K[32 * tj + col][c];
+            kk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, bk, kk, 0, 0, 0);
+            qk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, bk, qk, 0, 0, 0);
+        }
+        const int j = 32 * tj + col;
+        const float Gj = sm.G[j];
+        bf16 *qko = QKo + ((size_t)ch * Hv + hv) * CH * CH;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int i = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
+            const float dec = i >= j ? fast_exp(sm.G[i] - Gj) : 0.f;
+            sm.A[i][j] = i > j ? sm.B[i] * kk[r] * dec : 0.f;
+            qko[i * CH + j] = f2bf(i >= j ? qk[r] * dec : 0.f);
+        }
+    }
+    __syncthreads();
+
+    /* T = (I + A)^-1: 16x16 diagonal blocks by forward substitution (wave w
+     * inverts block w, lane c < 16 owns column c) ... */
+    if (lane < 16) {
+        const int b0 = 16 * wave, c = lane;
+        float t[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < i; k++)
+                acc += sm.A[b0 + i][b0 + k] * t[k];
+            t[i] = (i == c ? 1.f : 0.f) - acc;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            sm.T[b0 + i][b0 + c] = t[i];
+    }
+    /* ... then the strictly lower blocks by distance from the diagonal:
+     * T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj */
+    for (int lvl = 1; lvl < 4; lvl++) {
+        __syncthreads();
+        const int nb = 4 - lvl;
+        for (int e = tid; e < nb * 256; e += 256) {
+            const int b = e >> 8, r = (e >> 4) & 15, c = e & 15;
+            const int bj = b, bi = b + lvl;
+            float acc = 0.f;
+            for (int bk = bj; bk < bi; bk++)
+#pragma unroll
+                for (int x = 0; x < 16; x++)
+                    acc += sm.A[16 * bi + r][16 * bk + x] * sm.T[16 * bk + x][16 * bj + c];
+            sm.M[b][r][c] = acc;
+        }
+        __syncthreads();
+        for (int e = tid; e < nb * 256; e += 256) {
+            const int b = e >> 8, r = (e >> 4) & 15, c = e & 15;
+            const int bj = b, bi = b + lvl;
+            float acc = 0.f;
+#pragma unroll
+            for (int x = 0; x < 16; x++)
+                acc += sm.T[16 * bi + r][16 * bi + x] * sm.M[b][x][c];
+            sm.T[16 * bi + r][16 * bj + c] = -acc;
+        }
+    }
+    /* zero the strictly upper part */
+    for (int e = tid; e < CH * CH; e += 256) {
+        const int i = e >> 6, j = e & 63;
+        if ((j >> 4) > (i >> 4))
+            sm.T[i][j] = 0.f;
+    }
+    __syncthreads();
+
+    /* W = T (beta e^G K), U = T (beta V): wave w owns rows 32(w>>1).., and
+     * columns 64(w&1)..+64 of both */
+    {
+        const int mi = wave >> 1, nh = wave & 1;
+        floatx16 w[2] = {}, u[2] = {};
+#pragma unroll
+        for (int ks = 0; ks < CH / 16; ks++) {
+            const int k0 = 16 * ks + 8 * h;
+            bf16x8 a;
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                a[e] = f2bf(sm.T[32 * mi + col][k0 + e]);
+#pragma unroll
+            for (int nj = 0; nj < 2; nj++) {
+                const int c = 64 * nh + 32 * nj + col;
+                bf16x8 bk = *(const bf16x8 *)&sm.Kt[c][k0];
+                bf16x8 bv = *(const bf16x8 *)&sm.Vt[c][k0];
+                w[nj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bk, w[nj], 0, 0, 0);
+                u[nj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bv, u[nj], 0, 0, 0);
+            }
+        }
+        bf16 *wo = Wo + ((size_t)ch * Hv + hv) * CH * DK;
+        bf16 *uo = Uo + ((size_t)ch * Hv + hv) * CH * DV;
+#pragma unroll
+        for (int nj = 0; nj < 2; nj++) {
+            const int c = 64 * nh + 32 * nj + col;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int i = 32 * mi + 8 * (r >> 2) + 4 * h + (r & 3);
+                wo[i * DK + c] = f2bf(w[nj][r]);
+                uo[i * DV + c] = f2bf(u[nj][r]);
+            }
+        }
+    }
+    if (tid < CH)
+        Go[((size_t)ch * Hv + hv) * CH + tid] = sm.G[tid];
+}
+
+/* ---------------------------------------------------------------------- */
+/* phase B: state recurrence over chunks + gated RMSNorm                    */
+/* ---------------------------------------------------------------------- */
+struct __attribute__((aligned(16))) ChunkB_Smem {
+    bf16 W[CH][DK + 8];
+    bf16 Qg[CH][DK + 8];  /* q e^G               */
+    bf16 QK[CH][CH + 8];
+    bf16 KgT[DK][CH + 8]; /* (k e^{G_last-G})^T  */
+    float O[CH][DV + 4];
+    float G[CH];
+};
+
+/* A operand of a product whose B operand is an accumulator reused as B:
+ * k values 4h..4h+3 and 8+4h..8+4h+3 of the 16-wide step at `p`. */
+DEV bf16x8 ld_perm(const bf16 *p, int h) {
+    bf16x4 lo = *(const bf16x4 *)(p + 4 * h), hi = *(const bf16x4 *)(p + 8 + 4 * h);
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+/* accumulator registers 8s..8s+7 as a bf16 B operand */
+DEV bf16x8 acc_as_b(const floatx16 &c, int s) {
+    bf16x8 b;
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        b[e] = f2bf(c[8 * s + e]);
+    return b;
+}
+
+__global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
+    const bf16 *__restrict__ qh, const bf16 *__restrict__ kh_, const bf16 *__restrict__ Wi,
+    const bf16 *__restrict__ Ui, const bf16 *__restrict__ QKi, const float *__restrict__ Gi,
+    const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
+    const int32_t *__restrict__ seg_chunk0, const int32_t *__restrict__ seg_nchunk,
+    const float *__restrict__ S_in, float *__restrict__ S_out, const bf16 *__restrict__ z, int zs,
+    const float *__restrict__ norm_w, float eps, int Hk, int Hv, bf16 *__restrict__ y) {
+    __shared__ ChunkB_Smem sm;
+    const int seg = blockIdx.x, hv = blockIdx.y;
+    const int hk = hv / (Hv / Hk);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, col = lane & 31;
+    const int dv = 32 * wave + col; /* this lane's state column */
+
+    floatx16 S[4]; /* S[:, dv] rows 32ti + 8(r/4) + 4h + r%4 */
+#pragma unroll
+    for (int ti = 0; ti < 4; ti++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int dk = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
+            S[ti][r] = S_in ? S_in[((size_t)hv * DK + dk) * DV + dv] : 0.f;
+        }
+    }
+
+    const int c0 = seg_chunk0[seg], nc = seg_nchunk[seg];
+    for (int ci = 0; ci < nc; ci++) {
+        const int ch = c0 + ci;
+        const int t0 = chunk_tok0[ch], L = chunk_len[ch];
+        const size_t cbase = (size_t)ch * Hv + hv;
+        __syncthreads();
+        if (tid < CH)
+            sm.G[tid] = Gi[cbase * CH + tid];
+        __syncthreads();
+        const float Glast = sm.G[CH - 1];
+        for (int i = tid; i < CH * (DK / 8); i += 256) {
+            const int t = i / (DK / 8), c8 = (i % (DK / 8)) * 8;
+            *(bf16x8 *)&sm.W[t][c8] = ld8(Wi + cbase * CH * DK + t * DK + c8);
+            bf16x8 qv = {}, kv = {};
+            if (t < L) {
+                qv = ld8(qh + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
+                kv = ld8(kh_ + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
+            }
+            const float eq = fast_exp(sm.G[t]), ek = fast_exp(Glast - sm.G[t]);
+            bf16x8 qg;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                qg[e] = f2bf(bf2f(qv[e]) * eq);
+                sm.KgT[c8 + e][t] = f2bf(bf2f(kv[e]) * ek);
+            }
+            *(bf16x8 *)&sm.Qg[t][c8] = qg;
+        }
+        for (int i = tid; i < CH * (CH / 8); i += 256) {
+            const int t = i / (CH / 8), c8 = (i % (CH / 8)) * 8;
+            *(bf16x8 *)&sm.QK[t][c8] = ld8(QKi + cbase * CH * CH + t * CH + c8);
+        }
+        __syncthreads();
+
+        /* S as B operand (8 k-steps over dk) */
+        bf16x8 Sb[8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+            Sb[ks] = acc_as_b(S[ks >> 1], ks & 1);
+
+        /* V' = U - W S  (tokens x dv) */
+        floatx16 Vn[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            floatx16 acc = {};
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    ld_perm(&sm.W[32 * mt + col][16 * ks], h), Sb[ks], acc, 0, 0, 0);
+            const bf16 *up = Ui + cbase * CH * DV;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int t = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+                Vn[mt][r] = bf2f(up[t * DV + dv]) - acc[r];
+            }
+        }
+        bf16x8 Vb[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+            Vb[ks] = acc_as_b(Vn[ks >> 1], ks & 1);
+
+        /* O = (Q e^G) S + QKm V' */
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            floatx16 acc = {};
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    ld_perm(&sm.Qg[32 * mt + col][16 * ks], h), Sb[ks], acc, 0, 0, 0);
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    ld_perm(&sm.QK[32 * mt + col][16 * ks], h), Vb[ks], acc, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int t = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+                sm.O[t][dv] = acc[r];
+            }
+        }
+
+        /* S = e^{G_last} S + (K e^{G_last - G})^T V' */
+        const float dec = fast_exp(Glast);
+#pragma unroll
+        for (int ti = 0; ti < 4; ti++) {
+            floatx16 acc = S[ti] * dec;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    ld_perm(&sm.KgT[32 * ti + col][16 * ks], h), Vb[ks], acc, 0, 0, 0);
+            S[ti] = acc;
+        }
+        __syncthreads();
+
+        /* gated RMSNorm of the chunk's outputs: wave per token row */
+        for (int t = wave; t < L; t += 4) {
+            const float o0 = sm.O[t][2 * lane], o1 = sm.O[t][2 * lane + 1];
+            const float ss = wave_sum(o0 * o0 + o1 * o1);
+            const float inv = rsqrtf(ss * (1.f / DV) + eps);
+            const bf16 *zr = z + (size_t)(t0 + t) * zs + hv * DV + 2 * lane;
+            bf16 *yr = y + ((size_t)(t0 + t) * Hv + hv) * DV + 2 * lane;
+            const float n0 = bf2f(f2bf(o0 * inv)) * norm_w[2 * lane];
+            const float n1 = bf2f(f2bf(o1 * inv)) * norm_w[2 * lane + 1];
+            yr[0] = f2bf(n0 * silu_f(bf2f(zr[0])));
+            yr[1] = f2bf(n1 * silu_f(bf2f(zr[1])));
+        }
+    }
+    if (S_out && seg == 0) {
+#pragma unroll
+        for (int ti = 0; ti < 4; ti++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int dk = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
+                S_out[((size_t)hv * DK + dk) * DV + dv] = S[ti][r];
+            }
+        }
+    }
+}
+
+} // namespace
+
+extern "C" hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const float *conv_w,
+                                      const float *conv_in, float *conv_out, int seg0_len,
+                                      const int32_t *own_base, const float *A_neg_exp,
+                                      const float *dt_bias, int N, int Hk, int Hv, bf16_t *q,
+                                      bf16_t *k, bf16_t *v, float *g, float *beta,
+                                      hipStream_t stream) {
+    if (N <= 0)
+        return hipSuccess;
+    if (Hk <= 0 || Hv % Hk != 0)
+        return hipErrorInvalidValue;
+    const int nheads = 2 * Hk + Hv;
+    hipLaunchKernelGGL(gdn_conv_prep_kernel, dim3((unsigned)N, (unsigned)CEIL_DIV(nheads, 4)),
+                       dim3(256), 0, stream, (const bf16 *)proj, proj_stride, conv_w, conv_in,
+                       own_base, A_neg_exp, dt_bias, Hk, Hv, (bf16 *)q, (bf16 *)k, (bf16 *)v, g,
+                       beta);
+    if (conv_out) {
+        const int C = nheads * DK;
+        hipLaunchKernelGGL(gdn_conv_tail_kernel, dim3((unsigned)CEIL_DIV(C, 256)), dim3(256), 0,
+                           stream, (const bf16 *)proj, proj_stride, conv_in, conv_out, seg0_len, C);
+    }
+    return hipGetLastError();
+}
+
+extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const float *g,
+                                 const float *beta, const cujev_chunks *ck, const float *S_in,
+                                 float *S_out, const bf16_t *z, int z_stride, const float *norm_w,
+                                 float eps, int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *ws,
+                                 hipStream_t stream) {
+    if (ck->num_chunks <= 0)
+        return hipSuccess;
+    if (Hk <= 0 || Hv % Hk != 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gdn_chunk_a_kernel, dim3((unsigned)ck->num_chunks, (unsigned)Hv), dim3(256),
+                       0, stream, (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, g, beta,
+                       ck->chunk_tok0, ck->chunk_len, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->U,
+                       (bf16 *)ws->QK, ws->G);
+    hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)ck->num_segments, (unsigned)Hv),
+                       dim3(256), 0, stream, (const bf16 *)q, (const bf16 *)k,
+                       (const bf16 *)ws->W, (const bf16 *)ws->U, (const bf16 *)ws->QK, ws->G,
+                       ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk, S_in, S_out,
+                       (const bf16 *)z, z_stride, norm_w, eps, Hk, Hv, (bf16 *)y);
+    return hipGetLastError();
+}

@@ -50,6 +50,71 @@ hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_tok_stride,
                        const int32_t *own_base, int N, int Hq, int Hkv, bf16_t *out,
                        hipStream_t stream);
 
+/* ---- Gated DeltaNet -------------------------------------------------------
+ * proj[N, proj_stride] bf16 is the fused row [q Hk*128 | k Hk*128 | v Hv*128 |
+ * z Hv*128 | b Hv | a Hv]. Conv (width 4, no bias) + SiLU over the first
+ * C = (2Hk+Hv)*128 columns; taps before a segment start (local index from
+ * own_base) come from conv_in[C][3] (NULL = zeros). Then q,k l2-normalised
+ * (q also * 128^-1/2) -> bf16 q,k [N][Hk][128], v bf16 [N][Hv][128],
+ * g = A_neg_exp * softplus(a + dt_bias), beta = sigmoid(b) -> fp32 [N][Hv].
+ * If conv_out != NULL the last three pre-conv inputs of the first segment
+ * (tokens [0, seg0_len)) are written there as [C][3]. */
+hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const float *conv_w,
+                           const float *conv_in, float *conv_out, int seg0_len,
+                           const int32_t *own_base, const float *A_neg_exp, const float *dt_bias,
+                           int N, int Hk, int Hv, bf16_t *q, bf16_t *k, bf16_t *v, float *g,
+                           float *beta, hipStream_t stream);
+
+/* 64-token chunks of the packed segments; chunks never cross a segment. */
+typedef struct cujev_chunks {
+    const int32_t *chunk_tok0; /* [num_chunks] first packed token */
+    const int32_t *chunk_len;  /* [num_chunks] 1..64              */
+    const int32_t *seg_chunk0; /* [num_segments] first chunk      */
+    const int32_t *seg_nchunk; /* [num_segments] chunk count      */
+    int num_chunks;
+    int num_segments;
+} cujev_chunks;
+
+/* Per-chunk WY/UT factors, written by the scan's first phase. */
+typedef struct cujev_gdn_scratch {
+    void *W;  /* bf16 [num_chunks][Hv][64][128] */
+    void *U;  /* bf16 [num_chunks][Hv][64][128] */
+    void *QK; /* bf16 [num_chunks][Hv][64][64]  */
+    float *G; /* [num_chunks][Hv][64]           */
+} cujev_gdn_scratch;
+
+static inline size_t cujev_align256(size_t x) { return (x + 255) / 256 * 256; }
+static inline size_t cujev_gdn_scratch_bytes(int num_chunks, int Hv) {
+    const size_t per = (size_t)num_chunks * Hv * 64;
+    return 2 * cujev_align256(per * 128 * 2) + cujev_align256(per * 64 * 2) +
+           cujev_align256(per * 4);
+}
+/* Carve the scratch of cujev_gdn_scratch_bytes() starting at `base`. */
+static inline cujev_gdn_scratch cujev_gdn_scratch_carve(void *base, int num_chunks, int Hv) {
+    const size_t per = (size_t)num_chunks * Hv * 64;
+    char *p = (char *)base;
+    cujev_gdn_scratch s;
+    s.W = p;
+    p += cujev_align256(per * 128 * 2);
+    s.U = p;
+    p += cujev_align256(per * 128 * 2);
+    s.QK = p;
+    p += cujev_align256(per * 64 * 2);
+    s.G = (float *)p;
+    return s;
+}
+
+/* Chunked gated delta rule over every segment, each from S_in[Hv][128][128]
+ * (fp32, read-only; NULL = zeros); S_out (may be NULL) receives the final
+ * state of segment 0. The output goes straight through the gated RMSNorm:
+ * y[n, hv*128 + c] = bf16( bf16(o * rsqrt(mean o^2 + eps)) * norm_w[c]
+ *                          * silu(z[n*z_stride + hv*128 + c]) ). */
+hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const float *g,
+                      const float *beta, const cujev_chunks *chunks, const float *S_in,
+                      float *S_out, const bf16_t *z, int z_stride, const float *norm_w, float eps,
+                      int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *scratch,
+                      hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,3 +58,37 @@ EXPORT int cujev_op_attention(const void *q, const void *gate, int gate_tok_stri
                                 own_base, N, Hq, Hkv, (bf16_t *)out, (hipStream_t)stream),
                     "attention");
 }
+
+EXPORT int cujev_op_gdn_conv_prep(const void *proj, int proj_stride, const float *conv_w,
+                                  const float *conv_in, float *conv_out, int seg0_len,
+                                  const int32_t *own_base, const float *A_neg_exp,
+                                  const float *dt_bias, int N, int Hk, int Hv, void *q, void *k,
+                                  void *v, float *g, float *beta, void *stream) {
+    if (N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk || (conv_out && (seg0_len < 0 || seg0_len > N)))
+        return fail(1, "gdn_conv_prep: bad arguments");
+    return launched(k_gdn_conv_prep((const bf16_t *)proj, proj_stride, conv_w, conv_in, conv_out,
+                                    seg0_len, own_base, A_neg_exp, dt_bias, N, Hk, Hv,
+                                    (bf16_t *)q, (bf16_t *)k, (bf16_t *)v, g, beta,
+                                    (hipStream_t)stream),
+                    "gdn_conv_prep");
+}
+
+EXPORT size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv) {
+    return cujev_gdn_scratch_bytes(num_chunks, Hv);
+}
+
+EXPORT int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const float *g,
+                             const float *beta, const int32_t *chunk_tok0,
+                             const int32_t *chunk_len, int num_chunks, const int32_t *seg_chunk0,
+                             const int32_t *seg_nchunk, int num_segments, const float *S_in,
+                             float *S_out, const void *z, int z_stride, const float *norm_w,
+                             float eps, int Hk, int Hv, void *y, void *scratch, void *stream) {
+    if (num_chunks < 0 || num_segments < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk || !scratch)
+        return fail(1, "gdn_scan: bad arguments");
+    cujev_chunks ck = {chunk_tok0, chunk_len, seg_chunk0, seg_nchunk, num_chunks, num_segments};
+    cujev_gdn_scratch ws = cujev_gdn_scratch_carve(scratch, num_chunks, Hv);
+    return launched(k_gdn_scan((const bf16_t *)q, (const bf16_t *)k, (const bf16_t *)v, g, beta,
+                               &ck, S_in, S_out, (const bf16_t *)z, z_stride, norm_w, eps, Hk, Hv,
+                               (bf16_t *)y, &ws, (hipStream_t)stream),
+                    "gdn_scan");
+}

@@ -30,6 +30,10 @@ _D = C.c_double
 _SIGS = {
     "cujev_op_attn_prep": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _D, _F, _F, _P, _P, _P, _I, _P],
     "cujev_op_attention": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P],
+    "cujev_op_gdn_conv_prep": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P,
+                               _P, _P],
+    "cujev_op_gdn_scan": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _F, _I,
+                          _I, _P, _P, _P],
 }
 
 
@@ -49,6 +53,8 @@ def load():
     lib.cujev_ops_kv_stride.argtypes = [_I]
     lib.cujev_ops_kv_stride.restype = _I
     lib.cujev_ops_last_error.restype = C.c_char_p
+    lib.cujev_ops_gdn_scratch_bytes.argtypes = [_I, _I]
+    lib.cujev_ops_gdn_scratch_bytes.restype = C.c_size_t
     for name, args in _SIGS.items():
         fn = getattr(lib, name)
         fn.argtypes = args
@@ -58,7 +64,7 @@ def load():
 
 
 def exported_symbols():
-    return ["cujev_ops_kv_stride", "cujev_ops_last_error", *_SIGS]
+    return ["cujev_ops_kv_stride", "cujev_ops_last_error", "cujev_ops_gdn_scratch_bytes", *_SIGS]
 
 
 def _ptr(t):
@@ -97,3 +103,41 @@ def attention(q, gate, gate_tok_stride, gate_head_stride, pk, pvt, P, p_stride, 
     _call("cujev_op_attention", _ptr(q), _ptr(gate), gate_tok_stride, gate_head_stride,
           _ptr(pk), _ptr(pvt), int(P), p_stride, _ptr(ok), _ptr(ovt), o_stride, _ptr(own_base),
           N, Hq, Hkv, _ptr(out), _stream())
+
+
+def gdn_conv_prep(proj, conv_w, conv_in, conv_out, seg0_len, own_base, A_neg_exp, dt_bias,
+                  Hk, Hv, q, k, v, g, beta):
+    N = proj.shape[0]
+    _call("cujev_op_gdn_conv_prep", _ptr(proj), proj.stride(0), _ptr(conv_w), _ptr(conv_in),
+          _ptr(conv_out), int(seg0_len), _ptr(own_base), _ptr(A_neg_exp), _ptr(dt_bias), N, Hk,
+          Hv, _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _stream())
+
+
+def chunk_table(seg_lens, chunk=64):
+    """Host-side chunk table: every segment cut into `chunk`-token pieces."""
+    import numpy as np
+    tok0, clen, seg0, segn = [], [], [], []
+    start = 0
+    for L in seg_lens:
+        seg0.append(len(tok0))
+        n = 0
+        for c in range(0, L, chunk):
+            tok0.append(start + c)
+            clen.append(min(chunk, L - c))
+            n += 1
+        segn.append(n)
+        start += L
+    as_i = lambda x: np.asarray(x, dtype=np.int32)
+    return as_i(tok0), as_i(clen), as_i(seg0), as_i(segn)
+
+
+def gdn_scratch_bytes(num_chunks, Hv):
+    return int(load().cujev_ops_gdn_scratch_bytes(int(num_chunks), int(Hv)))
+
+
+def gdn_scan(q, k, v, g, beta, chunk_tok0, chunk_len, seg_chunk0, seg_nchunk, S_in, S_out, z,
+             z_stride, norm_w, eps, Hk, Hv, y, scratch):
+    _call("cujev_op_gdn_scan", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(chunk_tok0),
+          _ptr(chunk_len), chunk_tok0.shape[0], _ptr(seg_chunk0), _ptr(seg_nchunk),
+          seg_chunk0.shape[0], _ptr(S_in), _ptr(S_out), _ptr(z), int(z_stride), _ptr(norm_w),
+          float(eps), Hk, Hv, _ptr(y), _ptr(scratch), _stream())

@@ -51,6 +51,36 @@ int cujev_op_attention(const void *q, const void *gate, int gate_tok_stride, int
                        const void *ovt, int o_stride, const int32_t *own_base, int N, int Hq,
                        int Hkv, void *out, void *stream);
 
+/* Replaces reference src/kernels/kernels.h:214-215 (k_gdn_conv) and :221-223
+ * (k_gdn_prep), fused. proj rows [q Hk*128 | k Hk*128 | v Hv*128 | z | b | a].
+ * Conv (width 4) + SiLU with taps before a segment taken from conv_in [C][3]
+ * (NULL = zeros); own_base[n] = first token of n's segment. Outputs bf16
+ * q, k [N][Hk][128] (l2-normalised, q * 128^-1/2), v [N][Hv][128], fp32
+ * g, beta [N][Hv]. conv_out (may be NULL) gets the last three pre-conv inputs
+ * of tokens [0, seg0_len) as [C][3]. conv_w fp32 [C][4]. */
+int cujev_op_gdn_conv_prep(const void *proj, int proj_stride, const float *conv_w,
+                           const float *conv_in, float *conv_out, int seg0_len,
+                           const int32_t *own_base, const float *A_neg_exp,
+                           const float *dt_bias, int N, int Hk, int Hv, void *q, void *k,
+                           void *v, float *g, float *beta, void *stream);
+
+/* Bytes of device scratch cujev_op_gdn_scan needs for num_chunks chunks. */
+size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv);
+
+/* Replaces reference src/kernels/kernels.h:228-230 (k_gdn_scan) and :233-234
+ * (k_gdn_norm_gate), fused. Chunk table (device int32): chunk_tok0/chunk_len
+ * [num_chunks], seg_chunk0/seg_nchunk [num_segments]; each segment is cut into
+ * chunks of 64 tokens from its start. S_in fp32 [Hv][128][128] (NULL = 0),
+ * S_out (may be NULL) = final state of segment 0. y bf16 [N][Hv*128] is the
+ * gated-RMSNorm output; z is read at z[n*z_stride + hv*128 + c].
+ * scratch: cujev_ops_gdn_scratch_bytes(num_chunks, Hv) bytes, 256-aligned. */
+int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const float *g,
+                      const float *beta, const int32_t *chunk_tok0, const int32_t *chunk_len,
+                      int num_chunks, const int32_t *seg_chunk0, const int32_t *seg_nchunk,
+                      int num_segments, const float *S_in, float *S_out, const void *z,
+                      int z_stride, const float *norm_w, float eps, int Hk, int Hv, void *y,
+                      void *scratch, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
