@@ -1,0 +1,311 @@
+#!/usr/bin/env python3
+"""Benchmark of the branch-forward hot path on one MI355X.
+
+Workload (BASELINE.json metric, config 4): a random-init Qwen3.5-4B-shaped
+hybrid model (32 layers, every 4th full gated attention, hidden 2560, vocab
+248320, bf16 weights ~ N(0, 0.02)); one request = a fresh 530-token
+random-id state prefill + 4 question branches of 20 tokens, read out over
+3/2/2/4 single-token labels. A step is one request. `value` is requests/s
+(one request = one decision, the Starfighter sense); branch-decisions/s
+(4 per request, the cujev-bench sense) and p50 ms/request are reported next
+to it.
+
+Also measured, each in its own timed loop with HIP events on the stream the
+kernel is launched on:
+  roofline       the shared-prefix attention kernel at config 3 (Hq 16/Hkv 4,
+                 state 8192, 256 branches x 16 tokens) against the bf16 dense
+                 MFMA peak;
+  gdn_roofline   the Gated DeltaNet layer at config 2 (T=2048 prefill) against
+                 the HBM peak, from its compulsory bytes.
+cpu_baseline: transformers' Qwen3_5ForCausalLM in fp32 on the host cores, on
+the same checkpoint file and the same first request (the HF-batched method
+of the reference's benchmarks/benefit.py:77-92); it is also the parity check
+of the request's decision probabilities.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "cu-jev_amd"))
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+STATE_TOKENS = 530
+BRANCH_TOKENS = 20
+LABELS = [3, 2, 2, 4]      # labels per question (Starfighter-style)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_request(rng, vocab):
+    state = [int(x) for x in rng.integers(1000, 60000, size=STATE_TOKENS)]
+    branches = []
+    for n in LABELS:
+        toks = [int(x) for x in rng.integers(1000, 60000, size=BRANCH_TOKENS)]
+        cands = [int(x) for x in rng.choice(np.arange(16, 1000), size=n, replace=False)]
+        branches.append((toks, cands))
+    return state, branches
+
+
+# --------------------------------------------------------------------------
+# end to end
+# --------------------------------------------------------------------------
+def run_e2e(ckpt, steps, warmup, seed=0):
+    from cujev import Branch, Engine
+    eng = Engine(ckpt, max_state_tokens=1024, max_branch_tokens=256, max_branches=16,
+                 max_candidates=256)
+    rng = np.random.default_rng(seed)
+    reqs = [make_request(rng, eng.vocab_size) for _ in range(warmup + steps)]
+    first_out = None
+    wall, gpu = [], []
+    import torch
+    torch.cuda.synchronize()
+    for i, (state, brs) in enumerate(reqs):
+        t0 = time.perf_counter()
+        eng.prefill(state)
+        pre_ms = eng.last_timing().prefill_ms
+        out = eng.eval([Branch(t, c) for t, c in brs])
+        t1 = time.perf_counter()
+        ev_ms = eng.last_timing().eval_ms
+        if i == 0:
+            first_out = out
+        if i >= warmup:
+            wall.append((t1 - t0) * 1e3)
+            gpu.append(pre_ms + ev_ms)
+    # eval only, state cached (benchmarks/benefit.py:62-66)
+    state, brs = reqs[-1]
+    eng.prefill(state)
+    ev_only = []
+    for _ in range(max(steps, 5)):
+        t0 = time.perf_counter()
+        eng.eval([Branch(t, c) for t, c in brs])
+        ev_only.append((time.perf_counter() - t0) * 1e3)
+    info = dict(name=eng.name, weight_gib=eng.weight_bytes / 2 ** 30)
+    eng.close()
+    return dict(wall_ms=wall, gpu_ms=gpu, eval_only_ms=ev_only, first_req=reqs[0],
+                first_out=first_out, info=info)
+
+
+# --------------------------------------------------------------------------
+# kernel rooflines (operator C ABI, HIP events on the launch stream)
+# --------------------------------------------------------------------------
+def attention_roofline(iters=20):
+    import torch
+    from cujev import ops
+    ops.load()
+    D, Hq, Hkv, P, B, L = 256, 16, 4, 8192, 256, 16
+    N = B * L
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(1)
+    ps, os_ = ops.kv_stride(P), ops.kv_stride(N)
+    pk = torch.randn(Hkv, ps, D, device=dev, generator=g).to(torch.bfloat16)
+    pvt = torch.randn(Hkv, D, ps, device=dev, generator=g).to(torch.bfloat16)
+    ok = torch.randn(Hkv, os_, D, device=dev, generator=g).to(torch.bfloat16)
+    ovt = torch.randn(Hkv, D, os_, device=dev, generator=g).to(torch.bfloat16)
+    q = (torch.randn(N, Hq, D, device=dev, generator=g) * (1.4426950408889634 / 16)).to(torch.bfloat16)
+    gate = torch.randn(N, Hq, D, device=dev, generator=g).to(torch.bfloat16)
+    own_base = torch.arange(N, device=dev, dtype=torch.int32) // L * L
+    out = torch.empty(N, Hq * D, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def launch():
+        ops.attention(q, gate, Hq * D, D, pk, pvt, P, ps, ok, ovt, os_, own_base, Hq, Hkv, out)
+
+    for _ in range(3):
+        launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(iters):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / iters * 1e3
+    flop = 4.0 * D * Hq * (N * P + B * L * (L + 1) / 2)  # QK^T + PV, exact causal count
+    tflops = flop / (us * 1e-6) / 1e12
+    return dict(us=us, flop=flop, tflops=tflops)
+
+
+def gdn_roofline(iters=20):
+    import torch
+    from cujev import ops
+    ops.load()
+    Hk, Hv, T = 16, 32, 2048
+    C = (2 * Hk + Hv) * 128
+    Wd = C + Hv * 128 + 2 * Hv
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(2)
+    proj = torch.randn(T, Wd, device=dev, generator=g).to(torch.bfloat16)
+    conv_w = torch.randn(C, 4, device=dev, generator=g) * 0.5
+    A_neg = -torch.rand(Hv, device=dev, generator=g) * 4
+    dt_bias = torch.zeros(Hv, device=dev)
+    norm_w = torch.ones(128, device=dev)
+    own_base = torch.zeros(T, dtype=torch.int32, device=dev)
+    q = torch.empty(T, Hk, 128, dtype=torch.bfloat16, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty(T, Hv, 128, dtype=torch.bfloat16, device=dev)
+    gg = torch.empty(T, Hv, device=dev)
+    beta = torch.empty_like(gg)
+    conv_out = torch.empty(C, 3, device=dev)
+    S_out = torch.empty(Hv, 128, 128, device=dev)
+    y = torch.empty(T, Hv * 128, dtype=torch.bfloat16, device=dev)
+    tok0, clen, seg0, segn = (torch.as_tensor(a).to(dev) for a in ops.chunk_table([T]))
+    scratch = torch.empty(ops.gdn_scratch_bytes(len(tok0), Hv), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def launch():
+        ops.gdn_conv_prep(proj, conv_w, None, conv_out, T, own_base, A_neg, dt_bias, Hk, Hv, q, k,
+                          v, gg, beta)
+        ops.gdn_scan(q, k, v, gg, beta, tok0, clen, seg0, segn, None, S_out, proj[:, C:],
+                     proj.stride(0), norm_w, 1e-6, Hk, Hv, y, scratch)
+
+    for _ in range(3):
+        launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(iters):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / iters * 1e3
+    # compulsory bytes: pre-conv qkv, a/b, conv w, bf16 out, S_out, conv tail, z
+    nbytes = T * C * 2 + T * 2 * Hv * 2 + C * 4 * 4 + T * Hv * 128 * 2 + Hv * 128 * 128 * 4 \
+        + C * 3 * 4 + T * Hv * 128 * 2
+    return dict(us=us, bytes=nbytes, gbs=nbytes / (us * 1e-6) / 1e9)
+
+
+# --------------------------------------------------------------------------
+# CPU baseline: transformers fp32 on the host cores (and the parity check)
+# --------------------------------------------------------------------------
+def cpu_baseline(ckpt, req, eng_out):
+    try:
+        import torch
+        from transformers import AutoModelForCausalLM
+    except Exception as e:  # pragma: no cover
+        return None, {"error": f"CPU baseline unavailable: {e}"}
+    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16")))
+    torch.set_num_threads(threads)
+    t0 = time.perf_counter()
+    model = AutoModelForCausalLM.from_pretrained(ckpt, dtype=torch.float32).eval()
+    log(f"transformers model loaded on CPU in {time.perf_counter() - t0:.1f}s ({threads} threads)")
+    state, brs = req
+    ids = torch.tensor([state + t for t, _ in brs])
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        lg = model(ids, logits_to_keep=1).logits[:, -1, :]
+        dt = time.perf_counter() - t0
+    probs_ref = [torch.softmax(lg[i, c].double(), 0).numpy() for i, (_, c) in enumerate(brs)]
+    probs_eng = [np.exp(o - o.max()) / np.exp(o - o.max()).sum() for o in eng_out]
+    dp = max(float(np.abs(a - b).max()) for a, b in zip(probs_eng, probs_ref))
+    agree = all(int(np.argmax(a)) == int(np.argmax(b)) for a, b in zip(probs_eng, probs_ref))
+    margins = [float(np.sort(lg[i, c].numpy())[-1] - np.sort(lg[i, c].numpy())[-2])
+               for i, (_, c) in enumerate(brs)]
+    del model
+    base = {"value": round(1.0 / dt, 5), "unit": "requests/s", "cores": threads,
+            "kind": "reference",
+            "sample": (f"1 request (4 branches x [{STATE_TOKENS}+{BRANCH_TOKENS}] tokens, one "
+                       f"batch, logits_to_keep=1) through transformers Qwen3_5ForCausalLM fp32 "
+                       f"on {threads} host threads: {dt:.1f} s"),
+            "ms_per_request": round(dt * 1e3, 1)}
+    parity = {"max_abs_dprob_vs_transformers_fp32": dp, "argmax_identical": agree,
+              "top2_logit_margins": [round(m, 4) for m in margins]}
+    return base, parity
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--ckpt", default=os.environ.get("CUJEV_BENCH_CKPT", "/tmp/cujev_synth_4b"))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: the engine is single-device (one process, one "
+              "stream per model) and this build runs no multi-GPU path; use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    from cujev import synthetic
+    t0 = time.perf_counter()
+    ckpt = synthetic.ensure_checkpoint(a.ckpt, "4b", seed=0, device="cuda")
+    torch.cuda.empty_cache()
+    log(f"checkpoint ready at {ckpt} ({time.perf_counter() - t0:.1f}s)")
+
+    e2e = run_e2e(ckpt, a.steps, a.warmup)
+    wall = e2e["wall_ms"]
+    ms = statistics.mean(wall)
+    p50 = statistics.median(wall)
+    log(f"e2e: {ms:.2f} ms/request mean, p50 {p50:.2f} ms, GPU p50 "
+        f"{statistics.median(e2e['gpu_ms']):.2f} ms")
+    res = {
+        "metric": "decisions/sec + p50 ms/request (4B shape, 530-tok state); attn MFMA util %",
+        "value": round(1e3 / ms, 3),
+        "unit": "decisions/s (requests/s; 1 request = 4 questions)",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 3),
+        "p50_ms_per_request": round(p50, 3),
+        "branch_decisions_per_s": round(4 * 1e3 / ms, 2),
+        "gpu_ms_per_request_p50": round(statistics.median(e2e["gpu_ms"]), 3),
+        "eval_only_ms_p50": round(statistics.median(e2e["eval_only_ms"]), 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random token ids, random-init bf16 weights ~N(0,0.02))",
+        "config": {"workload": "Qwen3.5-4B-shaped hybrid, fresh 530-token state prefill + 4 "
+                               "branches x 20 tokens, 3/2/2/4 labels per request",
+                   "model": e2e["info"]["name"], "layers": 32, "hidden": 2560,
+                   "vocab": 248320, "weights_gib": round(e2e["info"]["weight_gib"], 2)},
+    }
+    if not a.no_kernels:
+        att = attention_roofline()
+        log(f"attention config 3: {att['us']:.1f} us, {att['tflops']:.1f} TFLOP/s")
+        res["roofline"] = {"kernel": "attention_kernel (ops library), config 3",
+                           "bound": "mfma", "achieved": round(att["tflops"], 2),
+                           "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(att["tflops"] / PEAK_BF16_TFLOPS, 4),
+                           "traffic": None, "us_per_launch": round(att["us"], 2),
+                           "flop_per_launch": att["flop"]}
+        gdn = gdn_roofline()
+        log(f"gdn config 2 prefill: {gdn['us']:.1f} us, {gdn['gbs']:.1f} GB/s")
+        res["gdn_roofline"] = {"kernel": "gdn_conv_prep + gdn_chunk_a + gdn_chunk_b, config 2 "
+                                         "T=2048 prefill", "bound": "hbm",
+                               "achieved": round(gdn["gbs"], 1), "peak": PEAK_HBM_GBS,
+                               "unit": "GB/s", "frac": round(gdn["gbs"] / PEAK_HBM_GBS, 4),
+                               "us_per_layer": round(gdn["us"], 2),
+                               "compulsory_bytes": gdn["bytes"]}
+    if not a.no_cpu_baseline:
+        torch.cuda.empty_cache()
+        base, parity = cpu_baseline(ckpt, e2e["first_req"], e2e["first_out"])
+        res["cpu_baseline"] = base
+        res["parity"] = parity
+        if base:
+            log(f"cpu baseline: {base['ms_per_request']:.0f} ms/request; parity {parity}")
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,170 @@
+/* The forward pass: one function for both uses (REF src/engine/forward.c:1-149).
+ *
+ *   PREFILL  N tokens, one segment. Full-attention K and V^T go into the
+ *            state's cache; each GDN layer's final S and conv tail go into
+ *            the state.
+ *   EVAL     N tokens in B segments (branches). Every token attends to the
+ *            state's prefix plus its own segment; every GDN segment starts
+ *            from the state's S and conv tail (read-only, never copied).
+ *
+ * Per-call metadata (positions, segment starts, final-norm rows, the GDN
+ * chunk table, candidates) is built on the host and uploaded with ONE copy.
+ * The residual add and the next RMSNorm are fused, so a layer is
+ * 4 GEMMs + 4 (attention) or 3 (GDN) kernels + 2 norm/add passes.
+ * CUJEV_DEBUG_SYNC=1 synchronises and checks after every stage
+ * (REF src/engine/forward.c:21-41). */
+#include "engine/model.h"
+#include <math.h>
+
+static int debug_sync_enabled(void) {
+    static int cached = -1;
+    if (cached < 0) {
+        const char *e = getenv("CUJEV_DEBUG_SYNC");
+        cached = e && *e && *e != '0';
+    }
+    return cached;
+}
+
+static cujev_status check(cujev_model *m, hipError_t launch, const char *what, int layer) {
+    if (launch != hipSuccess)
+        return cujev_fail(launch == hipErrorInvalidValue ? CUJEV_ERR_UNSUPPORTED : CUJEV_ERR_CUDA,
+                          "%s (layer %d): %s", what, layer, hipGetErrorString(launch));
+    if (!debug_sync_enabled())
+        return CUJEV_OK;
+    hipError_t e = hipStreamSynchronize(m->stream);
+    if (e == hipSuccess)
+        e = hipGetLastError();
+    if (e != hipSuccess)
+        return cujev_fail(CUJEV_ERR_CUDA, "%s (layer %d): %s", what, layer, hipGetErrorString(e));
+    return CUJEV_OK;
+}
+
+#define K_TRY(call, what, layer) CUJEV_TRY(check(m, (call), (what), (layer)))
+
+cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
+                                           const int32_t *tokens, int N, const int32_t *seg_start,
+                                           const int32_t *seg_len, int B, const int32_t *cand,
+                                           const int32_t *ncand, int maxc, int32_t **d_cand,
+                                           int32_t **d_ncand) {
+    const cujev_config *c = &m->cfg;
+    const int H = c->hidden_size, I = c->intermediate_size;
+    const int P = mode == CUJEV_FWD_EVAL ? st->num_tokens : 0;
+    const float eps = c->rms_norm_eps;
+    hipStream_t s = m->stream;
+
+    /* ---- metadata: one packed block, one upload ---- */
+    int nc = 0;
+    for (int b = 0; b < B; b++)
+        nc += (seg_len[b] + 63) / 64;
+    if (nc > m->max_chunks)
+        return cujev_fail(CUJEV_ERR_CAPACITY, "%d GDN chunks exceed %d", nc, m->max_chunks);
+    int32_t *h = m->h_meta;
+    size_t o = 0;
+    const size_t o_tok = o; o += (size_t)N;
+    const size_t o_pos = o; o += (size_t)N;
+    const size_t o_base = o; o += (size_t)N;
+    const size_t o_rows = o; o += (size_t)B;
+    const size_t o_ctok = o; o += (size_t)nc;
+    const size_t o_clen = o; o += (size_t)nc;
+    const size_t o_sc0 = o; o += (size_t)B;
+    const size_t o_snc = o; o += (size_t)B;
+    const size_t o_cand = o; o += cand ? (size_t)B * maxc : 0;
+    const size_t o_ncand = o; o += cand ? (size_t)B : 0;
+    if (o > m->meta_ints)
+        return cujev_fail(CUJEV_ERR_CAPACITY, "per-call metadata exceeds its buffer");
+    memcpy(h + o_tok, tokens, (size_t)N * 4);
+    int ci = 0;
+    for (int b = 0; b < B; b++) {
+        for (int t = 0; t < seg_len[b]; t++) {
+            const int n = seg_start[b] + t;
+            h[o_pos + n] = P + t;
+            h[o_base + n] = seg_start[b];
+        }
+        h[o_rows + b] = seg_start[b] + seg_len[b] - 1;
+        h[o_sc0 + b] = ci;
+        for (int t = 0; t < seg_len[b]; t += 64) {
+            h[o_ctok + ci] = seg_start[b] + t;
+            h[o_clen + ci] = seg_len[b] - t < 64 ? seg_len[b] - t : 64;
+            ci++;
+        }
+        h[o_snc + b] = ci - h[o_sc0 + b];
+    }
+    if (cand) {
+        memcpy(h + o_cand, cand, (size_t)B * maxc * 4);
+        memcpy(h + o_ncand, ncand, (size_t)B * 4);
+    }
+    HIP_TRY(hipMemcpyAsync(m->d_meta, h, o * 4, hipMemcpyHostToDevice, s));
+    const int32_t *d = m->d_meta;
+    if (d_cand) {
+        *d_cand = cand ? m->d_meta + o_cand : NULL;
+        *d_ncand = cand ? m->d_meta + o_ncand : NULL;
+    }
+    const cujev_chunks chunks = {d + o_ctok, d + o_clen, d + o_sc0, d + o_snc, nc, B};
+    const cujev_gdn_scratch gws = cujev_gdn_scratch_carve(m->gdn_scratch, nc, m->Hv);
+    const float q_scale = (1.0f / sqrtf((float)m->D)) * 1.4426950408889634f;
+
+    K_TRY(k_embed(d + o_tok, m->embed, m->x, N, H, s), "embed", -1);
+    K_TRY(k_add_rmsnorm(m->x, NULL, m->layers[0].in_norm, m->xb, N, H, eps, NULL, 0, s), "norm", 0);
+
+    for (int l = 0; l < c->num_layers; l++) {
+        cujev_layer *ly = &m->layers[l];
+        if (ly->type == CUJEV_LAYER_FULL) {
+            K_TRY(k_gemm(m->gemm, m->xb, ly->w_qkv, m->proj, 0, N, m->w_attn, H, s), "gemm qkv", l);
+            bf16_t *kdst, *vdst;
+            int kstride;
+            if (mode == CUJEV_FWD_PREFILL) {
+                kdst = st->kv_k[l];
+                vdst = st->kv_vt[l];
+                kstride = m->state_stride;
+            } else {
+                kdst = m->br_k;
+                vdst = m->br_vt;
+                kstride = m->branch_stride;
+            }
+            K_TRY(k_attn_prep(m->proj, m->w_attn, ly->q_norm, ly->k_norm, d + o_pos, N, m->Hq,
+                              m->Hkv, c->rotary_dim, m->inv_freq, eps, q_scale, m->q, kdst, vdst,
+                              kstride, s),
+                  "attn_prep", l);
+            K_TRY(k_attention(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l], st->kv_vt[l],
+                              P, m->state_stride, kdst, vdst, kstride, d + o_base, N, m->Hq,
+                              m->Hkv, m->mix_out, s),
+                  "attention", l);
+            K_TRY(k_gemm(m->gemm, m->mix_out, ly->w_o, m->y, 0, N, H, m->Hq * m->D, s), "gemm o",
+                  l);
+        } else {
+            K_TRY(k_gemm(m->gemm, m->xb, ly->w_in, m->proj, 0, N, m->w_gdn, H, s), "gemm in", l);
+            const float *conv_in = mode == CUJEV_FWD_EVAL ? st->conv[l] : NULL;
+            float *conv_out = mode == CUJEV_FWD_PREFILL ? st->conv[l] : NULL;
+            K_TRY(k_gdn_conv_prep(m->proj, m->w_gdn, ly->conv_w, conv_in, conv_out, N, d + o_base,
+                                  ly->A_neg_exp, ly->dt_bias, N, m->Hk, m->Hv, m->gq, m->gk, m->gv,
+                                  m->gg, m->gbeta, s),
+                  "gdn_conv_prep", l);
+            const float *S_in = mode == CUJEV_FWD_EVAL ? st->S[l] : NULL;
+            float *S_out = mode == CUJEV_FWD_PREFILL ? st->S[l] : NULL;
+            K_TRY(k_gdn_scan(m->gq, m->gk, m->gv, m->gg, m->gbeta, &chunks, S_in, S_out,
+                             m->proj + m->C, m->w_gdn, ly->g_norm, eps, m->Hk, m->Hv, m->mix_out,
+                             &gws, s),
+                  "gdn_scan", l);
+            K_TRY(k_gemm(m->gemm, m->mix_out, ly->w_out, m->y, 0, N, H, m->V, s), "gemm out", l);
+        }
+        K_TRY(k_add_rmsnorm(m->x, m->y, ly->post_norm, m->xb, N, H, eps, NULL, 0, s), "add+norm",
+              l);
+        K_TRY(k_gemm(m->gemm, m->xb, ly->w_gate_up, m->proj, 0, N, 2 * I, H, s), "gemm gate_up", l);
+        K_TRY(k_silu_mul(m->proj, m->act, N, I, s), "silu_mul", l);
+        K_TRY(k_gemm(m->gemm, m->act, ly->w_down, m->y, 0, N, H, I, s), "gemm down", l);
+        if (l + 1 < c->num_layers)
+            K_TRY(k_add_rmsnorm(m->x, m->y, m->layers[l + 1].in_norm, m->xb, N, H, eps, NULL, 0, s),
+                  "add+norm", l);
+        else /* final norm only at the last token of every segment */
+            K_TRY(k_add_rmsnorm(m->x, m->y, m->final_norm, m->hsel, N, H, eps, d + o_rows, B, s),
+                  "final norm", l);
+    }
+    return CUJEV_OK;
+}
+
+cujev_status cujev_forward(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
+                           const int32_t *tokens, int N, const int32_t *seg_start,
+                           const int32_t *seg_len, int B) {
+    return cujev_forward_with_candidates(m, st, mode, tokens, N, seg_start, seg_len, B, NULL, NULL,
+                                         0, NULL, NULL);
+}

@@ -1,0 +1,320 @@
+/* Weight upload and workspace sizing.
+ *
+ * Behaviour of REF src/engine/model.c:161-247 (which tensors, the "model." or
+ * "model.language_model." prefix, tied embeddings, row-fused q|k|v, qkv|z|b|a
+ * and gate|up, +1 on the zero-centred norms, A_neg_exp = -exp(A_log)) and
+ * :249-313 (one workspace arena for the largest call). Matrices are uploaded
+ * as bf16 (F16/F32 converted with round-to-nearest-even), vectors as fp32.
+ * Sizes are computed by a dry run of the same walk, so the arena is exact. */
+#include "engine/model.h"
+#include "core/safetensors.h"
+#include <math.h>
+
+static float bf16_bits_to_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static float f16_bits_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    int exp = (h >> 10) & 0x1f;
+    uint32_t mant = h & 0x3ff, u;
+    if (exp == 0x1f) {
+        u = sign | 0x7f800000u | (mant << 13);
+    } else if (exp == 0) {
+        if (mant == 0) {
+            u = sign;
+        } else { /* subnormal: normalise */
+            int e = -1;
+            do {
+                mant <<= 1;
+                e++;
+            } while (!(mant & 0x400));
+            mant &= 0x3ff;
+            u = sign | ((uint32_t)(127 - 15 - e) << 23) | (mant << 13);
+        }
+    } else {
+        u = sign | ((uint32_t)(exp - 15 + 127) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) /* NaN stays NaN */
+        return (uint16_t)((u >> 16) | 0x40);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+static float elem_f32(const st_tensor *t, size_t i) {
+    switch (t->dtype) {
+    case ST_F32: return ((const float *)t->data)[i];
+    case ST_BF16: return bf16_bits_to_f32(((const uint16_t *)t->data)[i]);
+    default: return f16_bits_to_f32(((const uint16_t *)t->data)[i]);
+    }
+}
+
+typedef struct loader {
+    cujev_model *m;
+    const st_bundle *b;
+    const char *prefix;
+    int dry;      /* size only */
+    size_t bytes; /* dry-run total */
+    uint16_t *conv; /* conversion buffer */
+    size_t conv_cap;
+} loader;
+
+static const st_tensor *find(loader *L, const char *fmt, int layer) {
+    char name[256], full[320];
+    snprintf(name, sizeof name, fmt, layer);
+    snprintf(full, sizeof full, "%s%s", L->prefix, name);
+    return st_bundle_find(L->b, full);
+}
+
+static cujev_status want(loader *L, const char *fmt, int layer, const st_tensor **out) {
+    *out = find(L, fmt, layer);
+    if (!*out) {
+        char name[256];
+        snprintf(name, sizeof name, fmt, layer);
+        return cujev_fail(CUJEV_ERR_FORMAT, "missing tensor %s%s", L->prefix, name);
+    }
+    if ((*out)->dtype == ST_OTHER)
+        return cujev_fail(CUJEV_ERR_UNSUPPORTED, "tensor %s: unsupported dtype", (*out)->name);
+    return CUJEV_OK;
+}
+
+static void *take(loader *L, size_t bytes) {
+    if (L->dry) {
+        L->bytes += cujev_align_up(bytes, 256);
+        return NULL;
+    }
+    return cujev_arena_alloc(&L->m->weights, bytes);
+}
+
+/* Row-concatenation of 2-D tensors [rows_i, K] -> one bf16 [sum rows, K]. */
+static cujev_status upload_fused(loader *L, const st_tensor **parts, int nparts, int K,
+                                 bf16_t **out) {
+    size_t rows = 0;
+    for (int i = 0; i < nparts; i++) {
+        if (parts[i]->ndim != 2 || parts[i]->shape[1] != K)
+            return cujev_fail(CUJEV_ERR_FORMAT, "tensor %s: expected [*, %d]", parts[i]->name, K);
+        rows += (size_t)parts[i]->shape[0];
+    }
+    bf16_t *d = (bf16_t *)take(L, rows * (size_t)K * 2);
+    if (L->dry)
+        return CUJEV_OK;
+    if (!d)
+        return cujev_fail(CUJEV_ERR_OOM, "weight arena exhausted");
+    size_t off = 0;
+    for (int i = 0; i < nparts; i++) {
+        const st_tensor *t = parts[i];
+        const size_t n = st_numel(t);
+        if (t->dtype == ST_BF16) {
+            HIP_TRY(hipMemcpy(d + off, t->data, n * 2, hipMemcpyHostToDevice));
+        } else {
+            const size_t step = (size_t)1 << 24;
+            if (L->conv_cap < step) {
+                free(L->conv);
+                L->conv = (uint16_t *)malloc(step * 2);
+                if (!L->conv)
+                    return cujev_fail(CUJEV_ERR_OOM, "host conversion buffer");
+                L->conv_cap = step;
+            }
+            for (size_t s = 0; s < n; s += step) {
+                const size_t c = n - s < step ? n - s : step;
+                for (size_t j = 0; j < c; j++)
+                    L->conv[j] = f32_to_bf16_bits(elem_f32(t, s + j));
+                HIP_TRY(hipMemcpy(d + off + s, L->conv, c * 2, hipMemcpyHostToDevice));
+            }
+        }
+        off += n;
+    }
+    *out = d;
+    return CUJEV_OK;
+}
+
+/* Small fp32 vector, optionally +add or -exp(x). */
+static cujev_status upload_f32(loader *L, const st_tensor *t, float add, int negexp, size_t expect,
+                               float **out) {
+    const size_t n = st_numel(t);
+    if (expect && n != expect)
+        return cujev_fail(CUJEV_ERR_FORMAT, "tensor %s: %zu elements, expected %zu", t->name, n,
+                          expect);
+    float *d = (float *)take(L, n * 4);
+    if (L->dry)
+        return CUJEV_OK;
+    if (!d)
+        return cujev_fail(CUJEV_ERR_OOM, "weight arena exhausted");
+    float *h = (float *)malloc(n * 4);
+    if (!h)
+        return cujev_fail(CUJEV_ERR_OOM, "host vector");
+    for (size_t i = 0; i < n; i++) {
+        const float v = elem_f32(t, i);
+        h[i] = negexp ? -expf(v) : v + add;
+    }
+    hipError_t e = hipMemcpy(d, h, n * 4, hipMemcpyHostToDevice);
+    free(h);
+    if (e != hipSuccess)
+        return cujev_fail(CUJEV_ERR_CUDA, "hipMemcpy: %s", hipGetErrorString(e));
+    *out = d;
+    return CUJEV_OK;
+}
+
+static cujev_status walk(loader *L) {
+    cujev_model *m = L->m;
+    const cujev_config *c = &m->cfg;
+    const int H = c->hidden_size;
+    const st_tensor *t, *parts[4];
+    CUJEV_TRY(want(L, "embed_tokens.weight", 0, &t));
+    if (t->ndim != 2 || t->shape[0] != c->vocab_size || t->shape[1] != H)
+        return cujev_fail(CUJEV_ERR_FORMAT, "embed_tokens shape mismatch");
+    CUJEV_TRY(upload_fused(L, &t, 1, H, &m->embed));
+    m->lm_head = m->embed;
+    if (!c->tie_word_embeddings) {
+        const st_tensor *lm = st_bundle_find(L->b, "lm_head.weight");
+        if (!lm)
+            return cujev_fail(CUJEV_ERR_FORMAT,
+                              "tie_word_embeddings is false but lm_head.weight is missing");
+        if (lm->ndim != 2 || lm->shape[0] != c->vocab_size)
+            return cujev_fail(CUJEV_ERR_FORMAT, "lm_head shape mismatch");
+        CUJEV_TRY(upload_fused(L, &lm, 1, H, &m->lm_head));
+    }
+    CUJEV_TRY(want(L, "norm.weight", 0, &t));
+    CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)H, &m->final_norm));
+    for (int l = 0; l < c->num_layers; l++) {
+        cujev_layer *ly = &m->layers[l];
+        ly->type = c->layer_types[l];
+        CUJEV_TRY(want(L, "layers.%d.input_layernorm.weight", l, &t));
+        CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)H, &ly->in_norm));
+        CUJEV_TRY(want(L, "layers.%d.post_attention_layernorm.weight", l, &t));
+        CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)H, &ly->post_norm));
+        if (ly->type == CUJEV_LAYER_FULL) {
+            CUJEV_TRY(want(L, "layers.%d.self_attn.q_proj.weight", l, &parts[0]));
+            CUJEV_TRY(want(L, "layers.%d.self_attn.k_proj.weight", l, &parts[1]));
+            CUJEV_TRY(want(L, "layers.%d.self_attn.v_proj.weight", l, &parts[2]));
+            if (parts[0]->shape[0] != (int64_t)m->Hq * 2 * m->D ||
+                parts[1]->shape[0] != (int64_t)m->Hkv * m->D ||
+                parts[2]->shape[0] != (int64_t)m->Hkv * m->D)
+                return cujev_fail(CUJEV_ERR_FORMAT, "layer %d: attention projection shapes", l);
+            CUJEV_TRY(upload_fused(L, parts, 3, H, &ly->w_qkv));
+            CUJEV_TRY(want(L, "layers.%d.self_attn.o_proj.weight", l, &t));
+            CUJEV_TRY(upload_fused(L, &t, 1, m->Hq * m->D, &ly->w_o));
+            CUJEV_TRY(want(L, "layers.%d.self_attn.q_norm.weight", l, &t));
+            CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)m->D, &ly->q_norm));
+            CUJEV_TRY(want(L, "layers.%d.self_attn.k_norm.weight", l, &t));
+            CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)m->D, &ly->k_norm));
+        } else {
+            CUJEV_TRY(want(L, "layers.%d.linear_attn.in_proj_qkv.weight", l, &parts[0]));
+            CUJEV_TRY(want(L, "layers.%d.linear_attn.in_proj_z.weight", l, &parts[1]));
+            CUJEV_TRY(want(L, "layers.%d.linear_attn.in_proj_b.weight", l, &parts[2]));
+            CUJEV_TRY(want(L, "layers.%d.linear_attn.in_proj_a.weight", l, &parts[3]));
+            if (parts[0]->shape[0] != m->C || parts[1]->shape[0] != m->V ||
+                parts[2]->shape[0] != m->Hv || parts[3]->shape[0] != m->Hv)
+                return cujev_fail(CUJEV_ERR_FORMAT, "layer %d: GDN projection shapes", l);
+            CUJEV_TRY(upload_fused(L, parts, 4, H, &ly->w_in));
+            CUJEV_TRY(want(L, "layers.%d.linear_attn.out_proj.weight", l, &t));
+            CUJEV_TRY(upload_fused(L, &t, 1, m->V, &ly->w_out));
+            CUJEV_TRY(want(L, "layers.%d.linear_attn.conv1d.weight", l, &t));
+            CUJEV_TRY(upload_f32(L, t, 0.f, 0, (size_t)m->C * 4, &ly->conv_w));
+            CUJEV_TRY(want(L, "layers.%d.linear_attn.A_log", l, &t));
+            CUJEV_TRY(upload_f32(L, t, 0.f, 1, (size_t)m->Hv, &ly->A_neg_exp));
+            CUJEV_TRY(want(L, "layers.%d.linear_attn.dt_bias", l, &t));
+            CUJEV_TRY(upload_f32(L, t, 0.f, 0, (size_t)m->Hv, &ly->dt_bias));
+            CUJEV_TRY(want(L, "layers.%d.linear_attn.norm.weight", l, &t));
+            CUJEV_TRY(upload_f32(L, t, 0.f, 0, 128, &ly->g_norm));
+        }
+        CUJEV_TRY(want(L, "layers.%d.mlp.gate_proj.weight", l, &parts[0]));
+        CUJEV_TRY(want(L, "layers.%d.mlp.up_proj.weight", l, &parts[1]));
+        if (parts[0]->shape[0] != c->intermediate_size || parts[1]->shape[0] != c->intermediate_size)
+            return cujev_fail(CUJEV_ERR_FORMAT, "layer %d: MLP shapes", l);
+        CUJEV_TRY(upload_fused(L, parts, 2, H, &ly->w_gate_up));
+        CUJEV_TRY(want(L, "layers.%d.mlp.down_proj.weight", l, &t));
+        CUJEV_TRY(upload_fused(L, &t, 1, c->intermediate_size, &ly->w_down));
+    }
+    return CUJEV_OK;
+}
+
+cujev_status cujev_model_load_weights(cujev_model *m, const char *dir) {
+    st_bundle b;
+    CUJEV_TRY(st_bundle_open(dir, &b));
+    loader L;
+    memset(&L, 0, sizeof L);
+    L.m = m;
+    L.b = &b;
+    L.prefix = st_bundle_find(&b, "model.language_model.embed_tokens.weight") ? "model.language_model."
+                                                                               : "model.";
+    L.dry = 1;
+    cujev_status s = walk(&L);
+    if (s == CUJEV_OK) {
+        cujev_log(m->opts.verbose, "weights: %.2f GiB in %d tensors, %d shards",
+                  L.bytes / 1073741824.0, b.num_tensors, b.num_files);
+        s = cujev_arena_init(&m->weights, L.bytes + 4096);
+    }
+    if (s == CUJEV_OK) {
+        L.dry = 0;
+        s = walk(&L);
+    }
+    free(L.conv);
+    st_bundle_close(&b);
+    return s;
+}
+
+cujev_status cujev_model_alloc_workspace(cujev_model *m) {
+    const cujev_config *c = &m->cfg;
+    const size_t N = (size_t)m->max_tokens, H = (size_t)c->hidden_size,
+                 I = (size_t)c->intermediate_size;
+    const size_t B = (size_t)(m->opts.max_branches > 0 ? m->opts.max_branches : 1);
+    const size_t mix = N * (size_t)((m->Hq * m->D > m->V) ? m->Hq * m->D : m->V);
+    const size_t br_kv = (size_t)m->Hkv * m->branch_stride * m->D * 2;
+    m->max_chunks = m->max_tokens / 64 + (int)B + 1;
+    m->meta_ints = 3 * N + 3 * B + 2 * (size_t)m->max_chunks + B * (size_t)m->opts.max_candidates + B;
+    m->gemm_ws_bytes = (size_t)64 << 20;
+    struct {
+        void **p;
+        size_t bytes;
+    } parts[] = {
+        {(void **)&m->x, N * H * 4},
+        {(void **)&m->xb, N * H * 2},
+        {(void **)&m->proj, N * (size_t)m->w_proj * 2},
+        {(void **)&m->y, N * H * 2},
+        {(void **)&m->q, N * (size_t)m->Hq * m->D * 2},
+        {(void **)&m->mix_out, mix * 2},
+        {(void **)&m->br_k, br_kv},
+        {(void **)&m->br_vt, br_kv},
+        {(void **)&m->gq, N * (size_t)m->Hk * 128 * 2},
+        {(void **)&m->gk, N * (size_t)m->Hk * 128 * 2},
+        {(void **)&m->gv, N * (size_t)m->Hv * 128 * 2},
+        {(void **)&m->gg, N * (size_t)m->Hv * 4},
+        {(void **)&m->gbeta, N * (size_t)m->Hv * 4},
+        {(void **)&m->gdn_scratch, cujev_gdn_scratch_bytes(m->max_chunks, m->Hv)},
+        {(void **)&m->act, N * I * 2},
+        {(void **)&m->hsel, B * H * 2},
+        {(void **)&m->full_logits, B * (size_t)c->vocab_size * 4},
+        {(void **)&m->gemm_ws, m->gemm_ws_bytes},
+        {(void **)&m->d_meta, m->meta_ints * 4},
+        {(void **)&m->d_logits, B * (size_t)(m->opts.max_candidates > 0 ? m->opts.max_candidates : 1) * 4},
+    };
+    const int np = (int)(sizeof parts / sizeof parts[0]);
+    size_t total = 0;
+    for (int i = 0; i < np; i++)
+        total += cujev_align_up(parts[i].bytes, 256);
+    CUJEV_TRY(cujev_arena_init(&m->work, total + 4096));
+    for (int i = 0; i < np; i++) {
+        *parts[i].p = cujev_arena_alloc(&m->work, parts[i].bytes);
+        if (!*parts[i].p)
+            return cujev_fail(CUJEV_ERR_OOM, "workspace arena undersized");
+    }
+    /* Branch K/V scratch must hold finite values everywhere: 64-key tiles read
+     * past the valid keys (masked to p = 0, and 0 * NaN would be NaN). */
+    HIP_TRY(hipMemset(m->br_k, 0, br_kv));
+    HIP_TRY(hipMemset(m->br_vt, 0, br_kv));
+    HIP_TRY(hipHostMalloc((void **)&m->h_meta, m->meta_ints * 4, hipHostMallocDefault));
+    cujev_log(m->opts.verbose, "workspace: %.2f GiB for %zu tokens, %zu branches",
+              m->work.used / 1073741824.0, N, B);
+    return CUJEV_OK;
+}

@@ -1,0 +1,119 @@
+/* Model, state and workspace of the host engine.
+ * Role of REF src/engine/model.h:15-98, with the MI355X data layout:
+ *   state, per full layer   K   bf16 [Hkv][kv_stride(max_state)][256]
+ *                           V^T bf16 [Hkv][256][kv_stride(max_state)]
+ *   state, per GDN layer    S fp32 [Hv][128][128], conv tail fp32 [C][3]
+ *   workspace               branch K / V^T in the same layouts, bf16 q,
+ *                           GDN bf16 q/k/v + chunk scratch, fp32 residual. */
+#ifndef CUJEV_MODEL_H
+#define CUJEV_MODEL_H
+
+#include "core/config.h"
+#include "core/util.h"
+#include "cujev.h"
+#include "kernels/kernels.h"
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct cujev_layer {
+    cujev_layer_type type;
+    float *in_norm;   /* [H] fp32, 1 + w */
+    float *post_norm; /* [H] fp32, 1 + w */
+    /* full attention */
+    bf16_t *w_qkv;          /* [Hq*512 + 2*Hkv*256, H] row-fused q|k|v */
+    float *q_norm, *k_norm; /* [256], 1 + w */
+    bf16_t *w_o;            /* [H, Hq*256] */
+    /* gated delta net */
+    bf16_t *w_in;     /* [C + V + 2Hv, H] row-fused qkv|z|b|a */
+    float *conv_w;    /* [C][4] */
+    float *A_neg_exp; /* [Hv] = -exp(A_log) */
+    float *dt_bias;   /* [Hv] */
+    float *g_norm;    /* [128] (not zero-centred) */
+    bf16_t *w_out;    /* [H, V] */
+    /* mlp */
+    bf16_t *w_gate_up; /* [2I, H] row-fused gate|up */
+    bf16_t *w_down;    /* [H, I] */
+} cujev_layer;
+
+struct cujev_model {
+    cujev_config cfg;
+    cujev_options opts;
+    cujev_arena weights;
+    cujev_arena work;
+    cujev_gemm *gemm;
+    hipStream_t stream;
+    hipEvent_t ev0, ev1;
+    cujev_timing timing;
+    float inv_freq[32]; /* RoPE 1/theta^(2i/rot), computed in double */
+
+    bf16_t *embed;     /* [V, H] */
+    bf16_t *lm_head;   /* [V, H]; == embed when tied */
+    float *final_norm; /* [H], 1 + w */
+    cujev_layer layers[CUJEV_MAX_LAYERS];
+
+    /* derived widths */
+    int D, Hq, Hkv, Hk, Hv, K, V, C;
+    int w_attn, w_gdn, w_proj;
+    int max_tokens;     /* workspace rows: max(max_state, max_branch) */
+    int max_chunks;     /* GDN chunks of one forward */
+    int state_stride;   /* kv stride of the state caches */
+    int branch_stride;  /* kv stride of the branch scratch */
+
+    /* workspace (device) */
+    float *x;        /* [N,H] fp32 residual */
+    bf16_t *xb;      /* [N,H] normed input */
+    bf16_t *proj;    /* [N, w_proj] */
+    bf16_t *y;       /* [N,H] */
+    bf16_t *q;       /* [N,Hq,256] prescaled */
+    bf16_t *mix_out; /* [N, max(Hq*256, V)] */
+    bf16_t *br_k, *br_vt;
+    bf16_t *gq, *gk, *gv; /* [N][Hk|Hv][128] */
+    float *gg, *gbeta;    /* [N][Hv] */
+    void *gdn_scratch;
+    bf16_t *act;  /* [N, I] */
+    bf16_t *hsel; /* [B, H] */
+    float *full_logits; /* [B, vocab] */
+    void *gemm_ws;
+    size_t gemm_ws_bytes;
+    /* per-call metadata, one device block uploaded with one copy */
+    int32_t *d_meta, *h_meta; /* h_meta is pinned host memory */
+    size_t meta_ints;
+    float *d_logits; /* [B, max_candidates] */
+};
+
+struct cujev_state {
+    cujev_model *model;
+    cujev_arena mem;
+    int num_tokens;
+    bf16_t **kv_k, **kv_vt; /* per layer, NULL for GDN layers */
+    float **S;              /* per layer, NULL for full layers */
+    float **conv;           /* per layer, NULL for full layers */
+};
+
+cujev_status cujev_model_load_weights(cujev_model *m, const char *dir);
+cujev_status cujev_model_alloc_workspace(cujev_model *m);
+
+typedef enum { CUJEV_FWD_PREFILL = 0, CUJEV_FWD_EVAL = 1 } cujev_fwd_mode;
+
+/* Run the network over N tokens in B segments (host arrays). PREFILL: one
+ * segment, side outputs go to the state. EVAL: every segment sees the state's
+ * prefix and itself. On return hsel[B,H] holds the final-norm output of every
+ * segment's last token, and candidates (if any) were staged by the caller. */
+cujev_status cujev_forward(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
+                           const int32_t *tokens, int N, const int32_t *seg_start,
+                           const int32_t *seg_len, int B);
+/* Same, also uploading candidate ids (host [B][maxc]) and counts (host [B])
+ * with the metadata; their device copies are returned in d_cand / d_ncand. */
+cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
+                                           const int32_t *tokens, int N, const int32_t *seg_start,
+                                           const int32_t *seg_len, int B, const int32_t *cand,
+                                           const int32_t *ncand, int maxc, int32_t **d_cand,
+                                           int32_t **d_ncand);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

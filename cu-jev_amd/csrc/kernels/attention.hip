@@ -31,6 +31,7 @@
 #include "common.h"
 #include "kernels.h"
 
+namespace CUJEV_KNS {
 namespace {
 
 constexpr int D = 256;
@@ -40,7 +41,8 @@ constexpr int K_BYTES = BK * D * 2;      /* 32 KiB: K tile [64][256]    */
 constexpr int V_BYTES = D * BK * 2;      /* 32 KiB: V^T tile [256][64]  */
 constexpr int BUF_BYTES = K_BYTES + V_BYTES;
 
-/* 16-byte chunk swizzles (see the bank analysis in DESIGN.md). */
+/* 16-byte chunk swizzles: the 16 lanes of one ds_read_b128 phase hit 16
+ * distinct 16-byte bank groups (and any 8 consecutive lanes 8 distinct ones). */
 DEV int swz_k(int key) { return ((key & 4) << 1) | ((key & 8) >> 1) | (key & 3); }
 DEV int swz_v(int d) { return (d & 7) ^ ((d >> 3) & 1); }
 /* MFMA row m of the S^T tile holds key perm_row(m) of its 32-key block. */
@@ -360,6 +362,8 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
 }
 
 } // namespace
+} // namespace CUJEV_KNS
+using namespace CUJEV_KNS;
 
 extern "C" hipError_t k_attn_prep(const bf16_t *proj, int proj_stride, const float *q_norm_w,
                                   const float *k_norm_w, const int32_t *pos, int N, int Hq, int Hkv,

@@ -18,6 +18,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 #define DEV __device__ __forceinline__
 
+/* Kernels live in this namespace. The engine library and the operator
+ * library compile the same sources under different names, so profiles tell
+ * their launches apart. */
+#ifndef CUJEV_KNS
+#define CUJEV_KNS cujev
+#endif
+
 DEV float bf2f(bf16 x) { return (float)x; }
 DEV bf16 f2bf(float x) { return (bf16)x; } /* round to nearest even */
 

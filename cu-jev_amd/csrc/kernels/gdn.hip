@@ -30,6 +30,7 @@
 #include "common.h"
 #include "kernels.h"
 
+namespace CUJEV_KNS {
 namespace {
 
 constexpr int DK = 128; /* key head dim   */
@@ -476,6 +477,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
 }
 
 } // namespace
+} // namespace CUJEV_KNS
+using namespace CUJEV_KNS;
 
 extern "C" hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const float *conv_w,
                                       const float *conv_in, float *conv_out, int seg0_len,

@@ -1,0 +1,118 @@
+/* Projection GEMMs through hipBLASLt (the role cuBLAS GemmEx plays in the
+ * reference, src/kernels/elementwise.cu:56-75).
+ *
+ * Y[N, M] = X[N, K] . W[M, K]^T, bf16 inputs, fp32 accumulation, bf16 or fp32
+ * output, all row-major. In hipBLASLt's column-major terms this is
+ * D(M x N) = op_T(A = W seen as K x M) . B (= X seen as K x N).
+ * Descriptors and the heuristic's algorithm are cached per (N, M, K, out). */
+#include "kernels.h"
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+struct GemmPlan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo;
+    size_t ws = 0;
+};
+
+struct cujev_gemm {
+    hipblasLtHandle_t handle = nullptr;
+    void *workspace = nullptr;
+    size_t ws_bytes = 0;
+    std::map<std::tuple<int, int, int, int>, GemmPlan> plans;
+    std::mutex mu;
+};
+
+static void destroy_plan(GemmPlan &p) {
+    if (p.desc)
+        hipblasLtMatmulDescDestroy(p.desc);
+    if (p.a)
+        hipblasLtMatrixLayoutDestroy(p.a);
+    if (p.b)
+        hipblasLtMatrixLayoutDestroy(p.b);
+    if (p.c)
+        hipblasLtMatrixLayoutDestroy(p.c);
+}
+
+extern "C" int cujev_gemm_create(cujev_gemm **out, void *workspace, size_t ws_bytes) {
+    cujev_gemm *g = new (std::nothrow) cujev_gemm();
+    if (!g)
+        return -1;
+    if (hipblasLtCreate(&g->handle) != HIPBLAS_STATUS_SUCCESS) {
+        delete g;
+        return -1;
+    }
+    g->workspace = workspace;
+    g->ws_bytes = ws_bytes;
+    *out = g;
+    return 0;
+}
+
+extern "C" void cujev_gemm_destroy(cujev_gemm *g) {
+    if (!g)
+        return;
+    for (auto &kv : g->plans)
+        destroy_plan(kv.second);
+    if (g->handle)
+        hipblasLtDestroy(g->handle);
+    delete g;
+}
+
+static bool make_plan(cujev_gemm *g, int N, int M, int K, int f32out, GemmPlan &p) {
+    const hipDataType out_t = f32out ? HIP_R_32F : HIP_R_16BF;
+    if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
+        return false;
+    const int32_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta);
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb);
+    if (hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, K, M, K) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, K, N, K) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&p.c, out_t, M, N, M) != HIPBLAS_STATUS_SUCCESS)
+        return false;
+    hipblasLtMatmulPreference_t pref;
+    if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS)
+        return false;
+    uint64_t ws = g->ws_bytes;
+    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                          sizeof ws);
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int count = 0;
+    hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(g->handle, p.desc, p.a, p.b, p.c, p.c,
+                                                         pref, 1, res, &count);
+    hipblasLtMatmulPreferenceDestroy(pref);
+    if (st != HIPBLAS_STATUS_SUCCESS || count < 1)
+        return false;
+    p.algo = res[0].algo;
+    p.ws = res[0].workspaceSize;
+    return true;
+}
+
+extern "C" hipError_t k_gemm(cujev_gemm *g, const bf16_t *X, const bf16_t *W, void *Y, int f32out,
+                             int N, int M, int K, hipStream_t stream) {
+    if (N <= 0)
+        return hipSuccess;
+    GemmPlan *plan;
+    {
+        std::lock_guard<std::mutex> lk(g->mu);
+        auto key = std::make_tuple(N, M, K, f32out);
+        auto it = g->plans.find(key);
+        if (it == g->plans.end()) {
+            GemmPlan p;
+            if (!make_plan(g, N, M, K, f32out, p)) {
+                destroy_plan(p);
+                return hipErrorNotSupported;
+            }
+            it = g->plans.emplace(key, p).first;
+        }
+        plan = &it->second;
+    }
+    const float alpha = 1.f, beta = 0.f;
+    hipblasStatus_t st = hipblasLtMatmul(g->handle, plan->desc, &alpha, W, plan->a, X, plan->b,
+                                         &beta, Y, plan->c, Y, plan->c, &plan->algo, g->workspace,
+                                         plan->ws, stream);
+    return st == HIPBLAS_STATUS_SUCCESS ? hipSuccess : hipErrorLaunchFailure;
+}

@@ -115,6 +115,36 @@ hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const f
                       int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *scratch,
                       hipStream_t stream);
 
+/* ---- per-layer glue --------------------------------------------------------
+ * x[N,H] fp32 residual = E[tokens] (bf16 table).  REF elementwise.cu:3-11. */
+hipError_t k_embed(const int32_t *tokens, const bf16_t *E, float *x, int N, int H, hipStream_t s);
+
+/* Fused residual add + RMSNorm (REF elementwise.cu:13-40). Output row r reads
+ * source row src = rows ? rows[r] : r (R rows, else N):
+ *   v = x[src] + (y ? y[src] : 0);  x[src] = v when y && !rows;
+ *   out[r] = bf16(v * rsqrt(mean v^2 + eps) * w)   (w holds 1 + weight).
+ * H must be a multiple of 4 and at most 16384. */
+hipError_t k_add_rmsnorm(float *x, const bf16_t *y, const float *w, bf16_t *out, int N, int H,
+                         float eps, const int32_t *rows, int R, hipStream_t s);
+
+/* act[N,I] = bf16(silu(gu[:, :I]) * gu[:, I:])  (REF elementwise.cu:42-54). */
+hipError_t k_silu_mul(const bf16_t *gu, bf16_t *act, int N, int I, hipStream_t s);
+
+/* logits[b*ld + i] = h[b] . E[cand[b*cand_ld + i]], i < ncand[b]
+ * (REF elementwise.cu:78-97). h bf16 [B,H], fp32 accumulation. */
+hipError_t k_readout(const bf16_t *h, const bf16_t *E, const int32_t *cand, const int32_t *ncand,
+                     int cand_ld, float *logits, int ld, int B, int H, hipStream_t s);
+
+/* ---- projection GEMMs (hipBLASLt) ------------------------------------------
+ * Y[N,M] = X[N,K] . W[M,K]^T, bf16 in, fp32 accumulate, bf16 (f32out = 0) or
+ * fp32 out. REF elementwise.cu:56-75. `workspace` (ws_bytes) is device memory
+ * owned by the caller. */
+typedef struct cujev_gemm cujev_gemm;
+int cujev_gemm_create(cujev_gemm **out, void *workspace, size_t ws_bytes);
+void cujev_gemm_destroy(cujev_gemm *g);
+hipError_t k_gemm(cujev_gemm *g, const bf16_t *X, const bf16_t *W, void *Y, int f32out, int N,
+                  int M, int K, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -179,10 +179,12 @@ def shared_prefix_attention(q, gate, k_state, v_state, k_own, v_own, own_base,
     return out * sigmoid(gate)
 
 
-def causal_gqa_attention(q, gate, k, v, scale=1.0 / 16.0):
+def causal_gqa_attention(q, gate, k, v, scale=1.0 / 16.0, bf16_p=False):
     """transformers-style causal attention over one sequence
     (TF:604-626 eager_attention_forward + repeat_kv TF:592-601, gate TF:697-700).
-    q, gate: [T, Hq, D]; k, v: [T, Hkv, D]."""
+    q, gate: [T, Hq, D]; k, v: [T, Hkv, D]. bf16_p: the probabilities are
+    rounded to bf16 before the PV product, the row sum is not (engine
+    semantics, REF attention.cu:270-278)."""
     T, Hq, D = q.shape
     Hkv = k.shape[1]
     grp = Hq // Hkv
@@ -193,8 +195,10 @@ def causal_gqa_attention(q, gate, k, v, scale=1.0 / 16.0):
     s = np.where(mask[None], -np.inf, s)
     s = s - s.max(-1, keepdims=True)
     p = np.exp(s)
-    p /= p.sum(-1, keepdims=True)
-    o = np.einsum("hts,shd->thd", p, vr)
+    l = p.sum(-1, keepdims=True)
+    if bf16_p:
+        p = bf16_round(p.astype(np.float32)).astype(np.float64)
+    o = np.einsum("hts,shd->thd", p / l, vr)
     return o * sigmoid(gate)
 
 
@@ -311,7 +315,8 @@ def gdn_chunked(q, k, v, g, beta, S0=None, chunk=64):
             Q, K, Vv = q[c0:c1, h], k[c0:c1, h], v[c0:c1, h]
             bt = beta[c0:c1, h]
             G = np.cumsum(g[c0:c1, h])
-            Gam = np.exp(G[:, None] - G[None, :])
+            with np.errstate(over="ignore"):  # only the masked upper part overflows
+                Gam = np.exp(G[:, None] - G[None, :])
             A = np.tril((bt[:, None] * (K @ K.T)) * Gam, -1)
             Tm = np.linalg.inv(np.eye(L) + A)
             W = Tm @ (K * (bt * np.exp(G))[:, None])
@@ -336,3 +341,98 @@ def gated_rmsnorm(o, z, w, eps, bf16_roundtrip=True):
     if bf16_roundtrip:
         hn = bf16_round(hn.astype(np.float32)).astype(np.float64)
     return hn * np.asarray(w, np.float64) * silu(z)
+
+
+# --------------------------------------------------------------------------
+# whole model (transformers Qwen3_5ForCausalLM semantics, float64)
+# --------------------------------------------------------------------------
+def load_checkpoint(path):
+    """config.json + *.safetensors of a local directory -> (cfg, {name: f64}).
+    Reads with safetensors' torch loader (no pickle); text model only."""
+    import json
+    from pathlib import Path
+
+    from safetensors.torch import load_file
+
+    path = Path(path)
+    cfg = json.loads((path / "config.json").read_text())
+    cfg = cfg.get("text_config", cfg)
+    W = {}
+    for f in sorted(path.glob("*.safetensors")):
+        for k, v in load_file(str(f)).items():
+            W[k.replace("model.language_model.", "model.")] = v.float().numpy().astype(np.float64)
+    return cfg, W
+
+
+def _b(x, on):
+    """bf16 rounding point of the engine, applied when `on`."""
+    return bf16_round(np.asarray(x, np.float32)).astype(np.float64) if on else x
+
+
+def model_last_logits(cfg, W, ids, chunked=True, engine_numerics=False):
+    """Next-token logits at the last position of one causal sequence `ids`.
+
+    Decoder layer TF:740-793 (pre-norm, residual), full attention TF:656-701,
+    GDN TF:432-543 in its fp32 form (no bf16 round trip inside the gated norm),
+    MLP TF:704-717, final norm and LM head (tied: the embedding) TF:1571-1650.
+    Pinned by the transformers golden logits (tests/test_golden.py) and by the
+    engine invariants it is used for (branch = [state ++ branch]).
+
+    engine_numerics=True rounds to bf16 where the reference engine stores
+    bf16 (REF docs/ARCHITECTURE.md:67-75, src/kernels/*.cu): every GEMM input
+    and output, q (after its scale * log2 e), the K/V cache, the attention
+    probabilities, the attention and GDN outputs, silu*up, the final-norm row,
+    and the gated-norm round trip (REF gdn.cu:213); the residual stays full
+    precision. This is the reference engine's own path on the same weights."""
+    ids = np.asarray(ids)
+    T = len(ids)
+    e = engine_numerics
+    eps = cfg["rms_norm_eps"]
+    Hq, Hkv, D = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"]
+    Hk, Hv = cfg["linear_num_key_heads"], cfg["linear_num_value_heads"]
+    rp = cfg.get("rope_parameters") or {}
+    theta = rp.get("rope_theta", cfg.get("rope_theta", 10000.0))
+    rot = int(D * rp.get("partial_rotary_factor", cfg.get("partial_rotary_factor", 0.25)))
+    pos = np.arange(T)
+    x = W["model.embed_tokens.weight"][ids]
+    for i, lt in enumerate(cfg["layer_types"]):
+        p = f"model.layers.{i}."
+        h = _b(rmsnorm(x, 1.0 + W[p + "input_layernorm.weight"], eps), e)
+        if lt == "full_attention":
+            a = p + "self_attn."
+            proj = _b(np.concatenate([h @ W[a + "q_proj.weight"].T, h @ W[a + "k_proj.weight"].T,
+                                      h @ W[a + "v_proj.weight"].T], -1), e)
+            q, gate, k, v = attn_prep(proj, 1.0 + W[a + "q_norm.weight"],
+                                      1.0 + W[a + "k_norm.weight"], pos, Hq, Hkv, rot, theta, eps, D)
+            if e:
+                qs = _b(q * (D ** -0.5 * LOG2E), True)
+                o = causal_gqa_attention(qs, gate, _b(k, True), v, scale=np.log(2.0), bf16_p=True)
+            else:
+                o = causal_gqa_attention(q, gate, k, v, scale=D ** -0.5)
+            o = _b(o.reshape(T, Hq * D), e)
+            x = x + _b(o @ W[a + "o_proj.weight"].T, e)
+        else:
+            g_ = p + "linear_attn."
+            xq = _b(h @ W[g_ + "in_proj_qkv.weight"].T, e)
+            z = _b(h @ W[g_ + "in_proj_z.weight"].T, e)
+            b = _b(h @ W[g_ + "in_proj_b.weight"].T, e)
+            aa = _b(h @ W[g_ + "in_proj_a.weight"].T, e)
+            xc = gdn_conv(xq, W[g_ + "conv1d.weight"].reshape(-1, 4))
+            q, k, v, g, beta = gdn_prep(xc, b, aa, W[g_ + "A_log"], W[g_ + "dt_bias"], Hk, Hv)
+            if chunked:
+                o, _ = gdn_chunked(q, k, v, g, beta)
+            else:
+                o, _ = gdn_recurrent(q, k, v, g, beta)
+            y = gated_rmsnorm(o, z.reshape(T, Hv, -1), W[g_ + "norm.weight"], eps,
+                              bf16_roundtrip=e)
+            y = _b(y.reshape(T, -1), e)
+            x = x + _b(y @ W[g_ + "out_proj.weight"].T, e)
+        m = p + "mlp."
+        h = _b(rmsnorm(x, 1.0 + W[p + "post_attention_layernorm.weight"], eps), e)
+        gu_g = _b(h @ W[m + "gate_proj.weight"].T, e)
+        gu_u = _b(h @ W[m + "up_proj.weight"].T, e)
+        act = _b(silu(gu_g) * gu_u, e)
+        x = x + _b(act @ W[m + "down_proj.weight"].T, e)
+    hl = _b(rmsnorm(x[-1], 1.0 + W["model.norm.weight"], eps), e)
+    head = W["lm_head.weight"] if "lm_head.weight" in W else W["model.embed_tokens.weight"]
+    return head @ hl
