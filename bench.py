@@ -165,7 +165,7 @@ def gdn_roofline(iters=20):
     S_out = torch.empty(Hv, 128, 128, device=dev)
     y = torch.empty(T, Hv * 128, dtype=torch.bfloat16, device=dev)
     tok0, clen, seg0, segn = (torch.as_tensor(a).to(dev) for a in ops.chunk_table([T]))
-    scratch = torch.empty(ops.gdn_scratch_bytes(len(tok0), Hv), dtype=torch.uint8, device=dev)
+    scratch = torch.empty(ops.gdn_scratch_bytes(len(tok0), Hv, T), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
 
     def launch():

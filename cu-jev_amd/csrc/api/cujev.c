@@ -80,8 +80,7 @@ API cujev_status cujev_model_open(const char *dir, const cujev_options *opts, cu
                         : m->opts.max_branch_tokens;
     m->state_stride = cujev_kv_stride(m->opts.max_state_tokens);
     m->branch_stride = cujev_kv_stride(m->opts.max_branch_tokens);
-    for (int i = 0; i < c->rotary_dim / 2; i++)
-        m->inv_freq[i] = (float)(1.0 / pow(c->rope_theta, 2.0 * i / c->rotary_dim));
+    m->rope_positions = m->opts.max_state_tokens + m->opts.max_branch_tokens;
 
     hipError_t e = hipSetDevice(m->opts.device);
     if (e != hipSuccess) {

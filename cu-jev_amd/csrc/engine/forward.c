@@ -122,7 +122,7 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
                 kstride = m->branch_stride;
             }
             K_TRY(k_attn_prep(m->proj, m->w_attn, ly->q_norm, ly->k_norm, d + o_pos, N, m->Hq,
-                              m->Hkv, c->rotary_dim, m->inv_freq, eps, q_scale, m->q, kdst, vdst,
+                              m->Hkv, c->rotary_dim, m->rope, eps, q_scale, m->q, kdst, vdst,
                               kstride, s),
                   "attn_prep", l);
             K_TRY(k_attention(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l], st->kv_vt[l],
@@ -143,7 +143,7 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
             float *S_out = mode == CUJEV_FWD_PREFILL ? st->S[l] : NULL;
             K_TRY(k_gdn_scan(m->gq, m->gk, m->gv, m->gg, m->gbeta, &chunks, S_in, S_out,
                              m->proj + m->C, m->w_gdn, ly->g_norm, eps, m->Hk, m->Hv, m->mix_out,
-                             &gws, s),
+                             &gws, N, s),
                   "gdn_scan", l);
             K_TRY(k_gemm(m->gemm, m->mix_out, ly->w_out, m->y, 0, N, H, m->V, s), "gemm out", l);
         }

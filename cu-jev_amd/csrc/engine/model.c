@@ -291,13 +291,14 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
         {(void **)&m->gv, N * (size_t)m->Hv * 128 * 2},
         {(void **)&m->gg, N * (size_t)m->Hv * 4},
         {(void **)&m->gbeta, N * (size_t)m->Hv * 4},
-        {(void **)&m->gdn_scratch, cujev_gdn_scratch_bytes(m->max_chunks, m->Hv)},
+        {(void **)&m->gdn_scratch, cujev_gdn_scratch_bytes(m->max_chunks, m->Hv, m->max_tokens)},
         {(void **)&m->act, N * I * 2},
         {(void **)&m->hsel, B * H * 2},
         {(void **)&m->full_logits, B * (size_t)c->vocab_size * 4},
         {(void **)&m->gemm_ws, m->gemm_ws_bytes},
         {(void **)&m->d_meta, m->meta_ints * 4},
         {(void **)&m->d_logits, B * (size_t)(m->opts.max_candidates > 0 ? m->opts.max_candidates : 1) * 4},
+        {(void **)&m->rope, (size_t)m->rope_positions * c->rotary_dim * 4},
     };
     const int np = (int)(sizeof parts / sizeof parts[0]);
     size_t total = 0;
@@ -314,6 +315,17 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
     HIP_TRY(hipMemset(m->br_k, 0, br_kv));
     HIP_TRY(hipMemset(m->br_vt, 0, br_kv));
     HIP_TRY(hipHostMalloc((void **)&m->h_meta, m->meta_ints * 4, hipHostMallocDefault));
+    {
+        const size_t rb = (size_t)m->rope_positions * c->rotary_dim * 4;
+        float *h = (float *)malloc(rb);
+        if (!h)
+            return cujev_fail(CUJEV_ERR_OOM, "RoPE table");
+        cujev_rope_table_host(c->rope_theta, c->rotary_dim, m->rope_positions, h);
+        hipError_t e = hipMemcpy(m->rope, h, rb, hipMemcpyHostToDevice);
+        free(h);
+        if (e != hipSuccess)
+            return cujev_fail(CUJEV_ERR_CUDA, "RoPE table upload: %s", hipGetErrorString(e));
+    }
     cujev_log(m->opts.verbose, "workspace: %.2f GiB for %zu tokens, %zu branches",
               m->work.used / 1073741824.0, N, B);
     return CUJEV_OK;

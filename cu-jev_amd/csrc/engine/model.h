@@ -47,7 +47,6 @@ struct cujev_model {
     hipStream_t stream;
     hipEvent_t ev0, ev1;
     cujev_timing timing;
-    float inv_freq[32]; /* RoPE 1/theta^(2i/rot), computed in double */
 
     bf16_t *embed;     /* [V, H] */
     bf16_t *lm_head;   /* [V, H]; == embed when tied */
@@ -82,6 +81,8 @@ struct cujev_model {
     int32_t *d_meta, *h_meta; /* h_meta is pinned host memory */
     size_t meta_ints;
     float *d_logits; /* [B, max_candidates] */
+    float *rope;     /* [max positions][rot/2] (cos, sin) */
+    int rope_positions;
 };
 
 struct cujev_state {

@@ -267,32 +267,37 @@ __global__ __launch_bounds__(256 * TG) void attention_kernel(
 }
 
 /* ---- prep: norm + RoPE + scale for q, norm + RoPE for k, V transposed ----
- * Workgroup = 64 consecutive tokens x one kv-group (4 q-heads, its k and v
- * head); 256 threads. A wave normalises one 256-wide head row at a time, lane
- * l holding dims 4l..4l+3; RoPE pairs dim i with i + rot/2, i.e. lane l with
- * lane l ^ (rot/8). */
-struct InvFreq {
-    float v[32];
-};
+ * Workgroup = 16 consecutive tokens x one kv-group: waves 0-3 the 4 q-heads,
+ * wave 4 the k-head, all five waves the V transpose. A wave normalises one
+ * 256-wide row per step, lane l holding dims 4l..4l+3; RoPE pairs dim i with
+ * i + rot/2, i.e. lane l with lane l ^ (rot/8). cos/sin come from a table
+ * rope[pos][rot/2] of (cos, sin) pairs built once on the host. */
+constexpr int PREP_TOK = 16;
 
-__global__ __launch_bounds__(256) void attn_prep_kernel(
+__global__ __launch_bounds__(320) void attn_prep_kernel(
     const bf16 *__restrict__ proj, int ps, const float *__restrict__ qw, const float *__restrict__ kw,
-    const int32_t *__restrict__ pos, int N, int Hq, int Hkv, int rot, InvFreq inv_freq, float eps,
-    float q_scale, bf16 *__restrict__ q_out, bf16 *__restrict__ kc, bf16 *__restrict__ vtc, int cs) {
-    __shared__ bf16 vs[256][64 + 8]; /* V^T staging [d][token] */
-    const int n0 = blockIdx.x * 64, kh = blockIdx.y;
+    const int32_t *__restrict__ pos, int N, int Hq, int Hkv, int rot,
+    const float2 *__restrict__ rope, float eps, float q_scale, bf16 *__restrict__ q_out,
+    bf16 *__restrict__ kc, bf16 *__restrict__ vtc, int cs) {
+    __shared__ bf16 vs[256][PREP_TOK + 8]; /* V^T staging [d][token] */
+    const int n0 = blockIdx.x * PREP_TOK, kh = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nt = min(64, N - n0);
+    const int nt = min(PREP_TOK, N - n0);
     const int half_lanes = rot / 8; /* lanes holding the first rot/2 dims */
+    const int hr = rot / 2;
 
-    /* rows: 64 tokens x 5 heads (4 q-heads then the k-head) */
-    for (int rr = wave; rr < 64 * 5; rr += 4) {
-        const int t = rr / 5, which = rr % 5;
-        if (t >= nt)
-            continue;
+    const float *w = wave < 4 ? qw : kw;
+    float wl[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        wl[e] = w[4 * lane + e];
+    const bool rotates = lane < 2 * half_lanes;
+    const bool first = lane < half_lanes;
+    const int fi0 = first ? 4 * lane : 4 * lane - hr;
+    for (int t = 0; t < nt; t++) {
         const int nn = n0 + t;
-        const bf16 *src = which < 4 ? proj + (size_t)nn * ps + (kh * 4 + which) * 512
-                                    : proj + (size_t)nn * ps + Hq * 512 + kh * 256;
+        const bf16 *src = wave < 4 ? proj + (size_t)nn * ps + (kh * 4 + wave) * 512
+                                   : proj + (size_t)nn * ps + Hq * 512 + kh * 256;
         bf16x4 raw = *(const bf16x4 *)(src + 4 * lane);
         float x[4];
         float ss = 0.f;
@@ -303,32 +308,27 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
         }
         ss = wave_sum(ss);
         const float rinv = rsqrtf(ss * (1.f / 256.f) + eps);
-        const float *w = which < 4 ? qw : kw;
 #pragma unroll
         for (int e = 0; e < 4; e++)
-            x[e] = x[e] * rinv * w[4 * lane + e];
+            x[e] = x[e] * rinv * wl[e];
         float partner[4];
 #pragma unroll
         for (int e = 0; e < 4; e++)
             partner[e] = __shfl_xor(x[e], half_lanes, 64);
-        if (lane < 2 * half_lanes) {
-            const bool first = lane < half_lanes;
-            const float p = (float)pos[nn];
+        if (rotates) {
+            const float2 *cs_row = rope + (size_t)pos[nn] * hr + fi0;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int d = 4 * lane + e;
-                const int fi = first ? d : d - rot / 2;
-                float sn, cs_;
-                sincosf(p * inv_freq.v[fi], &sn, &cs_);
-                x[e] = first ? x[e] * cs_ - partner[e] * sn : x[e] * cs_ + partner[e] * sn;
+                const float2 c = cs_row[e];
+                x[e] = first ? x[e] * c.x - partner[e] * c.y : x[e] * c.x + partner[e] * c.y;
             }
         }
         bf16x4 o;
-        if (which < 4) {
+        if (wave < 4) {
 #pragma unroll
             for (int e = 0; e < 4; e++)
                 o[e] = f2bf(x[e] * q_scale);
-            *(bf16x4 *)(q_out + ((size_t)nn * Hq + kh * 4 + which) * 256 + 4 * lane) = o;
+            *(bf16x4 *)(q_out + ((size_t)nn * Hq + kh * 4 + wave) * 256 + 4 * lane) = o;
         } else {
 #pragma unroll
             for (int e = 0; e < 4; e++)
@@ -337,8 +337,8 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
         }
     }
 
-    /* V: [64 tokens][256] -> LDS [256][64] -> vt cache rows of 64 columns */
-    for (int idx = threadIdx.x; idx < 64 * 32; idx += 256) {
+    /* V: [16 tokens][256] -> LDS [256][16] -> 256 vt rows of 16 columns */
+    for (int idx = threadIdx.x; idx < PREP_TOK * 32; idx += 320) {
         const int t = idx >> 5, c = idx & 31;
         if (t < nt) {
             bf16x8 v = *(const bf16x8 *)(proj + (size_t)(n0 + t) * ps + Hq * 512 + Hkv * 256 +
@@ -349,8 +349,8 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
         }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < 256 * 8; idx += 256) {
-        const int d = idx >> 3, c = idx & 7;
+    for (int idx = threadIdx.x; idx < 256 * 2; idx += 320) {
+        const int d = idx >> 1, c = idx & 1;
         bf16 *dst = vtc + ((size_t)kh * 256 + d) * cs + n0 + 8 * c;
         if (8 * c + 8 <= nt) {
             *(bf16x8 *)dst = *(const bf16x8 *)&vs[d][8 * c];
@@ -367,20 +367,18 @@ using namespace CUJEV_KNS;
 
 extern "C" hipError_t k_attn_prep(const bf16_t *proj, int proj_stride, const float *q_norm_w,
                                   const float *k_norm_w, const int32_t *pos, int N, int Hq, int Hkv,
-                                  int rot, const float *inv_freq_host, float eps, float q_scale,
+                                  int rot, const float *rope_table, float eps, float q_scale,
                                   bf16_t *q_out, bf16_t *k_cache, bf16_t *vt_cache, int cache_stride,
                                   hipStream_t stream) {
     if (N <= 0)
         return hipSuccess;
     if (Hq != 4 * Hkv || rot > 64 || rot % 8 != 0)
         return hipErrorInvalidValue;
-    InvFreq f{};
-    for (int i = 0; i < rot / 2; i++)
-        f.v[i] = inv_freq_host[i];
-    dim3 grid((unsigned)CEIL_DIV(N, 64), (unsigned)Hkv);
-    hipLaunchKernelGGL(attn_prep_kernel, grid, dim3(256), 0, stream, (const bf16 *)proj,
-                       proj_stride, q_norm_w, k_norm_w, pos, N, Hq, Hkv, rot, f, eps, q_scale,
-                       (bf16 *)q_out, (bf16 *)k_cache, (bf16 *)vt_cache, cache_stride);
+    dim3 grid((unsigned)CEIL_DIV(N, PREP_TOK), (unsigned)Hkv);
+    hipLaunchKernelGGL(attn_prep_kernel, grid, dim3(320), 0, stream, (const bf16 *)proj,
+                       proj_stride, q_norm_w, k_norm_w, pos, N, Hq, Hkv, rot,
+                       (const float2 *)rope_table, eps, q_scale, (bf16 *)q_out, (bf16 *)k_cache,
+                       (bf16 *)vt_cache, cache_stride);
     return hipGetLastError();
 }
 

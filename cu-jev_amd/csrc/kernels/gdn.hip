@@ -126,34 +126,45 @@ __global__ void gdn_conv_tail_kernel(const bf16 *__restrict__ proj, int ps,
 }
 
 /* ---------------------------------------------------------------------- */
-/* phase A: intra-chunk WY/UT factors                                       */
+/* phase A: intra-chunk WY/UT factors, written in phase B's operand layouts */
 /* ---------------------------------------------------------------------- */
+/* Phase B feeds S and V' (accumulators) back into MFMAs as B operands. An
+ * accumulator supplies the k values of a 16-wide step in the order
+ * 4h+0..3, 8+4h+0..3 (lane half h), so every A operand phase B reads is stored
+ * with bits 2 and 3 of its column index swapped inside each 16-column group:
+ * the 8 consecutive stored values at 16ks + 8h are then exactly the matching
+ * original columns and one 16-byte read fetches them. */
+DEV int swap23(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
+
 struct __attribute__((aligned(16))) ChunkA_Smem {
-    bf16 K[CH][DK + 8];    /* k rows                       */
-    bf16 Q[CH][DK + 8];    /* q rows                       */
-    bf16 Kt[DK][CH + 8];   /* (beta e^G k)^T               */
-    bf16 Vt[DV][CH + 8];   /* (beta v)^T                   */
-    float A[CH][CH + 1];   /* strictly lower A             */
-    float T[CH][CH + 1];   /* (I + A)^-1                   */
-    float M[3][16][17];    /* block products               */
+    bf16 K[CH][DK + 8];  /* k rows                                          */
+    bf16 Q[CH][DK + 8];  /* q rows                                          */
+    bf16 Kt[DK][CH + 8]; /* (beta e^G k)^T, later (k e^{Glast-G})^T swapped */
+    bf16 Vt[DV][CH + 8]; /* (beta v)^T                                      */
+    float A[CH][CH + 1]; /* strictly lower A                                */
+    float T[CH][CH + 1]; /* (I + A)^-1                                      */
+    float M[3][16][17];  /* block products                                  */
     float G[CH], B[CH];
 };
 
 DEV bf16x8 ld8(const bf16 *p) { return *(const bf16x8 *)p; }
+DEV void st4(bf16 *p, bf16 a, bf16 b, bf16 c, bf16 d) { *(bf16x4 *)p = bf16x4{a, b, c, d}; }
 
 __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
     const bf16 *__restrict__ qh, const bf16 *__restrict__ kh_, const bf16 *__restrict__ vh,
     const float *__restrict__ g, const float *__restrict__ beta,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len, int Hk, int Hv,
-    bf16 *__restrict__ Wo, bf16 *__restrict__ Uo, bf16 *__restrict__ QKo, float *__restrict__ Go) {
+    bf16 *__restrict__ Wo, bf16 *__restrict__ Qgo, bf16 *__restrict__ QKo,
+    bf16 *__restrict__ KgTo, bf16 *__restrict__ Uo, float *__restrict__ Glo) {
     __shared__ ChunkA_Smem sm;
     const int ch = blockIdx.x, hv = blockIdx.y;
     const int hk = hv / (Hv / Hk);
     const int t0 = chunk_tok0[ch], L = chunk_len[ch];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, col = lane & 31;
+    const size_t cb = (size_t)ch * Hv + hv;
 
-    /* gates and cumulative log-decay */
+    /* gates and cumulative log-decay (zero past L, so G stays at G[L-1]) */
     if (wave == 0) {
         float gv = lane < L ? g[(size_t)(t0 + lane) * Hv + hv] : 0.f;
         const float bv = lane < L ? beta[(size_t)(t0 + lane) * Hv + hv] : 0.f;
@@ -166,7 +177,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
         sm.G[lane] = gv;
         sm.B[lane] = bv;
     }
-    /* q, k rows (zero past L) */
     for (int i = tid; i < CH * (DK / 8); i += 256) {
         const int t = i / (DK / 8), c8 = (i % (DK / 8)) * 8;
         bf16x8 kv = {}, qv = {};
@@ -178,19 +188,27 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
         *(bf16x8 *)&sm.Q[t][c8] = qv;
     }
     __syncthreads();
-    /* scaled, transposed k and v */
+    const float Glast = sm.G[CH - 1];
+    /* (beta e^G k)^T, (beta v)^T into LDS; q e^G straight to HBM */
     for (int i = tid; i < CH * (DK / 8); i += 256) {
         const int t = i / (DK / 8), c8 = (i % (DK / 8)) * 8;
-        const float sk = sm.B[t] * fast_exp(sm.G[t]), sv = sm.B[t];
+        const float eg = fast_exp(sm.G[t]);
+        const float sk = sm.B[t] * eg, sv = sm.B[t];
         bf16x8 kv = *(const bf16x8 *)&sm.K[t][c8];
+        bf16x8 qv = *(const bf16x8 *)&sm.Q[t][c8];
         bf16x8 vv = {};
         if (t < L)
             vv = ld8(vh + ((size_t)(t0 + t) * Hv + hv) * DV + c8);
+        bf16x8 qg;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             sm.Kt[c8 + e][t] = f2bf(bf2f(kv[e]) * sk);
             sm.Vt[c8 + e][t] = f2bf(bf2f(vv[e]) * sv);
+            qg[e] = f2bf(bf2f(qv[e]) * eg);
         }
+        bf16 *qrow = Qgo + cb * CH * DK + t * DK;
+        st4(qrow + swap23(c8), qg[0], qg[1], qg[2], qg[3]);
+        st4(qrow + swap23(c8 + 4), qg[4], qg[5], qg[6], qg[7]);
     }
 
     /* K K^T and Q K^T: wave w owns the 32x32 tile (w>>1, w&1) of both */
@@ -208,13 +226,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
         }
         const int j = 32 * tj + col;
         const float Gj = sm.G[j];
-        bf16 *qko = QKo + ((size_t)ch * Hv + hv) * CH * CH;
+        bf16 *qko = QKo + cb * CH * CH + swap23(j);
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int i = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
             const float dec = i >= j ? fast_exp(sm.G[i] - Gj) : 0.f;
             sm.A[i][j] = i > j ? sm.B[i] * kk[r] * dec : 0.f;
-            qko[i * CH + j] = f2bf(i >= j ? qk[r] * dec : 0.f);
+            qko[i * CH] = f2bf(i >= j ? qk[r] * dec : 0.f);
         }
     }
     __syncthreads();
@@ -262,7 +280,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
             sm.T[16 * bi + r][16 * bj + c] = -acc;
         }
     }
-    /* zero the strictly upper part */
     for (int e = tid; e < CH * CH; e += 256) {
         const int i = e >> 6, j = e & 63;
         if ((j >> 4) > (i >> 4))
@@ -270,8 +287,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
     }
     __syncthreads();
 
-    /* W = T (beta e^G K), U = T (beta V): wave w owns rows 32(w>>1).., and
-     * columns 64(w&1)..+64 of both */
+    /* W = T (beta e^G K), U = T (beta V): wave w owns rows 32(w>>1).. and
+     * columns 64(w&1)..+64 of both. W goes out row-major with swapped
+     * columns; U goes out in accumulator-fragment order, i.e. exactly the 16
+     * values lane l of phase B's wave (column block) needs, contiguous. */
     {
         const int mi = wave >> 1, nh = wave & 1;
         floatx16 w[2] = {}, u[2] = {};
@@ -291,42 +310,79 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
                 u[nj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bv, u[nj], 0, 0, 0);
             }
         }
-        bf16 *wo = Wo + ((size_t)ch * Hv + hv) * CH * DK;
-        bf16 *uo = Uo + ((size_t)ch * Hv + hv) * CH * DV;
+        bf16 *wo = Wo + cb * CH * DK;
 #pragma unroll
         for (int nj = 0; nj < 2; nj++) {
-            const int c = 64 * nh + 32 * nj + col;
+            const int c = swap23(64 * nh + 32 * nj + col);
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int i = 32 * mi + 8 * (r >> 2) + 4 * h + (r & 3);
                 wo[i * DK + c] = f2bf(w[nj][r]);
-                uo[i * DV + c] = f2bf(u[nj][r]);
             }
+            const int wblk = 2 * nh + nj; /* phase B's wave owning these 32 columns */
+            bf16 *uo = Uo + (((cb * 4 + wblk) * 2 + mi) * 64 + lane) * 16;
+            bf16x8 lo, hi;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                lo[e] = f2bf(u[nj][e]);
+                hi[e] = f2bf(u[nj][8 + e]);
+            }
+            *(bf16x8 *)uo = lo;
+            *(bf16x8 *)(uo + 8) = hi;
         }
     }
-    if (tid < CH)
-        Go[((size_t)ch * Hv + hv) * CH + tid] = sm.G[tid];
+    __syncthreads(); /* everyone is done with Kt */
+    /* (k e^{Glast - G})^T with swapped token columns, then rows to HBM */
+    for (int i = tid; i < CH * (DK / 8); i += 256) {
+        const int t = i / (DK / 8), c8 = (i % (DK / 8)) * 8;
+        const float ek = fast_exp(Glast - sm.G[t]);
+        bf16x8 kv = *(const bf16x8 *)&sm.K[t][c8];
+        const int ts = swap23(t);
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            sm.Kt[c8 + e][ts] = f2bf(bf2f(kv[e]) * ek);
+    }
+    __syncthreads();
+    for (int i = tid; i < DK * (CH / 8); i += 256) {
+        const int r = i >> 3, c8 = (i & 7) * 8;
+        *(bf16x8 *)(KgTo + cb * DK * CH + r * CH + c8) = *(const bf16x8 *)&sm.Kt[r][c8];
+    }
+    if (tid == 0)
+        Glo[cb] = Glast;
 }
 
 /* ---------------------------------------------------------------------- */
-/* phase B: state recurrence over chunks + gated RMSNorm                    */
+/* phase B: the state recurrence over chunks                                */
 /* ---------------------------------------------------------------------- */
-struct __attribute__((aligned(16))) ChunkB_Smem {
-    bf16 W[CH][DK + 8];
-    bf16 Qg[CH][DK + 8];  /* q e^G               */
-    bf16 QK[CH][CH + 8];
-    bf16 KgT[DK][CH + 8]; /* (k e^{G_last-G})^T  */
-    float O[CH][DV + 4];
-    float G[CH];
-};
+/* One LDS stage holds the shared A operands of one chunk, 16-byte chunks
+ * XOR-swizzled per row for conflict-free ds_read_b128:
+ *   W   [64][128]  at 0        Qg [64][128] at 16 KiB
+ *   QK  [64][64]   at 32 KiB   KgT [128][64] at 40 KiB        (56 KiB) */
+constexpr int B_W = 0, B_QG = 16384, B_QK = 32768, B_KGT = 40960, B_BUF = 57344;
+constexpr int B_CHUNKS = B_BUF / 16;     /* 3584 */
+constexpr int B_PER = B_CHUNKS / 256;    /* 14 per thread */
 
-/* A operand of a product whose B operand is an accumulator reused as B:
- * k values 4h..4h+3 and 8+4h..8+4h+3 of the 16-wide step at `p`. */
-DEV bf16x8 ld_perm(const bf16 *p, int h) {
-    bf16x4 lo = *(const bf16x4 *)(p + 4 * h), hi = *(const bf16x4 *)(p + 8 + 4 * h);
-    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+DEV int swz16(int r) { return r & 15; }
+DEV int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+/* global source and LDS offset of 16-byte chunk f of one stage */
+DEV void stage_addr(int f, const bf16 *W, const bf16 *Qg, const bf16 *QK, const bf16 *KgT,
+                    const bf16 *&src, int &dst) {
+    if (f < 2048) {
+        const int g = f & 1023, row = g >> 4, c = g & 15;
+        src = (f < 1024 ? W : Qg) + row * DK + c * 8;
+        dst = (f < 1024 ? B_W : B_QG) + row * 256 + ((c ^ swz16(row)) << 4);
+    } else if (f < 2560) {
+        const int g = f - 2048, row = g >> 3, c = g & 7;
+        src = QK + row * CH + c * 8;
+        dst = B_QK + row * 128 + ((c ^ swz8(row)) << 4);
+    } else {
+        const int g = f - 2560, row = g >> 3, c = g & 7;
+        src = KgT + row * CH + c * 8;
+        dst = B_KGT + row * 128 + ((c ^ swz8(row)) << 4);
+    }
 }
-/* accumulator registers 8s..8s+7 as a bf16 B operand */
+
 DEV bf16x8 acc_as_b(const floatx16 &c, int s) {
     bf16x8 b;
 #pragma unroll
@@ -336,20 +392,18 @@ DEV bf16x8 acc_as_b(const floatx16 &c, int s) {
 }
 
 __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
-    const bf16 *__restrict__ qh, const bf16 *__restrict__ kh_, const bf16 *__restrict__ Wi,
-    const bf16 *__restrict__ Ui, const bf16 *__restrict__ QKi, const float *__restrict__ Gi,
+    const bf16 *__restrict__ Wi, const bf16 *__restrict__ Qgi, const bf16 *__restrict__ QKi,
+    const bf16 *__restrict__ KgTi, const bf16 *__restrict__ Ui, const float *__restrict__ Gli,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
     const int32_t *__restrict__ seg_chunk0, const int32_t *__restrict__ seg_nchunk,
-    const float *__restrict__ S_in, float *__restrict__ S_out, const bf16 *__restrict__ z, int zs,
-    const float *__restrict__ norm_w, float eps, int Hk, int Hv, bf16 *__restrict__ y) {
-    __shared__ ChunkB_Smem sm;
+    const float *__restrict__ S_in, float *__restrict__ S_out, int Hv, float *__restrict__ o) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * B_BUF];
     const int seg = blockIdx.x, hv = blockIdx.y;
-    const int hk = hv / (Hv / Hk);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, col = lane & 31;
     const int dv = 32 * wave + col; /* this lane's state column */
 
-    floatx16 S[4]; /* S[:, dv] rows 32ti + 8(r/4) + 4h + r%4 */
+    floatx16 S[4]; /* S[:, dv], rows 32ti + 8(r/4) + 4h + r%4 */
 #pragma unroll
     for (int ti = 0; ti < 4; ti++) {
 #pragma unroll
@@ -358,60 +412,74 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
             S[ti][r] = S_in ? S_in[((size_t)hv * DK + dk) * DV + dv] : 0.f;
         }
     }
-
     const int c0 = seg_chunk0[seg], nc = seg_nchunk[seg];
+
+    u32x4 stage[B_PER];
+    bf16x8 ucur[4], unext[4];
+    auto fetch = [&](int ch) {
+        const size_t cb = (size_t)ch * Hv + hv;
+        const bf16 *W = Wi + cb * CH * DK, *Qg = Qgi + cb * CH * DK, *QK = QKi + cb * CH * CH,
+                   *KgT = KgTi + cb * DK * CH;
+#pragma unroll
+        for (int j = 0; j < B_PER; j++) {
+            const bf16 *src;
+            int dst;
+            stage_addr(tid + 256 * j, W, Qg, QK, KgT, src, dst);
+            stage[j] = *(const u32x4 *)src;
+        }
+        const bf16 *up = Ui + (cb * 4 + wave) * 2 * 64 * 16 + lane * 16;
+        unext[0] = ld8(up);
+        unext[1] = ld8(up + 8);
+        unext[2] = ld8(up + 64 * 16);
+        unext[3] = ld8(up + 64 * 16 + 8);
+    };
+    auto store = [&](unsigned char *buf) {
+#pragma unroll
+        for (int j = 0; j < B_PER; j++) {
+            const bf16 *src;
+            int dst;
+            stage_addr(tid + 256 * j, nullptr, nullptr, nullptr, nullptr, src, dst);
+            *(u32x4 *)(buf + dst) = stage[j];
+        }
+    };
+
+    if (nc > 0) {
+        fetch(c0);
+        store(smem);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            ucur[e] = unext[e];
+        __syncthreads();
+    }
     for (int ci = 0; ci < nc; ci++) {
         const int ch = c0 + ci;
         const int t0 = chunk_tok0[ch], L = chunk_len[ch];
-        const size_t cbase = (size_t)ch * Hv + hv;
-        __syncthreads();
-        if (tid < CH)
-            sm.G[tid] = Gi[cbase * CH + tid];
-        __syncthreads();
-        const float Glast = sm.G[CH - 1];
-        for (int i = tid; i < CH * (DK / 8); i += 256) {
-            const int t = i / (DK / 8), c8 = (i % (DK / 8)) * 8;
-            *(bf16x8 *)&sm.W[t][c8] = ld8(Wi + cbase * CH * DK + t * DK + c8);
-            bf16x8 qv = {}, kv = {};
-            if (t < L) {
-                qv = ld8(qh + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
-                kv = ld8(kh_ + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
-            }
-            const float eq = fast_exp(sm.G[t]), ek = fast_exp(Glast - sm.G[t]);
-            bf16x8 qg;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                qg[e] = f2bf(bf2f(qv[e]) * eq);
-                sm.KgT[c8 + e][t] = f2bf(bf2f(kv[e]) * ek);
-            }
-            *(bf16x8 *)&sm.Qg[t][c8] = qg;
-        }
-        for (int i = tid; i < CH * (CH / 8); i += 256) {
-            const int t = i / (CH / 8), c8 = (i % (CH / 8)) * 8;
-            *(bf16x8 *)&sm.QK[t][c8] = ld8(QKi + cbase * CH * CH + t * CH + c8);
-        }
-        __syncthreads();
+        const float Glast = Gli[(size_t)ch * Hv + hv];
+        const bool more = ci + 1 < nc;
+        if (more)
+            fetch(ch + 1);
+        const unsigned char *buf = smem + (ci & 1) * B_BUF;
 
-        /* S as B operand (8 k-steps over dk) */
         bf16x8 Sb[8];
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
             Sb[ks] = acc_as_b(S[ks >> 1], ks & 1);
 
-        /* V' = U - W S  (tokens x dv) */
+        /* V' = U - W S   (tokens x dv) */
         floatx16 Vn[2];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) {
             floatx16 acc = {};
+            const int r = 32 * mt + col;
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    ld_perm(&sm.W[32 * mt + col][16 * ks], h), Sb[ks], acc, 0, 0, 0);
-            const bf16 *up = Ui + cbase * CH * DV;
+            for (int ks = 0; ks < 8; ks++) {
+                bf16x8 a = *(const bf16x8 *)(buf + B_W + r * 256 + (((2 * ks + h) ^ swz16(r)) << 4));
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Sb[ks], acc, 0, 0, 0);
+            }
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int t = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
-                Vn[mt][r] = bf2f(up[t * DV + dv]) - acc[r];
+            for (int e = 0; e < 8; e++) {
+                Vn[mt][e] = bf2f(ucur[2 * mt][e]) - acc[e];
+                Vn[mt][8 + e] = bf2f(ucur[2 * mt + 1][e]) - acc[8 + e];
             }
         }
         bf16x8 Vb[4];
@@ -419,22 +487,26 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
         for (int ks = 0; ks < 4; ks++)
             Vb[ks] = acc_as_b(Vn[ks >> 1], ks & 1);
 
-        /* O = (Q e^G) S + QKm V' */
+        /* O = (Q e^G) S + QKm V' -> fp32 o[token][hv][dv] */
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) {
             floatx16 acc = {};
+            const int r = 32 * mt + col;
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    ld_perm(&sm.Qg[32 * mt + col][16 * ks], h), Sb[ks], acc, 0, 0, 0);
+            for (int ks = 0; ks < 8; ks++) {
+                bf16x8 a = *(const bf16x8 *)(buf + B_QG + r * 256 + (((2 * ks + h) ^ swz16(r)) << 4));
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Sb[ks], acc, 0, 0, 0);
+            }
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    ld_perm(&sm.QK[32 * mt + col][16 * ks], h), Vb[ks], acc, 0, 0, 0);
+            for (int ks = 0; ks < 4; ks++) {
+                bf16x8 a = *(const bf16x8 *)(buf + B_QK + r * 128 + (((2 * ks + h) ^ swz8(r)) << 4));
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Vb[ks], acc, 0, 0, 0);
+            }
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int t = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
-                sm.O[t][dv] = acc[r];
+            for (int rr = 0; rr < 16; rr++) {
+                const int t = 32 * mt + 8 * (rr >> 2) + 4 * h + (rr & 3);
+                if (t < L)
+                    o[((size_t)(t0 + t) * Hv + hv) * DV + dv] = acc[rr];
             }
         }
 
@@ -443,26 +515,22 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
 #pragma unroll
         for (int ti = 0; ti < 4; ti++) {
             floatx16 acc = S[ti] * dec;
+            const int r = 32 * ti + col;
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    ld_perm(&sm.KgT[32 * ti + col][16 * ks], h), Vb[ks], acc, 0, 0, 0);
+            for (int ks = 0; ks < 4; ks++) {
+                bf16x8 a = *(const bf16x8 *)(buf + B_KGT + r * 128 + (((2 * ks + h) ^ swz8(r)) << 4));
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Vb[ks], acc, 0, 0, 0);
+            }
             S[ti] = acc;
         }
-        __syncthreads();
 
-        /* gated RMSNorm of the chunk's outputs: wave per token row */
-        for (int t = wave; t < L; t += 4) {
-            const float o0 = sm.O[t][2 * lane], o1 = sm.O[t][2 * lane + 1];
-            const float ss = wave_sum(o0 * o0 + o1 * o1);
-            const float inv = rsqrtf(ss * (1.f / DV) + eps);
-            const bf16 *zr = z + (size_t)(t0 + t) * zs + hv * DV + 2 * lane;
-            bf16 *yr = y + ((size_t)(t0 + t) * Hv + hv) * DV + 2 * lane;
-            const float n0 = bf2f(f2bf(o0 * inv)) * norm_w[2 * lane];
-            const float n1 = bf2f(f2bf(o1 * inv)) * norm_w[2 * lane + 1];
-            yr[0] = f2bf(n0 * silu_f(bf2f(zr[0])));
-            yr[1] = f2bf(n1 * silu_f(bf2f(zr[1])));
+        if (more) {
+            store(smem + ((ci + 1) & 1) * B_BUF);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                ucur[e] = unext[e];
         }
+        __syncthreads();
     }
     if (S_out && seg == 0) {
 #pragma unroll
@@ -474,6 +542,29 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
             }
         }
     }
+}
+
+/* y = bf16( w * bf16(o * rsqrt(mean o^2 + eps)) * silu(z) ): one wave per
+ * (token, v-head) row, lane = 2 columns. REF src/kernels/gdn.cu:193-216. */
+__global__ __launch_bounds__(256) void gdn_norm_gate_kernel(const float *__restrict__ o,
+                                                            const bf16 *__restrict__ z, int zs,
+                                                            const float *__restrict__ w, float eps,
+                                                            int rows, int Hv,
+                                                            bf16 *__restrict__ y) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows)
+        return;
+    const int n = row / Hv, hv = row % Hv;
+    const float2 v = *(const float2 *)(o + (size_t)row * DV + 2 * lane);
+    const float ss = wave_sum(v.x * v.x + v.y * v.y);
+    const float inv = rsqrtf(ss * (1.f / DV) + eps);
+    const bf16 *zr = z + (size_t)n * zs + hv * DV + 2 * lane;
+    const float n0 = bf2f(f2bf(v.x * inv)) * w[2 * lane];
+    const float n1 = bf2f(f2bf(v.y * inv)) * w[2 * lane + 1];
+    bf16 *yr = y + (size_t)row * DV + 2 * lane;
+    yr[0] = f2bf(n0 * silu_f(bf2f(zr[0])));
+    yr[1] = f2bf(n1 * silu_f(bf2f(zr[1])));
 }
 
 } // namespace
@@ -507,19 +598,22 @@ extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t 
                                  const float *beta, const cujev_chunks *ck, const float *S_in,
                                  float *S_out, const bf16_t *z, int z_stride, const float *norm_w,
                                  float eps, int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *ws,
-                                 hipStream_t stream) {
-    if (ck->num_chunks <= 0)
+                                 int N, hipStream_t stream) {
+    if (ck->num_chunks <= 0 || N <= 0)
         return hipSuccess;
     if (Hk <= 0 || Hv % Hk != 0)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(gdn_chunk_a_kernel, dim3((unsigned)ck->num_chunks, (unsigned)Hv), dim3(256),
                        0, stream, (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, g, beta,
-                       ck->chunk_tok0, ck->chunk_len, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->U,
-                       (bf16 *)ws->QK, ws->G);
+                       ck->chunk_tok0, ck->chunk_len, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->Qg,
+                       (bf16 *)ws->QK, (bf16 *)ws->KgT, (bf16 *)ws->U, ws->Glast);
     hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)ck->num_segments, (unsigned)Hv),
-                       dim3(256), 0, stream, (const bf16 *)q, (const bf16 *)k,
-                       (const bf16 *)ws->W, (const bf16 *)ws->U, (const bf16 *)ws->QK, ws->G,
+                       dim3(256), 0, stream, (const bf16 *)ws->W, (const bf16 *)ws->Qg,
+                       (const bf16 *)ws->QK, (const bf16 *)ws->KgT, (const bf16 *)ws->U, ws->Glast,
                        ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk, S_in, S_out,
-                       (const bf16 *)z, z_stride, norm_w, eps, Hk, Hv, (bf16 *)y);
+                       Hv, ws->O);
+    const int rows = N * Hv;
+    hipLaunchKernelGGL(gdn_norm_gate_kernel, dim3((unsigned)CEIL_DIV(rows, 4)), dim3(256), 0,
+                       stream, ws->O, (const bf16 *)z, z_stride, norm_w, eps, rows, Hv, (bf16 *)y);
     return hipGetLastError();
 }

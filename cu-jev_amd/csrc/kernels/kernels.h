@@ -23,19 +23,35 @@ typedef uint16_t bf16_t; /* storage type of bfloat16 seen from C */
 #define CUJEV_ATT_KEY_TILE 64
 static inline int cujev_kv_stride(int max_tokens) { return (max_tokens + 63) / 64 * 64 + 64; }
 
+/* RoPE table rope[p][i] = (cos a, sin a), a = fl32(fl32(1/theta^(2i/rot)) * p),
+ * i < rot/2, p < npos: the fp32 angle transformers forms (inv_freq times the
+ * position in fp32), its cos/sin evaluated in double and rounded once.
+ * `out` has npos * rot floats (host memory). */
+#include <math.h>
+static inline void cujev_rope_table_host(double theta, int rot, int npos, float *out) {
+    for (int i = 0; i < rot / 2; i++) {
+        const float f = (float)(1.0 / pow(theta, 2.0 * i / rot));
+        for (int p = 0; p < npos; p++) {
+            const float a = f * (float)p;
+            out[((size_t)p * (rot / 2) + i) * 2] = (float)cos((double)a);
+            out[((size_t)p * (rot / 2) + i) * 2 + 1] = (float)sin((double)a);
+        }
+    }
+}
+
 /* ---- full attention -----------------------------------------------------
  * proj[N, proj_stride] bf16 is the fused projection row
  *   [Hq x (q 256 | gate 256)] [Hkv x K 256] [Hkv x V 256].
  * Per q-head: zero-centred RMSNorm (q_norm_w already holds 1+w), RoPE on the
- * first `rot` dims (rotate_half, angle pos*inv_freq[i]), times q_scale
+ * first `rot` dims (rotate_half with the device table rope_table of
+ * cujev_rope_table_host, indexed by pos[n]), times q_scale
  * (= head_dim^-1/2 * log2 e), rounded to bf16 -> q_out[N][Hq][256].
  * Per kv-head: the same for K -> k_cache[Hkv][cache_stride][256] row n;
  * V copied raw -> vt_cache[Hkv][256][cache_stride] column n (d-major).
- * The cache column of packed token n is n itself. inv_freq has rot/2 floats
- * in host memory. */
+ * The cache column of packed token n is n itself. */
 hipError_t k_attn_prep(const bf16_t *proj, int proj_stride, const float *q_norm_w,
                        const float *k_norm_w, const int32_t *pos, int N, int Hq, int Hkv, int rot,
-                       const float *inv_freq_host, float eps, float q_scale, bf16_t *q_out,
+                       const float *rope_table, float eps, float q_scale, bf16_t *q_out,
                        bf16_t *k_cache, bf16_t *vt_cache, int cache_stride, hipStream_t stream);
 
 /* out[n, h*256 + d] = sigmoid(gate[n*gate_tok_stride + h*gate_head_stride + d])
@@ -75,44 +91,57 @@ typedef struct cujev_chunks {
     int num_segments;
 } cujev_chunks;
 
-/* Per-chunk WY/UT factors, written by the scan's first phase. */
+/* Scratch of the chunked scan. Per (chunk, v-head), written by the parallel
+ * first phase in the operand layouts of the sequential second phase:
+ * W, q e^G, masked QK^T and (k e^{Glast-G})^T as bf16 (columns permuted),
+ * U in accumulator-fragment order, and the chunk's total log-decay. O is the
+ * unnormalised output [N][Hv][128] fp32 before the gated norm. */
 typedef struct cujev_gdn_scratch {
-    void *W;  /* bf16 [num_chunks][Hv][64][128] */
-    void *U;  /* bf16 [num_chunks][Hv][64][128] */
-    void *QK; /* bf16 [num_chunks][Hv][64][64]  */
-    float *G; /* [num_chunks][Hv][64]           */
+    void *W;      /* bf16 [chunks][Hv][64][128]  */
+    void *Qg;     /* bf16 [chunks][Hv][64][128]  */
+    void *QK;     /* bf16 [chunks][Hv][64][64]   */
+    void *KgT;    /* bf16 [chunks][Hv][128][64]  */
+    void *U;      /* bf16 [chunks][Hv][4][2][64][16] */
+    float *Glast; /* [chunks][Hv] */
+    float *O;     /* [N][Hv][128] */
 } cujev_gdn_scratch;
 
 static inline size_t cujev_align256(size_t x) { return (x + 255) / 256 * 256; }
-static inline size_t cujev_gdn_scratch_bytes(int num_chunks, int Hv) {
-    const size_t per = (size_t)num_chunks * Hv * 64;
-    return 2 * cujev_align256(per * 128 * 2) + cujev_align256(per * 64 * 2) +
-           cujev_align256(per * 4);
+static inline size_t cujev_gdn_scratch_bytes(int num_chunks, int Hv, int N) {
+    const size_t ch = (size_t)num_chunks * Hv;
+    return 4 * cujev_align256(ch * 64 * 128 * 2) + cujev_align256(ch * 64 * 64 * 2) +
+           cujev_align256(ch * 4) + cujev_align256((size_t)N * Hv * 128 * 4);
 }
 /* Carve the scratch of cujev_gdn_scratch_bytes() starting at `base`. */
 static inline cujev_gdn_scratch cujev_gdn_scratch_carve(void *base, int num_chunks, int Hv) {
-    const size_t per = (size_t)num_chunks * Hv * 64;
+    const size_t ch = (size_t)num_chunks * Hv;
     char *p = (char *)base;
     cujev_gdn_scratch s;
     s.W = p;
-    p += cujev_align256(per * 128 * 2);
+    p += cujev_align256(ch * 64 * 128 * 2);
+    s.Qg = p;
+    p += cujev_align256(ch * 64 * 128 * 2);
+    s.KgT = p;
+    p += cujev_align256(ch * 64 * 128 * 2);
     s.U = p;
-    p += cujev_align256(per * 128 * 2);
+    p += cujev_align256(ch * 64 * 128 * 2);
     s.QK = p;
-    p += cujev_align256(per * 64 * 2);
-    s.G = (float *)p;
+    p += cujev_align256(ch * 64 * 64 * 2);
+    s.Glast = (float *)p;
+    p += cujev_align256(ch * 4);
+    s.O = (float *)p;
     return s;
 }
 
-/* Chunked gated delta rule over every segment, each from S_in[Hv][128][128]
- * (fp32, read-only; NULL = zeros); S_out (may be NULL) receives the final
- * state of segment 0. The output goes straight through the gated RMSNorm:
- * y[n, hv*128 + c] = bf16( bf16(o * rsqrt(mean o^2 + eps)) * norm_w[c]
- *                          * silu(z[n*z_stride + hv*128 + c]) ). */
+/* Chunked gated delta rule over every segment (N packed tokens), each from
+ * S_in[Hv][128][128] (fp32, read-only; NULL = zeros); S_out (may be NULL)
+ * receives the final state of segment 0. The output goes through the gated
+ * RMSNorm: y[n, hv*128 + c] = bf16( bf16(o * rsqrt(mean o^2 + eps))
+ *                                   * norm_w[c] * silu(z[n*z_stride + hv*128 + c]) ). */
 hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const float *g,
                       const float *beta, const cujev_chunks *chunks, const float *S_in,
                       float *S_out, const bf16_t *z, int z_stride, const float *norm_w, float eps,
-                      int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *scratch,
+                      int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *scratch, int N,
                       hipStream_t stream);
 
 /* ---- per-layer glue --------------------------------------------------------

@@ -5,6 +5,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #define EXPORT extern "C" __attribute__((visibility("default")))
 
@@ -30,18 +31,30 @@ static int launched(hipError_t e, const char *what) {
 EXPORT int cujev_ops_kv_stride(int max_tokens) { return cujev_kv_stride(max_tokens); }
 EXPORT const char *cujev_ops_last_error(void) { return g_err; }
 
+EXPORT int cujev_op_rope_table(double theta, int rot, int npos, float *table) {
+    if (rot <= 0 || rot > 64 || rot % 8 || npos <= 0 || !table)
+        return fail(1, "rope_table: bad arguments");
+    const size_t bytes = (size_t)npos * rot * 4;
+    float *h = (float *)malloc(bytes);
+    if (!h)
+        return fail(5, "rope_table: host buffer");
+    cujev_rope_table_host(theta, rot, npos, h);
+    hipError_t e = hipMemcpy(table, h, bytes, hipMemcpyHostToDevice);
+    free(h);
+    return launched(e, "rope_table");
+}
+
 EXPORT int cujev_op_attn_prep(const void *proj, int proj_stride, const float *q_norm_w,
                               const float *k_norm_w, const int32_t *pos, int N, int Hq, int Hkv,
-                              int rot, double theta, float eps, float q_scale, void *q_out,
-                              void *k_cache, void *vt_cache, int cache_stride, void *stream) {
-    if (N < 0 || Hkv <= 0 || rot <= 0 || rot > 64 || cache_stride % 64)
+                              int rot, const float *rope_table, float eps, float q_scale,
+                              void *q_out, void *k_cache, void *vt_cache, int cache_stride,
+                              void *stream) {
+    if (N < 0 || Hkv <= 0 || rot <= 0 || rot > 64 || cache_stride % 64 || !rope_table)
         return fail(1, "attn_prep: bad arguments");
-    float inv[32];
-    for (int i = 0; i < rot / 2; i++)
-        inv[i] = (float)(1.0 / pow(theta, 2.0 * i / rot));
     return launched(k_attn_prep((const bf16_t *)proj, proj_stride, q_norm_w, k_norm_w, pos, N, Hq,
-                                Hkv, rot, inv, eps, q_scale, (bf16_t *)q_out, (bf16_t *)k_cache,
-                                (bf16_t *)vt_cache, cache_stride, (hipStream_t)stream),
+                                Hkv, rot, rope_table, eps, q_scale, (bf16_t *)q_out,
+                                (bf16_t *)k_cache, (bf16_t *)vt_cache, cache_stride,
+                                (hipStream_t)stream),
                     "attn_prep");
 }
 
@@ -73,8 +86,8 @@ EXPORT int cujev_op_gdn_conv_prep(const void *proj, int proj_stride, const float
                     "gdn_conv_prep");
 }
 
-EXPORT size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv) {
-    return cujev_gdn_scratch_bytes(num_chunks, Hv);
+EXPORT size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv, int N) {
+    return cujev_gdn_scratch_bytes(num_chunks, Hv, N);
 }
 
 EXPORT int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const float *g,
@@ -82,13 +95,14 @@ EXPORT int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const 
                              const int32_t *chunk_len, int num_chunks, const int32_t *seg_chunk0,
                              const int32_t *seg_nchunk, int num_segments, const float *S_in,
                              float *S_out, const void *z, int z_stride, const float *norm_w,
-                             float eps, int Hk, int Hv, void *y, void *scratch, void *stream) {
-    if (num_chunks < 0 || num_segments < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk || !scratch)
+                             float eps, int Hk, int Hv, int N, void *y, void *scratch,
+                             void *stream) {
+    if (num_chunks < 0 || num_segments < 0 || N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk || !scratch)
         return fail(1, "gdn_scan: bad arguments");
     cujev_chunks ck = {chunk_tok0, chunk_len, seg_chunk0, seg_nchunk, num_chunks, num_segments};
     cujev_gdn_scratch ws = cujev_gdn_scratch_carve(scratch, num_chunks, Hv);
     return launched(k_gdn_scan((const bf16_t *)q, (const bf16_t *)k, (const bf16_t *)v, g, beta,
                                &ck, S_in, S_out, (const bf16_t *)z, z_stride, norm_w, eps, Hk, Hv,
-                               (bf16_t *)y, &ws, (hipStream_t)stream),
+                               (bf16_t *)y, &ws, N, (hipStream_t)stream),
                     "gdn_scan");
 }

@@ -28,12 +28,13 @@ _D = C.c_double
 
 # name -> argtypes (all return int status)
 _SIGS = {
-    "cujev_op_attn_prep": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _D, _F, _F, _P, _P, _P, _I, _P],
+    "cujev_op_rope_table": [_D, _I, _I, _P],
+    "cujev_op_attn_prep": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _F, _F, _P, _P, _P, _I, _P],
     "cujev_op_attention": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P],
     "cujev_op_gdn_conv_prep": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P,
                                _P, _P],
     "cujev_op_gdn_scan": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _F, _I,
-                          _I, _P, _P, _P],
+                          _I, _I, _P, _P, _P],
 }
 
 
@@ -53,7 +54,7 @@ def load():
     lib.cujev_ops_kv_stride.argtypes = [_I]
     lib.cujev_ops_kv_stride.restype = _I
     lib.cujev_ops_last_error.restype = C.c_char_p
-    lib.cujev_ops_gdn_scratch_bytes.argtypes = [_I, _I]
+    lib.cujev_ops_gdn_scratch_bytes.argtypes = [_I, _I, _I]
     lib.cujev_ops_gdn_scratch_bytes.restype = C.c_size_t
     for name, args in _SIGS.items():
         fn = getattr(lib, name)
@@ -89,11 +90,20 @@ def kv_stride(max_tokens: int) -> int:
     return load().cujev_ops_kv_stride(int(max_tokens))
 
 
-def attn_prep(proj, q_norm_w, k_norm_w, pos, Hq, Hkv, rot, theta, eps, q_scale,
+def rope_table(theta, rot, npos):
+    """Device RoPE table for attn_prep (torch float32 [npos, rot/2, 2])."""
+    import torch
+    t = torch.empty(npos, rot // 2, 2, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    _call("cujev_op_rope_table", float(theta), int(rot), int(npos), _ptr(t))
+    return t
+
+
+def attn_prep(proj, q_norm_w, k_norm_w, pos, Hq, Hkv, rot, rope, eps, q_scale,
               q_out, k_cache, vt_cache, cache_stride):
     N = proj.shape[0]
     _call("cujev_op_attn_prep", _ptr(proj), proj.stride(0), _ptr(q_norm_w), _ptr(k_norm_w),
-          _ptr(pos), N, Hq, Hkv, rot, float(theta), float(eps), float(q_scale), _ptr(q_out),
+          _ptr(pos), N, Hq, Hkv, rot, _ptr(rope), float(eps), float(q_scale), _ptr(q_out),
           _ptr(k_cache), _ptr(vt_cache), cache_stride, _stream())
 
 
@@ -131,8 +141,8 @@ def chunk_table(seg_lens, chunk=64):
     return as_i(tok0), as_i(clen), as_i(seg0), as_i(segn)
 
 
-def gdn_scratch_bytes(num_chunks, Hv):
-    return int(load().cujev_ops_gdn_scratch_bytes(int(num_chunks), int(Hv)))
+def gdn_scratch_bytes(num_chunks, Hv, N):
+    return int(load().cujev_ops_gdn_scratch_bytes(int(num_chunks), int(Hv), int(N)))
 
 
 def gdn_scan(q, k, v, g, beta, chunk_tok0, chunk_len, seg_chunk0, seg_nchunk, S_in, S_out, z,
@@ -140,4 +150,4 @@ def gdn_scan(q, k, v, g, beta, chunk_tok0, chunk_len, seg_chunk0, seg_nchunk, S_
     _call("cujev_op_gdn_scan", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(chunk_tok0),
           _ptr(chunk_len), chunk_tok0.shape[0], _ptr(seg_chunk0), _ptr(seg_nchunk),
           seg_chunk0.shape[0], _ptr(S_in), _ptr(S_out), _ptr(z), int(z_stride), _ptr(norm_w),
-          float(eps), Hk, Hv, _ptr(y), _ptr(scratch), _stream())
+          float(eps), Hk, Hv, q.shape[0], _ptr(y), _ptr(scratch), _stream())

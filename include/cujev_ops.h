@@ -33,13 +33,19 @@ extern "C" {
 int cujev_ops_kv_stride(int max_tokens);
 const char *cujev_ops_last_error(void);
 
+/* Fills the device RoPE table used by cujev_op_attn_prep: table[p][i] =
+ * (cos a, sin a), a = fp32(fp32(theta^(-2i/rot)) * p), p < npos, i < rot/2
+ * (npos * rot floats). Synchronous. Replaces the reference's per-launch
+ * constant-memory inv_freq upload (src/kernels/attention.cu:87-96). */
+int cujev_op_rope_table(double theta, int rot, int npos, float *table);
+
 /* Replaces reference src/kernels/kernels.h:197-199 (k_attn_prep).
- * q_norm_w / k_norm_w: fp32 [256], already 1 + w. pos: int32 [N].
- * Writes q_out bf16 [N][Hq][256] scaled by q_scale (the engine passes
- * 256^-1/2 * log2 e), K rows n and V^T columns n of the caches. */
+ * q_norm_w / k_norm_w: fp32 [256], already 1 + w. pos: int32 [N] (< npos of
+ * the table). Writes q_out bf16 [N][Hq][256] scaled by q_scale (the engine
+ * passes 256^-1/2 * log2 e), K rows n and V^T columns n of the caches. */
 int cujev_op_attn_prep(const void *proj, int proj_stride, const float *q_norm_w,
                        const float *k_norm_w, const int32_t *pos, int N, int Hq, int Hkv,
-                       int rot, double theta, float eps, float q_scale, void *q_out,
+                       int rot, const float *rope_table, float eps, float q_scale, void *q_out,
                        void *k_cache, void *vt_cache, int cache_stride, void *stream);
 
 /* Replaces reference src/kernels/kernels.h:203-206 (k_attention).
@@ -64,8 +70,9 @@ int cujev_op_gdn_conv_prep(const void *proj, int proj_stride, const float *conv_
                            const float *dt_bias, int N, int Hk, int Hv, void *q, void *k,
                            void *v, float *g, float *beta, void *stream);
 
-/* Bytes of device scratch cujev_op_gdn_scan needs for num_chunks chunks. */
-size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv);
+/* Bytes of device scratch cujev_op_gdn_scan needs for num_chunks chunks of
+ * N packed tokens. */
+size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv, int N);
 
 /* Replaces reference src/kernels/kernels.h:228-230 (k_gdn_scan) and :233-234
  * (k_gdn_norm_gate), fused. Chunk table (device int32): chunk_tok0/chunk_len
@@ -73,13 +80,13 @@ size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv);
  * chunks of 64 tokens from its start. S_in fp32 [Hv][128][128] (NULL = 0),
  * S_out (may be NULL) = final state of segment 0. y bf16 [N][Hv*128] is the
  * gated-RMSNorm output; z is read at z[n*z_stride + hv*128 + c].
- * scratch: cujev_ops_gdn_scratch_bytes(num_chunks, Hv) bytes, 256-aligned. */
+ * scratch: cujev_ops_gdn_scratch_bytes(num_chunks, Hv, N) bytes, 256-aligned. */
 int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const float *g,
                       const float *beta, const int32_t *chunk_tok0, const int32_t *chunk_len,
                       int num_chunks, const int32_t *seg_chunk0, const int32_t *seg_nchunk,
                       int num_segments, const float *S_in, float *S_out, const void *z,
-                      int z_stride, const float *norm_w, float eps, int Hk, int Hv, void *y,
-                      void *scratch, void *stream);
+                      int z_stride, const float *norm_w, float eps, int Hk, int Hv, int N,
+                      void *y, void *scratch, void *stream);
 
 #ifdef __cplusplus
 }

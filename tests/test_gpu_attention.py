@@ -129,20 +129,21 @@ def test_attention_branch_isolation():
 def test_attn_prep_matches_oracle():
     o = ops()
     rng = np.random.default_rng(21)
-    Hq, Hkv, N, rot, theta, eps = 8, 2, 150, 64, 1e7, 1e-6
+    Hq, Hkv, N, rot, theta, eps = 8, 2, 150, 64, 1e7, 1e-6  # positions up to 8000 below
     W = Hq * 2 * D + 2 * Hkv * D
     proj = orc.bf16_round(rng.standard_normal((N, W)).astype(np.float32))
     qn = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
     kn = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
-    pos = (np.arange(N) + 500).astype(np.int32)
+    pos = (np.arange(N) * 53 + 11).astype(np.int32)
     stride = o.kv_stride(N)
     dev = "cuda"
     qs = orc.LOG2E / 16.0
     q_out = torch.empty(N, Hq, D, dtype=torch.bfloat16, device=dev)
     kc = torch.zeros(Hkv, stride, D, dtype=torch.bfloat16, device=dev)
     vtc = torch.zeros(Hkv, D, stride, dtype=torch.bfloat16, device=dev)
+    rope = o.rope_table(theta, rot, int(pos.max()) + 1)
     o.attn_prep(bf(proj).to(dev), torch.as_tensor(qn).to(dev), torch.as_tensor(kn).to(dev),
-                torch.as_tensor(pos).to(dev), Hq, Hkv, rot, theta, eps, qs, q_out, kc, vtc, stride)
+                torch.as_tensor(pos).to(dev), Hq, Hkv, rot, rope, eps, qs, q_out, kc, vtc, stride)
     torch.cuda.synchronize()
     rq, rg, rk, rv = orc.attn_prep(proj, qn, kn, pos, Hq, Hkv, rot, theta, eps)
     assert rel_err(np32(q_out), rq * qs) <= 1e-2

@@ -79,7 +79,7 @@ def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False):
     o.gdn_conv_prep(pd, t(L.conv_w), cin, cout, seg_lens[0], t(own_base), t(L.A_neg),
                     t(L.dt_bias), L.Hk, L.Hv, q, k, v, g, beta)
     tok0, clen, seg0, segn = o.chunk_table(seg_lens)
-    scratch = torch.empty(o.gdn_scratch_bytes(len(tok0), L.Hv), dtype=torch.uint8, device=dev)
+    scratch = torch.empty(o.gdn_scratch_bytes(len(tok0), L.Hv, N), dtype=torch.uint8, device=dev)
     sin = t(S_in.astype(np.float32)) if S_in is not None else None
     sout = torch.zeros(L.Hv, DK, DV, dtype=torch.float32, device=dev) if write_state else None
     y = torch.empty(N, L.Hv * DV, dtype=torch.bfloat16, device=dev)
