@@ -40,69 +40,117 @@ constexpr int CH = 64;  /* chunk length   */
 /* ---------------------------------------------------------------------- */
 /* conv + gates                                                            */
 /* ---------------------------------------------------------------------- */
-/* grid (N, ceil((2Hk+Hv)/4)), 256 threads: wave = one 128-channel head slice
- * of one token; lane holds 2 channels. */
+/* One group of 16 lanes = one 128-channel head slice of PREP_T consecutive
+ * tokens; lane s holds channels 8s..8s+7. The PREP_T + 3 pre-conv rows the
+ * group needs are loaded once (16 bytes per lane and row when the projection
+ * rows allow it) and the 4-tap window slides over them in registers. Groups
+ * are numbered token block fastest, 16 per 256-thread workgroup. Groups of
+ * head h < Hv also produce g and beta of v-head h for their tokens. */
+constexpr int PREP_T = 8;
+
+template <bool VEC>
 __global__ __launch_bounds__(256) void gdn_conv_prep_kernel(
     const bf16 *__restrict__ proj, int ps, const float *__restrict__ conv_w,
     const float *__restrict__ conv_in, const int32_t *__restrict__ own_base,
-    const float *__restrict__ A_neg_exp, const float *__restrict__ dt_bias, int Hk, int Hv,
+    const float *__restrict__ A_neg_exp, const float *__restrict__ dt_bias, int N, int Hk, int Hv,
     bf16 *__restrict__ qo, bf16 *__restrict__ ko, bf16 *__restrict__ vo, float *__restrict__ go,
     float *__restrict__ bo) {
-    const int n = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nheads = 2 * Hk + Hv;
-    const int head = blockIdx.y * 4 + wave;
+    const int ntb = (N + PREP_T - 1) / PREP_T;
+    const int grp = blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int s = threadIdx.x & 15;
+    if (grp >= ntb * nheads)
+        return; /* whole 16-lane groups leave together */
+    const int head = grp / ntb, n0 = (grp - head * ntb) * PREP_T;
     const int C = nheads * DK;
-    const int local = n - own_base[n];
-    if (head < nheads) {
-        const int c0 = head * DK + 2 * lane;
-        const float4 wa = *(const float4 *)(conv_w + (size_t)c0 * 4);
-        const float4 wb = *(const float4 *)(conv_w + (size_t)(c0 + 1) * 4);
-        const float w0[4] = {wa.x, wa.y, wa.z, wa.w}, w1[4] = {wb.x, wb.y, wb.z, wb.w};
-        float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int tau = local - 3 + j; /* local index of the tap */
-            float x0, x1;
-            if (tau >= 0) {
-                const bf16 *src = proj + (size_t)(n - 3 + j) * ps + c0;
-                x0 = bf2f(src[0]);
-                x1 = bf2f(src[1]);
-            } else if (conv_in) {
-                x0 = conv_in[(size_t)c0 * 3 + tau + 3];
-                x1 = conv_in[(size_t)(c0 + 1) * 3 + tau + 3];
-            } else {
-                x0 = x1 = 0.f;
-            }
-            a0 += w0[j] * x0;
-            a1 += w1[j] * x1;
-        }
-        float y0 = silu_f(a0), y1 = silu_f(a1);
-        bf16 *dst;
-        if (head < 2 * Hk) {
-            const float ss = wave_sum(y0 * y0 + y1 * y1);
-            float inv = rsqrtf(ss + 1e-6f);
-            if (head < Hk) {
-                inv *= 0.08838834764831845f; /* 128^-1/2 */
-                dst = qo + ((size_t)n * Hk + head) * DK;
-            } else {
-                dst = ko + ((size_t)n * Hk + head - Hk) * DK;
-            }
-            y0 *= inv;
-            y1 *= inv;
-        } else {
-            dst = vo + ((size_t)n * Hv + head - 2 * Hk) * DV;
-        }
-        dst[2 * lane] = f2bf(y0);
-        dst[2 * lane + 1] = f2bf(y1);
-    }
-    if (blockIdx.y == 0) {
+    const int c0 = head * DK + 8 * s;
+
+    if (head < Hv && s < PREP_T && n0 + s < N) {
+        const int n = n0 + s;
         const bf16 *ab = proj + (size_t)n * ps + C + Hv * DV; /* b then a */
-        for (int t = threadIdx.x; t < Hv; t += blockDim.x) {
-            const float b = bf2f(ab[t]), a = bf2f(ab[Hv + t]);
-            bo[(size_t)n * Hv + t] = sigmoid_f(b);
-            go[(size_t)n * Hv + t] = A_neg_exp[t] * softplus_f(a + dt_bias[t]);
+        const float bv = bf2f(ab[head]), av = bf2f(ab[Hv + head]);
+        bo[(size_t)n * Hv + head] = sigmoid_f(bv);
+        go[(size_t)n * Hv + head] = A_neg_exp[head] * softplus_f(av + dt_bias[head]);
+    }
+
+    float w[8][4];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float4 t = *(const float4 *)(conv_w + (size_t)(c0 + e) * 4);
+        w[e][0] = t.x;
+        w[e][1] = t.y;
+        w[e][2] = t.z;
+        w[e][3] = t.w;
+    }
+    bf16x8 x[PREP_T + 3];
+#pragma unroll
+    for (int r = 0; r < PREP_T + 3; r++) {
+        const int row = n0 - 3 + r;
+        x[r] = bf16x8{};
+        if (row >= 0 && row < N) {
+            const bf16 *src = proj + (size_t)row * ps + c0;
+            if constexpr (VEC) {
+                x[r] = *(const bf16x8 *)src;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    x[r][e] = src[e];
+            }
         }
+    }
+    bf16 *dst;
+    float scale = 1.f;
+    const bool norm = head < 2 * Hk;
+    if (head < Hk) {
+        dst = qo + (size_t)head * DK;
+        scale = 0.08838834764831845f; /* 128^-1/2 */
+    } else if (head < 2 * Hk) {
+        dst = ko + (size_t)(head - Hk) * DK;
+    } else {
+        dst = vo + (size_t)(head - 2 * Hk) * DV;
+    }
+    const int tok_stride = head < 2 * Hk ? Hk * DK : Hv * DV;
+#pragma unroll
+    for (int j = 0; j < PREP_T; j++) {
+        const int n = n0 + j;
+        if (n >= N)
+            break; /* uniform over the group */
+        const int local = n - own_base[n];
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            y[e] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tau = local - 3 + i; /* local index of the tap */
+            if (tau >= 0) {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    y[e] += w[e][i] * bf2f(x[j + i][e]);
+            } else if (conv_in) {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    y[e] += w[e][i] * conv_in[(size_t)(c0 + e) * 3 + tau + 3];
+            }
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            y[e] = silu_f(y[e]);
+            ss += y[e] * y[e];
+        }
+        float inv = 1.f;
+        if (norm) {
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1)
+                ss += __shfl_xor(ss, o, 64);
+            inv = rsqrtf(ss + 1e-6f) * scale;
+        }
+        bf16x8 out;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            out[e] = f2bf(y[e] * inv);
+        *(bf16x8 *)(dst + (size_t)n * tok_stride + 8 * s) = out;
     }
 }
 
@@ -137,13 +185,14 @@ __global__ void gdn_conv_tail_kernel(const bf16 *__restrict__ proj, int ps,
 DEV int swap23(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
 
 struct __attribute__((aligned(16))) ChunkA_Smem {
-    bf16 K[CH][DK + 8];  /* k rows                                          */
-    bf16 Q[CH][DK + 8];  /* q rows                                          */
-    bf16 Kt[DK][CH + 8]; /* (beta e^G k)^T, later (k e^{Glast-G})^T swapped */
-    bf16 Vt[DV][CH + 8]; /* (beta v)^T                                      */
-    float A[CH][CH + 1]; /* strictly lower A                                */
-    float T[CH][CH + 1]; /* (I + A)^-1                                      */
-    float M[3][16][17];  /* block products                                  */
+    bf16 K[CH][DK + 8];  /* k rows                                            */
+    bf16 Q[CH][DK + 8];  /* q rows; later W staged for coalesced stores       */
+    bf16 V[CH][DV + 8];  /* v rows; later masked QK^T staged                  */
+    bf16 Kt[DK][CH + 8]; /* (beta e^G k)^T, later (k e^{Glast-G})^T swapped   */
+    bf16 Vt[DV][CH + 8]; /* (beta v)^T                                        */
+    float A[CH][CH + 1]; /* strictly lower A                                  */
+    float T[CH][CH + 1]; /* (I + A)^-1                                        */
+    float M[3][16][17];  /* block products                                    */
     float G[CH], B[CH];
 };
 
@@ -177,39 +226,46 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
         sm.G[lane] = gv;
         sm.B[lane] = bv;
     }
+    /* q, k, v rows (zero past L), 16-byte coalesced */
     for (int i = tid; i < CH * (DK / 8); i += 256) {
-        const int t = i / (DK / 8), c8 = (i % (DK / 8)) * 8;
-        bf16x8 kv = {}, qv = {};
+        const int t = i >> 4, c8 = (i & 15) * 8;
+        bf16x8 kv = {}, qv = {}, vv = {};
         if (t < L) {
             kv = ld8(kh_ + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
             qv = ld8(qh + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
+            vv = ld8(vh + ((size_t)(t0 + t) * Hv + hv) * DV + c8);
         }
         *(bf16x8 *)&sm.K[t][c8] = kv;
         *(bf16x8 *)&sm.Q[t][c8] = qv;
+        *(bf16x8 *)&sm.V[t][c8] = vv;
     }
     __syncthreads();
     const float Glast = sm.G[CH - 1];
-    /* (beta e^G k)^T, (beta v)^T into LDS; q e^G straight to HBM */
+    /* q e^G straight to HBM (16 lanes per row: coalesced) */
     for (int i = tid; i < CH * (DK / 8); i += 256) {
-        const int t = i / (DK / 8), c8 = (i % (DK / 8)) * 8;
+        const int t = i >> 4, c8 = (i & 15) * 8;
         const float eg = fast_exp(sm.G[t]);
-        const float sk = sm.B[t] * eg, sv = sm.B[t];
-        bf16x8 kv = *(const bf16x8 *)&sm.K[t][c8];
         bf16x8 qv = *(const bf16x8 *)&sm.Q[t][c8];
-        bf16x8 vv = {};
-        if (t < L)
-            vv = ld8(vh + ((size_t)(t0 + t) * Hv + hv) * DV + c8);
-        bf16x8 qg;
+        bf16 *qrow = Qgo + cb * CH * DK + t * DK;
+        st4(qrow + swap23(c8), f2bf(bf2f(qv[0]) * eg), f2bf(bf2f(qv[1]) * eg),
+            f2bf(bf2f(qv[2]) * eg), f2bf(bf2f(qv[3]) * eg));
+        st4(qrow + swap23(c8 + 4), f2bf(bf2f(qv[4]) * eg), f2bf(bf2f(qv[5]) * eg),
+            f2bf(bf2f(qv[6]) * eg), f2bf(bf2f(qv[7]) * eg));
+    }
+    /* (beta e^G k)^T and (beta v)^T: consecutive lanes take consecutive
+     * tokens so the transposed 2-byte writes hit consecutive addresses */
+    for (int i = tid; i < CH * (DK / 8); i += 256) {
+        const int t = i & 63, c8 = (i >> 6) * 8;
+        const float sk = sm.B[t] * fast_exp(sm.G[t]), sv = sm.B[t];
+        bf16x8 kv = *(const bf16x8 *)&sm.K[t][c8];
+        bf16x8 vv = *(const bf16x8 *)&sm.V[t][c8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             sm.Kt[c8 + e][t] = f2bf(bf2f(kv[e]) * sk);
             sm.Vt[c8 + e][t] = f2bf(bf2f(vv[e]) * sv);
-            qg[e] = f2bf(bf2f(qv[e]) * eg);
         }
-        bf16 *qrow = Qgo + cb * CH * DK + t * DK;
-        st4(qrow + swap23(c8), qg[0], qg[1], qg[2], qg[3]);
-        st4(qrow + swap23(c8 + 4), qg[4], qg[5], qg[6], qg[7]);
     }
+    __syncthreads(); /* V rows are free from here on: QK^T staging */
 
     /* K K^T and Q K^T: wave w owns the 32x32 tile (w>>1, w&1) of both */
     {
@@ -226,19 +282,22 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
         }
         const int j = 32 * tj + col;
         const float Gj = sm.G[j];
-        bf16 *qko = QKo + cb * CH * CH + swap23(j);
+        bf16 *qks = &sm.V[0][0] + swap23(j); /* [64][72] bf16 staging */
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int i = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
             const float dec = i >= j ? fast_exp(sm.G[i] - Gj) : 0.f;
             sm.A[i][j] = i > j ? sm.B[i] * kk[r] * dec : 0.f;
-            qko[i * CH] = f2bf(i >= j ? qk[r] * dec : 0.f);
+            qks[i * (CH + 8)] = f2bf(i >= j ? qk[r] * dec : 0.f);
         }
     }
     __syncthreads();
-
-    /* T = (I + A)^-1: 16x16 diagonal blocks by forward substitution (wave w
-     * inverts block w, lane c < 16 owns column c) ... */
+    /* masked QK^T rows to HBM; T = (I + A)^-1 diagonal blocks by forward
+     * substitution (wave w inverts block w, lane c < 16 owns column c) */
+    for (int i = tid; i < CH * (CH / 8); i += 256) {
+        const int r = i >> 3, c8 = (i & 7) * 8;
+        *(bf16x8 *)(QKo + cb * CH * CH + r * CH + c8) = *(const bf16x8 *)(&sm.V[0][0] + r * (CH + 8) + c8);
+    }
     if (lane < 16) {
         const int b0 = 16 * wave, c = lane;
         float t[16];
@@ -288,9 +347,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
     __syncthreads();
 
     /* W = T (beta e^G K), U = T (beta V): wave w owns rows 32(w>>1).. and
-     * columns 64(w&1)..+64 of both. W goes out row-major with swapped
-     * columns; U goes out in accumulator-fragment order, i.e. exactly the 16
-     * values lane l of phase B's wave (column block) needs, contiguous. */
+     * columns 64(w&1)..+64 of both. W is staged (swapped columns) in the q
+     * rows' LDS for coalesced stores; U goes out in accumulator-fragment
+     * order, i.e. exactly the 16 values lane l of phase B's wave (column
+     * block) needs, contiguous. */
     {
         const int mi = wave >> 1, nh = wave & 1;
         floatx16 w[2] = {}, u[2] = {};
@@ -310,14 +370,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
                 u[nj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bv, u[nj], 0, 0, 0);
             }
         }
-        bf16 *wo = Wo + cb * CH * DK;
 #pragma unroll
         for (int nj = 0; nj < 2; nj++) {
             const int c = swap23(64 * nh + 32 * nj + col);
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int i = 32 * mi + 8 * (r >> 2) + 4 * h + (r & 3);
-                wo[i * DK + c] = f2bf(w[nj][r]);
+                sm.Q[i][c] = f2bf(w[nj][r]);
             }
             const int wblk = 2 * nh + nj; /* phase B's wave owning these 32 columns */
             bf16 *uo = Uo + (((cb * 4 + wblk) * 2 + mi) * 64 + lane) * 16;
@@ -331,10 +390,14 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
             *(bf16x8 *)(uo + 8) = hi;
         }
     }
-    __syncthreads(); /* everyone is done with Kt */
+    __syncthreads(); /* everyone is done with Kt; W is staged */
+    for (int i = tid; i < CH * (DK / 8); i += 256) {
+        const int t = i >> 4, c8 = (i & 15) * 8;
+        *(bf16x8 *)(Wo + cb * CH * DK + t * DK + c8) = *(const bf16x8 *)&sm.Q[t][c8];
+    }
     /* (k e^{Glast - G})^T with swapped token columns, then rows to HBM */
     for (int i = tid; i < CH * (DK / 8); i += 256) {
-        const int t = i / (DK / 8), c8 = (i % (DK / 8)) * 8;
+        const int t = i & 63, c8 = (i >> 6) * 8;
         const float ek = fast_exp(Glast - sm.G[t]);
         bf16x8 kv = *(const bf16x8 *)&sm.K[t][c8];
         const int ts = swap23(t);
@@ -582,10 +645,12 @@ extern "C" hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const
     if (Hk <= 0 || Hv % Hk != 0)
         return hipErrorInvalidValue;
     const int nheads = 2 * Hk + Hv;
-    hipLaunchKernelGGL(gdn_conv_prep_kernel, dim3((unsigned)N, (unsigned)CEIL_DIV(nheads, 4)),
-                       dim3(256), 0, stream, (const bf16 *)proj, proj_stride, conv_w, conv_in,
-                       own_base, A_neg_exp, dt_bias, Hk, Hv, (bf16 *)q, (bf16 *)k, (bf16 *)v, g,
-                       beta);
+    const int groups = CEIL_DIV(N, PREP_T) * nheads;
+    const bool vec = proj_stride % 8 == 0 && ((uintptr_t)proj & 15) == 0;
+    auto kern = vec ? gdn_conv_prep_kernel<true> : gdn_conv_prep_kernel<false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)CEIL_DIV(groups, 16)), dim3(256), 0, stream,
+                       (const bf16 *)proj, proj_stride, conv_w, conv_in, own_base, A_neg_exp,
+                       dt_bias, N, Hk, Hv, (bf16 *)q, (bf16 *)k, (bf16 *)v, g, beta);
     if (conv_out) {
         const int C = nheads * DK;
         hipLaunchKernelGGL(gdn_conv_tail_kernel, dim3((unsigned)CEIL_DIV(C, 256)), dim3(256), 0,

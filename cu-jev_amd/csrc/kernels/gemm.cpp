@@ -8,6 +8,8 @@
 #include "kernels.h"
 #include <hipblaslt/hipblaslt.h>
 
+#include <stdlib.h>
+
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -62,7 +64,20 @@ extern "C" void cujev_gemm_destroy(cujev_gemm *g) {
     delete g;
 }
 
-static bool make_plan(cujev_gemm *g, int N, int M, int K, int f32out, GemmPlan &p) {
+/* Heuristic candidates are timed once on the caller's buffers and stream
+ * (the output is simply rewritten), and the fastest is kept for the shape.
+ * CUJEV_GEMM_TUNE=0 keeps the heuristic's first choice. */
+static int tuning_enabled(void) {
+    static int cached = -1;
+    if (cached < 0) {
+        const char *e = getenv("CUJEV_GEMM_TUNE");
+        cached = !(e && *e == '0');
+    }
+    return cached;
+}
+
+static bool make_plan(cujev_gemm *g, int N, int M, int K, int f32out, GemmPlan &p, const void *X,
+                      const void *W, void *Y, hipStream_t stream) {
     const hipDataType out_t = f32out ? HIP_R_32F : HIP_R_16BF;
     if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
         return false;
@@ -79,15 +94,47 @@ static bool make_plan(cujev_gemm *g, int N, int M, int K, int f32out, GemmPlan &
     uint64_t ws = g->ws_bytes;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
                                           sizeof ws);
-    hipblasLtMatmulHeuristicResult_t res[1];
+    constexpr int MAXC = 16;
+    hipblasLtMatmulHeuristicResult_t res[MAXC];
     int count = 0;
-    hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(g->handle, p.desc, p.a, p.b, p.c, p.c,
-                                                         pref, 1, res, &count);
+    hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(
+        g->handle, p.desc, p.a, p.b, p.c, p.c, pref, tuning_enabled() ? MAXC : 1, res, &count);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (st != HIPBLAS_STATUS_SUCCESS || count < 1)
         return false;
-    p.algo = res[0].algo;
-    p.ws = res[0].workspaceSize;
+    int best = 0;
+    if (count > 1) {
+        hipEvent_t e0, e1;
+        hipEventCreate(&e0);
+        hipEventCreate(&e1);
+        const float alpha = 1.f, beta = 0.f;
+        float best_ms = 1e30f;
+        for (int i = 0; i < count; i++) {
+            if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > g->ws_bytes)
+                continue;
+            bool ok = true;
+            for (int r = 0; r < 4 && ok; r++) {
+                if (r == 1)
+                    hipEventRecord(e0, stream);
+                ok = hipblasLtMatmul(g->handle, p.desc, &alpha, W, p.a, X, p.b, &beta, Y, p.c, Y,
+                                     p.c, &res[i].algo, g->workspace, res[i].workspaceSize,
+                                     stream) == HIPBLAS_STATUS_SUCCESS;
+            }
+            hipEventRecord(e1, stream);
+            if (!ok || hipEventSynchronize(e1) != hipSuccess)
+                continue;
+            float ms = 0.f;
+            hipEventElapsedTime(&ms, e0, e1);
+            if (ms < best_ms) {
+                best_ms = ms;
+                best = i;
+            }
+        }
+        hipEventDestroy(e0);
+        hipEventDestroy(e1);
+    }
+    p.algo = res[best].algo;
+    p.ws = res[best].workspaceSize;
     return true;
 }
 
@@ -102,7 +149,7 @@ extern "C" hipError_t k_gemm(cujev_gemm *g, const bf16_t *X, const bf16_t *W, vo
         auto it = g->plans.find(key);
         if (it == g->plans.end()) {
             GemmPlan p;
-            if (!make_plan(g, N, M, K, f32out, p)) {
+            if (!make_plan(g, N, M, K, f32out, p, X, W, Y, stream)) {
                 destroy_plan(p);
                 return hipErrorNotSupported;
             }

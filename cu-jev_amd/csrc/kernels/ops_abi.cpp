@@ -29,6 +29,28 @@ static int launched(hipError_t e, const char *what) {
 }
 
 EXPORT int cujev_ops_kv_stride(int max_tokens) { return cujev_kv_stride(max_tokens); }
+
+/* One hipBLASLt context per process for the GEMM entry point; its workspace
+ * is the caller's. */
+static cujev_gemm *g_gemm = nullptr;
+static void *g_gemm_ws = nullptr;
+
+EXPORT int cujev_op_gemm(const void *X, const void *W, void *Y, int f32out, int N, int M, int K,
+                         void *workspace, size_t ws_bytes, void *stream) {
+    if (N < 0 || M <= 0 || K <= 0 || !X || !W || !Y)
+        return fail(1, "gemm: bad arguments");
+    if (!g_gemm || g_gemm_ws != workspace) {
+        if (g_gemm)
+            cujev_gemm_destroy(g_gemm);
+        g_gemm = nullptr;
+        if (cujev_gemm_create(&g_gemm, workspace, ws_bytes) != 0)
+            return fail(4, "gemm: hipblasLtCreate failed");
+        g_gemm_ws = workspace;
+    }
+    return launched(k_gemm(g_gemm, (const bf16_t *)X, (const bf16_t *)W, Y, f32out, N, M, K,
+                           (hipStream_t)stream),
+                    "gemm");
+}
 EXPORT const char *cujev_ops_last_error(void) { return g_err; }
 
 EXPORT int cujev_op_rope_table(double theta, int rot, int npos, float *table) {

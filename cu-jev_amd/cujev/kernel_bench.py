@@ -1,0 +1,118 @@
+"""Kernel-level workloads of the hot path through the operator C ABI, used by
+bench.py (timed with HIP events on the launch stream) and runnable on their
+own for profilers:
+
+    python -m cujev.kernel_bench attention|gdn|copy [iters]
+
+attention  config 3: Hq 16 / Hkv 4, D 256, state 8192 keys, 256 branches x 16
+gdn        config 2: Hk 16 / Hv 32, T = 2048 prefill (conv+gates, scan, norm)
+copy       a plain device-to-device copy of 256 MiB (scale factor for the
+           FETCH_SIZE / WRITE_SIZE counters)
+"""
+from __future__ import annotations
+
+import sys
+
+
+def attention_case():
+    import torch
+    from . import ops
+    ops.load()
+    D, Hq, Hkv, P, B, L = 256, 16, 4, 8192, 256, 16
+    N = B * L
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(1)
+    ps, os_ = ops.kv_stride(P), ops.kv_stride(N)
+    t = dict(
+        pk=torch.randn(Hkv, ps, D, device=dev, generator=g).to(torch.bfloat16),
+        pvt=torch.randn(Hkv, D, ps, device=dev, generator=g).to(torch.bfloat16),
+        ok=torch.randn(Hkv, os_, D, device=dev, generator=g).to(torch.bfloat16),
+        ovt=torch.randn(Hkv, D, os_, device=dev, generator=g).to(torch.bfloat16),
+        q=(torch.randn(N, Hq, D, device=dev, generator=g) * (1.4426950408889634 / 16)).to(
+            torch.bfloat16),
+        gate=torch.randn(N, Hq, D, device=dev, generator=g).to(torch.bfloat16),
+        own_base=torch.arange(N, device=dev, dtype=torch.int32) // L * L,
+        out=torch.empty(N, Hq * D, dtype=torch.bfloat16, device=dev))
+
+    def launch():
+        ops.attention(t["q"], t["gate"], Hq * D, D, t["pk"], t["pvt"], P, ps, t["ok"], t["ovt"],
+                      os_, t["own_base"], Hq, Hkv, t["out"])
+
+    flop = 4.0 * D * Hq * (N * P + B * L * (L + 1) / 2)  # QK^T + PV, exact causal count
+    return launch, {"flop": flop}
+
+
+def gdn_case():
+    import torch
+    from . import ops
+    ops.load()
+    Hk, Hv, T = 16, 32, 2048
+    C = (2 * Hk + Hv) * 128
+    Wd = C + Hv * 128 + 2 * Hv
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(2)
+    proj = torch.randn(T, Wd, device=dev, generator=g).to(torch.bfloat16)
+    conv_w = torch.randn(C, 4, device=dev, generator=g) * 0.5
+    A_neg = -torch.rand(Hv, device=dev, generator=g) * 4
+    dt_bias = torch.zeros(Hv, device=dev)
+    norm_w = torch.ones(128, device=dev)
+    own_base = torch.zeros(T, dtype=torch.int32, device=dev)
+    q = torch.empty(T, Hk, 128, dtype=torch.bfloat16, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty(T, Hv, 128, dtype=torch.bfloat16, device=dev)
+    gg = torch.empty(T, Hv, device=dev)
+    beta = torch.empty_like(gg)
+    conv_out = torch.empty(C, 3, device=dev)
+    S_out = torch.empty(Hv, 128, 128, device=dev)
+    y = torch.empty(T, Hv * 128, dtype=torch.bfloat16, device=dev)
+    tok0, clen, seg0, segn = (torch.as_tensor(a).to(dev) for a in ops.chunk_table([T]))
+    scratch = torch.empty(ops.gdn_scratch_bytes(len(tok0), Hv, T), dtype=torch.uint8, device=dev)
+
+    def launch():
+        ops.gdn_conv_prep(proj, conv_w, None, conv_out, T, own_base, A_neg, dt_bias, Hk, Hv, q, k,
+                          v, gg, beta)
+        ops.gdn_scan(q, k, v, gg, beta, tok0, clen, seg0, segn, None, S_out, proj[:, C:],
+                     proj.stride(0), norm_w, 1e-6, Hk, Hv, y, scratch)
+
+    # compulsory bytes: pre-conv qkv, a/b, conv w, z, bf16 out, S_out, conv tail
+    nbytes = T * C * 2 + T * 2 * Hv * 2 + C * 4 * 4 + T * Hv * 128 * 2 + T * Hv * 128 * 2 \
+        + Hv * 128 * 128 * 4 + C * 3 * 4
+    return launch, {"bytes": nbytes}
+
+
+def copy_case(nbytes=256 << 20):
+    import torch
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+
+    def launch():
+        b.copy_(a)
+
+    return launch, {"bytes": nbytes}
+
+
+def time_launches(launch, iters=20, warmup=3):
+    """Average microseconds per launch, HIP events on torch's current stream
+    (the stream the operator ABI launches on)."""
+    import torch
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(iters):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters * 1e3
+
+
+CASES = {"attention": attention_case, "gdn": gdn_case, "copy": copy_case}
+
+if __name__ == "__main__":
+    name = sys.argv[1]
+    iters = int(sys.argv[2]) if len(sys.argv) > 2 else 20
+    launch, info = CASES[name]()
+    us = time_launches(launch, iters)
+    print(f"{name}: {us:.1f} us per launch {info}", flush=True)

@@ -28,6 +28,7 @@ _D = C.c_double
 
 # name -> argtypes (all return int status)
 _SIGS = {
+    "cujev_op_gemm": [_P, _P, _P, _I, _I, _I, _I, _P, C.c_size_t, _P],
     "cujev_op_rope_table": [_D, _I, _I, _P],
     "cujev_op_attn_prep": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _F, _F, _P, _P, _P, _I, _P],
     "cujev_op_attention": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P],
@@ -151,3 +152,18 @@ def gdn_scan(q, k, v, g, beta, chunk_tok0, chunk_len, seg_chunk0, seg_nchunk, S_
           _ptr(chunk_len), chunk_tok0.shape[0], _ptr(seg_chunk0), _ptr(seg_nchunk),
           seg_chunk0.shape[0], _ptr(S_in), _ptr(S_out), _ptr(z), int(z_stride), _ptr(norm_w),
           float(eps), Hk, Hv, q.shape[0], _ptr(y), _ptr(scratch), _stream())
+
+
+_gemm_ws = None
+
+
+def gemm(X, W, Y, f32out=False):
+    """Y[N,M] = X[N,K] . W[M,K]^T (bf16 in, fp32 accumulate)."""
+    import torch
+    global _gemm_ws
+    if _gemm_ws is None:
+        _gemm_ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    N, K = X.shape
+    M = W.shape[0]
+    _call("cujev_op_gemm", _ptr(X), _ptr(W), _ptr(Y), int(bool(f32out)), N, M, K, _ptr(_gemm_ws),
+          _gemm_ws.numel(), _stream())

@@ -33,6 +33,13 @@ extern "C" {
 int cujev_ops_kv_stride(int max_tokens);
 const char *cujev_ops_last_error(void);
 
+/* Replaces reference src/kernels/kernels.h:50-53 (k_gemm_bf16*): Y[N,M] =
+ * X[N,K] . W[M,K]^T, bf16 inputs, fp32 accumulation, bf16 (f32out = 0) or fp32
+ * output, through hipBLASLt. `workspace` (ws_bytes, e.g. 64 MiB) is device
+ * memory the caller keeps for the process; plans are cached per shape. */
+int cujev_op_gemm(const void *X, const void *W, void *Y, int f32out, int N, int M, int K,
+                  void *workspace, size_t ws_bytes, void *stream);
+
 /* Fills the device RoPE table used by cujev_op_attn_prep: table[p][i] =
  * (cos a, sin a), a = fp32(fp32(theta^(-2i/rot)) * p), p < npos, i < rot/2
  * (npos * rot floats). Synchronous. Replaces the reference's per-launch
