@@ -9,37 +9,53 @@
  * (modeling_qwen3_5.py:656-701).
  *
  * The kernel is designed for CDNA4, not translated:
- *  - One workgroup owns one kv-head and 32*TG consecutive packed tokens; its
- *    4*TG waves are (token group) x (the 4 q-heads of the kv-group). Every
- *    64-key K/V tile staged in LDS therefore serves 128*TG query rows of
- *    possibly several branches: the state keys are identical for all of them.
+ *  - One workgroup owns one kv-head and 32 consecutive packed tokens; its 4
+ *    waves are the 4 q-heads of the kv-group. Every 64-key K/V tile staged in
+ *    LDS therefore serves 128 query rows of possibly several branches: the
+ *    state keys are identical for all of them.
  *  - The MFMA is v_mfma_f32_32x32x16_bf16 computing S^T = K Q^T (keys on the
  *    M side, queries on N), so each lane holds 16 keys of ONE query: row max
- *    and row sum are in-lane plus one lane^32 exchange.
+ *    and row sum are in-lane plus one v_permlane32_swap.
  *  - K rows are fed to the A operand in a permuted order (bits 2 and 3 of the
  *    row swapped) so that the S^T accumulator of a lane is exactly the 8
  *    consecutive keys the B operand of O^T += V^T P^T needs: P goes from the
  *    accumulator to the next MFMA without any cross-lane movement.
  *  - V is kept d-major in HBM (vt cache [Hkv][256][stride]) so the V^T A
  *    operand is a 16-byte LDS read; the prep kernel writes it that way.
- *  - LDS tiles are XOR-swizzled for conflict-free ds_read_b128; the next tile
- *    is fetched to registers while the current one is multiplied (one barrier
- *    per tile).
+ *  - Tiles move HBM -> LDS with buffer_load ... lds (no staging registers),
+ *    XOR-swizzled for conflict-free ds_read_b128. K and V^T have separate
+ *    double buffers: while a wave runs the softmax of tile i interleaved with
+ *    the S^T MFMAs of tile i+1 and then the PV MFMAs of tile i, the V^T of
+ *    tile i+1 and the K of tile i+2 are in flight. One barrier per tile.
+ *  - S accumulators start at -m (the running max), so scores arrive shifted;
+ *    m only moves when a tile's max exceeds it by more than 2^8, which after
+ *    the first tiles is rare, and then the O/l rescale runs.
  *  - blockIdx -> (kv-head, token tile) is XCD-aware: the 8 XCDs (own L2 each)
  *    are split among the kv-heads so the WGs sharing an L2 stream the same
  *    K/V. Tiles run last-to-first so the longest causal rows start first. */
 #include "common.h"
 #include "kernels.h"
 
+#include <type_traits>
+
 namespace CUJEV_KNS {
 namespace {
 
 constexpr int D = 256;
-constexpr int BK = 64;                   /* keys per tile */
-constexpr int QW = 32;                   /* query tokens per wave */
-constexpr int K_BYTES = BK * D * 2;      /* 32 KiB: K tile [64][256]    */
-constexpr int V_BYTES = D * BK * 2;      /* 32 KiB: V^T tile [256][64]  */
-constexpr int BUF_BYTES = K_BYTES + V_BYTES;
+constexpr int BK = 64;              /* keys per tile */
+constexpr int QW = 32;              /* query tokens per wave */
+constexpr int K_BYTES = BK * D * 2; /* 32 KiB: K tile [64][256]    */
+constexpr int V_BYTES = D * BK * 2; /* 32 KiB: V^T tile [256][64]  */
+/* LDS: V^T buffers first, K buffers after, so every ds_read offset of a
+ * buffer fits the 16-bit immediate from one per-lane base register. */
+constexpr int V_OFF = 0, K_OFF = 2 * V_BYTES, LDS_BYTES = 2 * V_BYTES + 2 * K_BYTES;
+/* Lazy rescale: the running max only moves when a tile's max exceeds it by
+ * more than 2^TAU, so p <= 2^TAU; the softmax is exact for any reference m
+ * (it cancels in o / l) and p keeps its bf16 rounding. */
+#ifndef CUJEV_ATTN_TAU
+#define CUJEV_ATTN_TAU 8.f
+#endif
+constexpr float TAU = CUJEV_ATTN_TAU;
 
 /* 16-byte chunk swizzles: the 16 lanes of one ds_read_b128 phase hit 16
  * distinct 16-byte bank groups (and any 8 consecutive lanes 8 distinct ones). */
@@ -48,57 +64,64 @@ DEV int swz_v(int d) { return (d & 7) ^ ((d >> 3) & 1); }
 /* MFMA row m of the S^T tile holds key perm_row(m) of its 32-key block. */
 DEV int perm_row(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
+typedef __attribute__((address_space(3))) void *lds_ptr;
+typedef __attribute__((address_space(3))) const unsigned char lds_u8;
+/* 16-byte LDS read at a byte offset from the start of the tile buffers */
+DEV bf16x8 lds_read16(lds_u8 *base, uint32_t off) {
+    return *(__attribute__((address_space(3))) const bf16x8 *)(base + off);
+}
+
+/* Tiles go HBM -> LDS directly (buffer_load_dwordx4 ... lds): lane l of a
+ * wave writes the 16 bytes it fetched at LDS base + 16 l, so the swizzle is
+ * applied on the global side: the lane landing on chunk slot p of LDS row r
+ * fetches chunk p ^ swz(r). Per tile and operand each of the 4 waves issues 8
+ * such loads: K load j of wave w covers rows 8j + 2w + {0,1}; V^T load j covers
+ * d rows 8(4j + w) .. +7. No registers hold the tile in flight, and the buffer
+ * form only counts against vmcnt, so LDS reads keep their own fine-grained
+ * waits. Each operand of a kv-head has its own buffer resource whose size is
+ * the cache slice, so the hardware range check covers every load. */
 struct TileSrc {
-    const bf16 *k;  /* K rows of this kv-head */
-    const bf16 *vt; /* V^T rows of this kv-head */
-    int kbase;      /* first key of the tile (multiple of 64) */
-    int stride;     /* cache stride in tokens */
+    __amdgpu_buffer_rsrc_t k;  /* K rows [stride][256] of this kv-head */
+    __amdgpu_buffer_rsrc_t vt; /* V^T rows [256][stride] of this kv-head */
+    int kbase;                 /* first key of the tile (multiple of 64) */
+    uint32_t voff;             /* this lane's byte offset inside a V^T load */
+    int vrow_bytes;            /* V^T row pitch in bytes */
 };
 
-template <int NT>
-DEV void fetch_tile(const TileSrc &s, u32x4 (&stage)[2 * 2048 / NT]) {
-    constexpr int PER = 2048 / NT; /* 16-byte chunks per thread per operand */
-    const int t = threadIdx.x;
+DEV __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+
+DEV void issue_k(const TileSrc &s, unsigned char *kbuf, const uint32_t (&koff)[2], int wave) {
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int idx = t + NT * j;
-        const int row = idx >> 5, c = idx & 31;
-        stage[j] = *(const u32x4 *)(s.k + (size_t)(s.kbase + row) * D + c * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int idx = t + NT * j;
-        const int d = idx >> 3, c = idx & 7;
-        stage[PER + j] = *(const u32x4 *)(s.vt + (size_t)d * s.stride + s.kbase + c * 8);
+    for (int j = 0; j < 8; j++) {
+        const int r0 = 8 * j + 2 * wave;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(s.k, (lds_ptr)(kbuf + r0 * 512), 16, koff[j & 1],
+                                                 (s.kbase + r0) * 512, 0, 0);
     }
 }
 
-template <int NT>
-DEV void store_tile(unsigned char *buf, const u32x4 (&stage)[2 * 2048 / NT]) {
-    constexpr int PER = 2048 / NT;
-    const int t = threadIdx.x;
+DEV void issue_v(const TileSrc &s, unsigned char *vbuf, int wave) {
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int idx = t + NT * j;
-        const int row = idx >> 5, c = idx & 31;
-        *(u32x4 *)(buf + row * 512 + ((c ^ swz_k(row)) << 4)) = stage[j];
-    }
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int idx = t + NT * j;
-        const int d = idx >> 3, c = idx & 7;
-        *(u32x4 *)(buf + K_BYTES + d * 128 + ((c ^ swz_v(d)) << 4)) = stage[PER + j];
+    for (int j = 0; j < 8; j++) {
+        const int d0 = 8 * (4 * j + wave);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(s.vt, (lds_ptr)(vbuf + d0 * 128), 16, s.voff,
+                                                 d0 * s.vrow_bytes + s.kbase * 2, 0, 0);
     }
 }
 
-template <int TG>
-__global__ __launch_bounds__(256 * TG) void attention_kernel(
+DEV void wait_tile_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+/* One workgroup = 4 waves = the 4 q-heads of kv-head kh x 32 packed tokens.
+ * Per key tile i the loop overlaps, in each wave, the S^T MFMAs of tile i+1
+ * with the softmax of tile i, then runs the PV MFMAs of tile i, while the
+ * V^T of tile i+1 and the K of tile i+2 stream into the idle buffers. */
+__global__ __launch_bounds__(256) void attention_kernel(
     const bf16 *__restrict__ q, const bf16 *__restrict__ gate, int gts, int ghs,
     const bf16 *__restrict__ pk, const bf16 *__restrict__ pvt, int P, int p_stride,
     const bf16 *__restrict__ ok, const bf16 *__restrict__ ovt, int o_stride,
     const int32_t *__restrict__ own_base, int N, int Hq, int Hkv, int ntile, bf16 *__restrict__ out) {
-    constexpr int NT = 256 * TG;
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * BUF_BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[LDS_BYTES];
 
     /* ---- XCD-aware work mapping ---- */
     int kh, tile;
@@ -116,12 +139,11 @@ __global__ __launch_bounds__(256 * TG) void attention_kernel(
             return;
         tile = ntile - 1 - tile;
     }
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int hq = wave & 3, tg = wave >> 2;
-    const int head = kh * 4 + hq;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int head = kh * 4 + wave;
     const int h = lane >> 5, col = lane & 31;
-    const int n0 = tile * (QW * TG);
-    const int n = n0 + tg * QW + col; /* this lane's query token */
+    const int n0 = tile * QW;
+    const int n = n0 + col; /* this lane's query token */
     const bool qvalid = n < N;
 
     /* ---- Q^T B-operand fragments, resident for the whole kernel ---- */
@@ -138,110 +160,210 @@ __global__ __launch_bounds__(256 * TG) void attention_kernel(
 
     /* ---- key tiles: state [0,P) then own [own_lo, own_hi] (64-aligned) ---- */
     const int own_lo = own_base[n0];
-    const int own_hi = min(n0 + QW * TG, N) - 1;
+    const int own_hi = min(n0 + QW, N) - 1;
     const int nst = (P + BK - 1) / BK;
     const int own_t0 = own_lo / BK;
     const int ntl = nst + own_hi / BK - own_t0 + 1;
-    const bf16 *pk_h = pk + (size_t)kh * p_stride * D, *pv_h = pvt + (size_t)kh * D * p_stride;
-    const bf16 *ok_h = ok + (size_t)kh * o_stride * D, *ov_h = ovt + (size_t)kh * D * o_stride;
+
+    uint32_t koff[2];
+#pragma unroll
+    for (int par = 0; par < 2; par++) {
+        const int hi = lane >> 5, row = 8 * par + 2 * wave + hi;
+        koff[par] = hi * 512 + (((lane & 31) ^ swz_k(row)) << 4);
+    }
+    const int vl = lane >> 3, vc = ((lane & 7) ^ ((lane >> 3) ^ (wave & 1))) << 4;
+    TileSrc st, ow;
+    const uint32_t p_bytes = (uint32_t)p_stride * D * 2, o_bytes = (uint32_t)o_stride * D * 2;
+    st.k = make_rsrc(pk + (size_t)kh * p_stride * D, p_bytes);
+    st.vt = make_rsrc(pvt + (size_t)kh * D * p_stride, p_bytes);
+    st.vrow_bytes = p_stride * 2;
+    st.voff = vl * st.vrow_bytes + vc;
+    ow.k = make_rsrc(ok + (size_t)kh * o_stride * D, o_bytes);
+    ow.vt = make_rsrc(ovt + (size_t)kh * D * o_stride, o_bytes);
+    ow.vrow_bytes = o_stride * 2;
+    ow.voff = vl * ow.vrow_bytes + vc;
     auto src_of = [&](int i) {
-        TileSrc s;
-        if (i < nst) {
-            s.k = pk_h; s.vt = pv_h; s.kbase = i * BK; s.stride = p_stride;
-        } else {
-            s.k = ok_h; s.vt = ov_h; s.kbase = (own_t0 + i - nst) * BK; s.stride = o_stride;
-        }
+        TileSrc s = i < nst ? st : ow;
+        s.kbase = i < nst ? i * BK : (own_t0 + i - nst) * BK;
         return s;
     };
+
+    /* per-lane LDS read addresses; the rest of each address is an immediate */
+    const int arow = perm_row(col); /* key rows arow and 32 + arow */
+    lds_u8 *lds = (lds_u8 *)smem;
+    const int xk = h ^ swz_k(arow);
+    uint32_t ka[8];
+#pragma unroll
+    for (int c8 = 0; c8 < 8; c8++)
+        ka[c8] = K_OFF + arow * 512 + (((2 * c8) ^ xk) << 4);
+    const int xv = h ^ swz_v(col);
+    uint32_t va[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++)
+        va[s4] = V_OFF + col * 128 + (((2 * s4) ^ xv) << 4);
 
     floatx16 o[8];
 #pragma unroll
     for (int i = 0; i < 8; i++)
         o[i] = floatx16{};
-    float m_run = -INFINITY, l_run = 0.f;
+    /* m_run: running max (log2 units); S accumulators start at -mu, mu being
+     * the running max when the tile's S^T began (0 before any key), so the
+     * scores reach the softmax already shifted. sbase_* tracks that shift. */
+    float m_run = -INFINITY, l_run = 0.f, mu_run = 0.f;
 
-    u32x4 stage[2 * 2048 / NT];
-    fetch_tile<NT>(src_of(0), stage);
-    store_tile<NT>(smem, stage);
+    constexpr int QD = 3; /* S^T A-operand reads in flight, in k-steps */
+    constexpr int VD = 4; /* V^T A-operand reads in flight, in MFMAs   */
+    auto kaddr = [&](int ks, int buf) { return ka[ks & 7] + (ks >> 3) * 256 + buf * K_BYTES; };
+    auto vaddr = [&](int t, int buf) { return va[t >> 3] + (t & 7) * 4096 + buf * V_BYTES; };
+
+    /* prologue: K0, V0, K1 in flight; S^T of tile 0 */
+    issue_k(src_of(0), smem + K_OFF, koff, wave);
+    issue_v(src_of(0), smem + V_OFF, wave);
+    if (ntl > 1)
+        issue_k(src_of(1), smem + K_OFF + K_BYTES, koff, wave);
+    wait_tile_loads();
     __syncthreads();
-
-    const int arow0 = perm_row(col), arow1 = 32 + perm_row(col);
-    for (int i = 0; i < ntl; i++) {
-        const bool more = i + 1 < ntl;
-        if (more)
-            fetch_tile<NT>(src_of(i + 1), stage);
-        const unsigned char *kt = smem + (i & 1) * BUF_BYTES;
-        const unsigned char *vt = kt + K_BYTES;
-
-        /* S^T = K Q^T for 64 keys x this wave's 32 queries */
-        floatx16 s0 = floatx16{}, s1 = floatx16{};
+    floatx16 sa0 = floatx16{}, sa1 = floatx16{}, sb0, sb1;
+    float sbase_a = 0.f, sbase_b = 0.f;
 #pragma unroll
-        for (int ks = 0; ks < 16; ks++) {
-            const int c = 2 * ks + h;
-            bf16x8 a0 = *(const bf16x8 *)(kt + arow0 * 512 + ((c ^ swz_k(arow0)) << 4));
-            bf16x8 a1 = *(const bf16x8 *)(kt + arow1 * 512 + ((c ^ swz_k(arow1)) << 4));
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[ks], s1, 0, 0, 0);
-        }
+    for (int ks = 0; ks < 16; ks++) {
+        sa0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_read16(lds, kaddr(ks, 0)), qf[ks], sa0, 0, 0, 0);
+        sa1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_read16(lds, kaddr(ks, 0) + 16384), qf[ks],
+                                                      sa1, 0, 0, 0);
+    }
+    __syncthreads(); /* K buffer 0 is refilled in the first step */
+
+    /* One key tile i with scores S = (s0, s1) shifted by sbase. With a next
+     * tile, its S^T MFMAs run in the same straight-line block as this tile's
+     * softmax: per k-step two MFMAs, the LDS reads QD k-steps ahead and a
+     * slice of the softmax VALU work, pinned in that order by scheduling
+     * barriers. The PV MFMAs of tile i follow with their reads VD ahead. */
+    auto step = [&](auto has_next, int i, floatx16 &s0, floatx16 &s1, float &sbase, floatx16 &n0_,
+                    floatx16 &n1_, float &nbase, int kbuf_next, int vbuf) {
+        constexpr bool NEXT = decltype(has_next)::value;
+        if (NEXT)
+            issue_v(src_of(i + 1), smem + V_OFF + (vbuf ^ 1) * V_BYTES, wave);
+        if (i + 2 < ntl)
+            issue_k(src_of(i + 2), smem + K_OFF + (kbuf_next ^ 1) * K_BYTES, koff, wave);
 
         /* mask: key of accumulator slot r of block t is 32t + 16(r>>3) + 8h + (r&7) */
-        const TileSrc cur = src_of(i);
         const bool own = i >= nst;
-        if (own || cur.kbase + BK > P) {
-            const int k8 = cur.kbase + 8 * h;
+        const int kbase = own ? (own_t0 + i - nst) * BK : i * BK;
+        if (own || kbase + BK > P) {
+            const int lo = own ? base_n : 0, hi = own ? n : P - 1;
+            const int k8 = kbase + 8 * h;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int j0 = k8 + 16 * (r >> 3) + (r & 7), j1 = j0 + 32;
-                const bool v0 = own ? (j0 >= base_n && j0 <= n) : (j0 < P);
-                const bool v1 = own ? (j1 >= base_n && j1 <= n) : (j1 < P);
-                s0[r] = v0 ? s0[r] : -INFINITY;
-                s1[r] = v1 ? s1[r] : -INFINITY;
+                s0[r] = (j0 >= lo && j0 <= hi) ? s0[r] : -INFINITY;
+                s1[r] = (j1 >= lo && j1 <= hi) ? s1[r] : -INFINITY;
             }
         }
 
-        /* online softmax (base 2); rescale only when some row max moved */
-        float mx = -INFINITY;
+        bf16x8 r0[QD], r1[QD];
+        if constexpr (NEXT) {
+            nbase = mu_run;
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-            mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx);
-        const bool moved = m_new > m_run;
-        if (__any(moved)) {
-            const float alpha = moved ? fast_exp2(m_run - m_new) : 1.f;
-            l_run *= alpha;
+            for (int e = 0; e < 16; e++)
+                n0_[e] = n1_[e] = -mu_run;
 #pragma unroll
-            for (int dt = 0; dt < 8; dt++)
-                o[dt] *= alpha;
+            for (int ks = 0; ks < QD; ks++) {
+                r0[ks] = lds_read16(lds, kaddr(ks, kbuf_next));
+                r1[ks] = lds_read16(lds, kaddr(ks, kbuf_next) + 16384);
+            }
         }
-        m_run = m_new;
-        const float mu = m_run == -INFINITY ? 0.f : m_run;
+        float mx = -INFINITY, lsum = 0.f;
         bf16x8 pf[4];
-        float lsum = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const float p0 = fast_exp2(s0[r] - mu), p1 = fast_exp2(s1[r] - mu);
-            lsum += p0 + p1;
-            pf[(r >> 3)][r & 7] = f2bf(p0);
-            pf[2 + (r >> 3)][r & 7] = f2bf(p1);
+        for (int ks = 0; ks < 16; ks++) {
+            if constexpr (NEXT) {
+                const bf16x8 a0 = r0[ks % QD], a1 = r1[ks % QD];
+                if (ks + QD < 16) {
+                    r0[ks % QD] = lds_read16(lds, kaddr(ks + QD, kbuf_next));
+                    r1[ks % QD] = lds_read16(lds, kaddr(ks + QD, kbuf_next) + 16384);
+                }
+                n0_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], n0_, 0, 0, 0);
+                n1_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[ks], n1_, 0, 0, 0);
+            }
+            if (ks < 4) { /* row max, 8 scores per k-step */
+#pragma unroll
+                for (int r = 4 * ks; r < 4 * ks + 4; r++)
+                    mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+            } else if (ks == 4) {
+                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx),
+                                                                 __float_as_uint(mx), false, false);
+                mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+                const float m_true = mx + sbase;
+                const bool grow = m_true > m_run + TAU;
+                const float m_new = grow ? m_true : m_run;
+                const float mu_new = m_new == -INFINITY ? 0.f : m_new;
+                const float dshift = mu_new - sbase;
+                if (__any(dshift != 0.f)) { /* rare: the max moved, or S predates a move */
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        s0[r] -= dshift;
+                        s1[r] -= dshift;
+                    }
+                    const float alpha = grow ? fast_exp2(m_run - m_new) : 1.f;
+                    if (__any(grow)) {
+                        l_run *= alpha;
+#pragma unroll
+                        for (int dt = 0; dt < 8; dt++)
+                            o[dt] *= alpha;
+                    }
+                }
+                m_run = m_new;
+                mu_run = mu_new;
+                sbase = mu_new;
+            } else { /* exponentials: score pairs (2q, 2q+1), q in [lo, hi) */
+                const int lo = (ks - 5) * 16 / 11, hi = (ks - 4) * 16 / 11;
+#pragma unroll
+                for (int q2 = lo; q2 < hi; q2++) {
+                    const int v = 2 * q2;
+                    const float x0 = v < 16 ? s0[v] : s1[v - 16];
+                    const float x1 = v < 16 ? s0[v + 1] : s1[v - 15];
+                    const float p0 = fast_exp2(x0), p1 = fast_exp2(x1);
+                    lsum += p0 + p1;
+                    const int blk = (v < 16 ? 0 : 2) + ((v & 15) >> 3), e = v & 7;
+                    pf[blk][e] = f2bf(p0);
+                    pf[blk][e + 1] = f2bf(p1);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         l_run += lsum;
 
         /* O^T += V^T P^T */
+        bf16x8 vr[VD];
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const int c = 2 * s + h;
+        for (int t = 0; t < VD; t++)
+            vr[t] = lds_read16(lds, vaddr(t, vbuf));
 #pragma unroll
-            for (int dt = 0; dt < 8; dt++) {
-                const int d = 32 * dt + col;
-                bf16x8 a = *(const bf16x8 *)(vt + d * 128 + ((c ^ swz_v(d)) << 4));
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[s], o[dt], 0, 0, 0);
-            }
+        for (int t = 0; t < 32; t++) {
+            const bf16x8 a = vr[t % VD];
+            if (t + VD < 32)
+                vr[t % VD] = lds_read16(lds, vaddr(t + VD, vbuf));
+            o[t & 7] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[t >> 3], o[t & 7], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
-
-        if (more)
-            store_tile<NT>(smem + ((i + 1) & 1) * BUF_BYTES, stage);
+        wait_tile_loads();
         __syncthreads();
+    };
+
+    /* unrolled by two so buffer indices are compile-time; the last tile has
+     * no successor */
+    const std::true_type more{};
+    const std::false_type last{};
+    int i = 0;
+    for (; i + 2 < ntl; i += 2) {
+        step(more, i, sa0, sa1, sbase_a, sb0, sb1, sbase_b, 1, 0);
+        step(more, i + 1, sb0, sb1, sbase_b, sa0, sa1, sbase_a, 0, 1);
+    }
+    if (ntl - i == 2) {
+        step(more, i, sa0, sa1, sbase_a, sb0, sb1, sbase_b, 1, 0);
+        step(last, i + 1, sb0, sb1, sbase_b, sa0, sa1, sbase_a, 0, 1);
+    } else {
+        step(last, i, sa0, sa1, sbase_a, sb0, sb1, sbase_b, 1, 0);
     }
 
     /* ---- epilogue: normalise, gate, store ---- */
@@ -391,8 +513,7 @@ extern "C" hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_
         return hipSuccess;
     if (Hq != 4 * Hkv || P < 0 || p_stride % 64 != 0 || o_stride % 64 != 0)
         return hipErrorInvalidValue;
-    constexpr int TG = 1;
-    const int ntile = CEIL_DIV(N, QW * TG);
+    const int ntile = CEIL_DIV(N, QW);
     int nblk;
     if (8 % Hkv == 0) {
         const int G = 8 / Hkv;
@@ -400,7 +521,7 @@ extern "C" hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_
     } else {
         nblk = ntile * Hkv;
     }
-    hipLaunchKernelGGL(attention_kernel<TG>, dim3((unsigned)nblk), dim3(256 * TG), 0, stream,
+    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)nblk), dim3(256), 0, stream,
                        (const bf16 *)q, (const bf16 *)gate, gate_tok_stride, gate_head_stride,
                        (const bf16 *)pk, (const bf16 *)pvt, P, p_stride, (const bf16 *)ok,
                        (const bf16 *)ovt, o_stride, own_base, N, Hq, Hkv, ntile, (bf16 *)out);
