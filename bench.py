@@ -236,22 +236,27 @@ def main():
                    "vocab": 248320, "weights_gib": round(e2e["info"]["weight_gib"], 2)},
     }
     if not a.no_kernels:
+        from cujev import kernel_bench
         att = attention_roofline()
         log(f"attention config 3: {att['us']:.1f} us, {att['tflops']:.1f} TFLOP/s")
         res["roofline"] = {"kernel": "attention_kernel (ops library), config 3",
                            "bound": "mfma", "achieved": round(att["tflops"], 2),
                            "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                            "frac": round(att["tflops"] / PEAK_BF16_TFLOPS, 4),
-                           "traffic": None, "us_per_launch": round(att["us"], 2),
+                           "traffic": kernel_bench.measured_traffic("attention"),
+                           "traffic_source": "rocprofv3 --pmc FETCH_SIZE x2 + WRITE_SIZE x1 "
+                                             "(copy-calibrated), bytes per launch",
+                           "us_per_launch": round(att["us"], 2),
                            "flop_per_launch": att["flop"]}
         gdn = gdn_roofline()
         log(f"gdn config 2 prefill: {gdn['us']:.1f} us, {gdn['gbs']:.1f} GB/s")
-        res["gdn_roofline"] = {"kernel": "gdn_conv_prep + gdn_chunk_a + gdn_chunk_b, config 2 "
-                                         "T=2048 prefill", "bound": "hbm",
+        res["gdn_roofline"] = {"kernel": "gdn_conv_prep + conv_tail + chunk_a + chunk_b + "
+                                         "norm_gate, config 2 T=2048 prefill", "bound": "hbm",
                                "achieved": round(gdn["gbs"], 1), "peak": PEAK_HBM_GBS,
                                "unit": "GB/s", "frac": round(gdn["gbs"] / PEAK_HBM_GBS, 4),
                                "us_per_layer": round(gdn["us"], 2),
-                               "compulsory_bytes": gdn["bytes"]}
+                               "compulsory_bytes": gdn["bytes"],
+                               "traffic": kernel_bench.measured_traffic("gdn")}
     if not a.no_cpu_baseline:
         torch.cuda.empty_cache()
         base, parity = cpu_baseline(ckpt, e2e["first_req"], e2e["first_out"], e2e["first_full"])

@@ -13,6 +13,25 @@ from __future__ import annotations
 
 import sys
 
+# HBM traffic per launch, measured with rocprofv3 --pmc on MI355X (one
+# counter group per run): FETCH_SIZE and WRITE_SIZE in KiB per dispatch,
+# summed over the kernels of the case. A plain 256 MiB device copy reads
+# 131084 KiB of FETCH_SIZE and 262144 KiB of WRITE_SIZE, so FETCH_SIZE is
+# scaled by 2 and WRITE_SIZE by 1. The figures belong to the kernels of this
+# tree; re-measure after changing a kernel.
+COPY_SCALE = {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0}
+MEASURED_KIB = {
+    "attention": {"FETCH_SIZE": 115282.3, "WRITE_SIZE": 32872.3},
+    "gdn": {"FETCH_SIZE": 17640.4 + 36.5 + 16995.0 + 37040.1 + 24594.2,
+            "WRITE_SIZE": 33280.1 + 96.0 + 73734.8 + 34816.0 + 16384.0},
+}
+
+
+def measured_traffic(case):
+    """HBM bytes per launch of a case from the counter figures above."""
+    kib = MEASURED_KIB[case]
+    return int(sum(kib[c] * COPY_SCALE[c] for c in kib) * 1024)
+
 
 def attention_case():
     import torch
