@@ -94,34 +94,62 @@ def tensor_shapes(cfg):
     return out
 
 
-def write_checkpoint(path, cfg, *, seed=0, std=0.02, norm_std=0.0, device="cpu"):
-    """Write config.json + model.safetensors under `path`; returns the path."""
+def write_checkpoint(path, cfg, *, seed=0, std=0.02, norm_std=0.0, device="cpu",
+                     generator="torch"):
+    """Write config.json + model.safetensors under `path`; returns the path.
+
+    generator="torch" draws with torch's generator on `device` (fast for the
+    multi-GiB shapes); generator="numpy" draws with numpy's PCG64, whose
+    streams are the same on every host, so the file is bit-identical wherever
+    it is rebuilt (used for committed golden vectors)."""
+    import numpy as np
     import torch
     from safetensors.torch import save_file
 
     path = Path(path)
     path.mkdir(parents=True, exist_ok=True)
-    gen = torch.Generator(device=device).manual_seed(seed)
+    if generator == "numpy":
+        rng = np.random.default_rng(seed)
+
+        def randn(shape):
+            return torch.from_numpy(rng.standard_normal(shape, dtype=np.float32))
+
+        def rand(shape):
+            return torch.from_numpy(rng.random(shape, dtype=np.float32))
+        dev = "cpu"
+    else:
+        gen = torch.Generator(device=device).manual_seed(seed)
+
+        def randn(shape):
+            return torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
+
+        def rand(shape):
+            return torch.rand(shape, generator=gen, device=device, dtype=torch.float32)
+        dev = device
     tensors = {}
     for name, shape in tensor_shapes(cfg):
         leaf = name.rsplit(".", 1)[0] if name.endswith(".weight") else name
         if len(shape) >= 2:
-            t = torch.randn(shape, generator=gen, device=device, dtype=torch.float32) * std
-            t = t.to(torch.bfloat16)
+            t = (randn(shape) * std).to(torch.bfloat16)
         elif name.endswith("A_log"):
-            u = torch.rand(shape, generator=gen, device=device, dtype=torch.float32) * 16.0
-            t = torch.log(u.clamp_min(1e-3))
+            u = (rand(shape) * 16.0).clamp_min(1e-3)
+            if generator == "numpy":  # scalar libm log: no vector-path ulp differences
+                import math
+                t = torch.tensor([math.log(float(x)) for x in u.reshape(-1)],
+                                 dtype=torch.float32).reshape(shape)
+            else:
+                t = torch.log(u)
         elif name.endswith("dt_bias"):
-            t = torch.ones(shape, dtype=torch.float32, device=device)
+            t = torch.ones(shape, dtype=torch.float32, device=dev)
         elif leaf.endswith("linear_attn.norm"):
-            t = torch.ones(shape, dtype=torch.float32, device=device)
+            t = torch.ones(shape, dtype=torch.float32, device=dev)
             if norm_std > 0:
-                t = t + torch.randn(shape, generator=gen, device=device) * norm_std
+                t = t + randn(shape) * norm_std
             t = t.to(torch.bfloat16)
         else:  # zero-centred RMSNorm weights
-            t = torch.zeros(shape, dtype=torch.float32, device=device)
+            t = torch.zeros(shape, dtype=torch.float32, device=dev)
             if norm_std > 0:
-                t = t + torch.randn(shape, generator=gen, device=device) * norm_std
+                t = t + randn(shape) * norm_std
             t = t.to(torch.bfloat16)
         tensors[name] = t.cpu().contiguous()
     save_file(tensors, str(path / "model.safetensors"), metadata={"format": "pt"})

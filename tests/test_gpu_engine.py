@@ -177,3 +177,34 @@ def test_timing_is_reported(engine):
     t = engine.last_timing()
     assert t.prefill_tokens == 100 and t.eval_tokens == 4 and t.eval_branches == 2
     assert t.prefill_ms > 0 and t.eval_ms > 0
+
+
+def test_golden_transformers_logits(tmp_path):
+    """The engine on the micro checkpoint of tests/golden against transformers'
+    float32 logits stored there: state = first half of each sequence, one
+    branch = the rest, full-vocabulary readout."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    import make_golden
+
+    g = np.load(Path(__file__).resolve().parent / "golden" / "qwen35_micro.npz",
+                allow_pickle=False)
+    _, digest = make_golden.build_checkpoint(tmp_path)
+    assert digest == str(g["checkpoint_sha256"])
+    e = Engine(str(tmp_path), max_state_tokens=256, max_branch_tokens=256, max_branches=4,
+               max_candidates=512)
+    try:
+        off = 0
+        for n, ref in zip(g["lengths"], g["logits"]):
+            ids = [int(x) for x in g["ids"][off:off + n]]
+            off += n
+            if n < 2:
+                continue
+            cut = n // 2
+            e.prefill(ids[:cut])
+            out = e.eval_full_logits([Branch(ids[cut:], [])])[0]
+            check_probs(np.asarray(out, np.float64), ref.astype(np.float64),
+                        f"golden len {n}")
+    finally:
+        e.close()
