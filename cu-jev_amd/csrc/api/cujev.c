@@ -23,6 +23,7 @@ API void cujev_model_close(cujev_model *m) {
         return;
     if (m->stream)
         hipStreamSynchronize(m->stream);
+    cujev_graphs_forget(m, NULL);
     cujev_gemm_destroy(m->gemm);
     if (m->h_meta)
         hipHostFree(m->h_meta);
@@ -128,6 +129,10 @@ API cujev_status cujev_model_info_get(const cujev_model *m, cujev_model_info *o)
 API void cujev_state_destroy(cujev_state *st) {
     if (!st)
         return;
+    if (st->model) {
+        hipStreamSynchronize(st->model->stream);
+        cujev_graphs_forget(st->model, st);
+    }
     cujev_arena_free(&st->mem);
     free(st->kv_k);
     free(st->kv_vt);
@@ -316,12 +321,9 @@ API cujev_status cujev_eval(cujev_model *m, cujev_state *st, const cujev_branch 
                                           cand, ncand, maxc, &d_cand, &d_ncand);
         if (s != CUJEV_OK)
             goto sync_out;
-        if (maxc > 0) {
-            e = k_readout(m->hsel, m->lm_head, d_cand, d_ncand, maxc, m->d_logits, maxc, B,
-                          m->cfg.hidden_size, m->stream);
-            if (e == hipSuccess)
-                e = hipMemcpy2DAsync(logits_out, (size_t)ld * 4, m->d_logits, (size_t)maxc * 4,
-                                     (size_t)maxc * 4, (size_t)B, hipMemcpyDeviceToHost, m->stream);
+        if (maxc > 0) { /* the forward ran the readout into d_logits[B][maxc] */
+            e = hipMemcpy2DAsync(logits_out, (size_t)ld * 4, m->d_logits, (size_t)maxc * 4,
+                                 (size_t)maxc * 4, (size_t)B, hipMemcpyDeviceToHost, m->stream);
             if (e != hipSuccess) {
                 s = cujev_fail(CUJEV_ERR_CUDA, "readout: %s", hipGetErrorString(e));
                 goto sync_out;

@@ -41,16 +41,192 @@ static cujev_status check(cujev_model *m, hipError_t launch, const char *what, i
 
 #define K_TRY(call, what, layer) CUJEV_TRY(check(m, (call), (what), (layer)))
 
+/* Everything the launch sequence needs besides the model and the state. */
+typedef struct {
+    cujev_fwd_mode mode;
+    int N, B, P, nc, maxc;
+    const int32_t *tok, *pos, *base, *rows, *cand, *ncand; /* device metadata */
+    cujev_chunks chunks;
+} fwd_launch;
+
+/* The kernels of one forward (and the candidate readout); no host sync. */
+static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch *a) {
+    const cujev_config *c = &m->cfg;
+    const int H = c->hidden_size, I = c->intermediate_size, N = a->N, B = a->B, P = a->P;
+    const cujev_fwd_mode mode = a->mode;
+    const float eps = c->rms_norm_eps;
+    hipStream_t s = m->stream;
+    const cujev_gdn_scratch gws = cujev_gdn_scratch_carve(m->gdn_scratch, a->nc, m->Hv);
+    const float q_scale = (1.0f / sqrtf((float)m->D)) * 1.4426950408889634f;
+
+    K_TRY(k_embed(a->tok, m->embed, m->x, N, H, s), "embed", -1);
+    K_TRY(k_add_rmsnorm(m->x, NULL, m->layers[0].in_norm, m->xb, N, H, eps, NULL, 0, s), "norm", 0);
+
+    for (int l = 0; l < c->num_layers; l++) {
+        cujev_layer *ly = &m->layers[l];
+        if (ly->type == CUJEV_LAYER_FULL) {
+            K_TRY(k_gemm(m->gemm, m->xb, ly->w_qkv, m->proj, 0, N, m->w_attn, H, s), "gemm qkv", l);
+            bf16_t *kdst, *vdst;
+            int kstride;
+            if (mode == CUJEV_FWD_PREFILL) {
+                kdst = st->kv_k[l];
+                vdst = st->kv_vt[l];
+                kstride = m->state_stride;
+            } else {
+                kdst = m->br_k;
+                vdst = m->br_vt;
+                kstride = m->branch_stride;
+            }
+            K_TRY(k_attn_prep(m->proj, m->w_attn, ly->q_norm, ly->k_norm, a->pos, N, m->Hq,
+                              m->Hkv, c->rotary_dim, m->rope, eps, q_scale, m->q, kdst, vdst,
+                              kstride, s),
+                  "attn_prep", l);
+            K_TRY(k_attention(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l], st->kv_vt[l],
+                              P, m->state_stride, kdst, vdst, kstride, a->base, N, m->Hq,
+                              m->Hkv, m->mix_out, s),
+                  "attention", l);
+            K_TRY(k_gemm(m->gemm, m->mix_out, ly->w_o, m->y, 0, N, H, m->Hq * m->D, s), "gemm o",
+                  l);
+        } else {
+            K_TRY(k_gemm(m->gemm, m->xb, ly->w_in, m->proj, 0, N, m->w_gdn, H, s), "gemm in", l);
+            const float *conv_in = mode == CUJEV_FWD_EVAL ? st->conv[l] : NULL;
+            float *conv_out = mode == CUJEV_FWD_PREFILL ? st->conv[l] : NULL;
+            K_TRY(k_gdn_conv_prep(m->proj, m->w_gdn, ly->conv_w, conv_in, conv_out, N, a->base,
+                                  ly->A_neg_exp, ly->dt_bias, N, m->Hk, m->Hv, m->gq, m->gk, m->gv,
+                                  m->gg, m->gbeta, s),
+                  "gdn_conv_prep", l);
+            const float *S_in = mode == CUJEV_FWD_EVAL ? st->S[l] : NULL;
+            float *S_out = mode == CUJEV_FWD_PREFILL ? st->S[l] : NULL;
+            K_TRY(k_gdn_scan(m->gq, m->gk, m->gv, m->gg, m->gbeta, &a->chunks, S_in, S_out,
+                             m->proj + m->C, m->w_gdn, ly->g_norm, eps, m->Hk, m->Hv, m->mix_out,
+                             &gws, N, s),
+                  "gdn_scan", l);
+            K_TRY(k_gemm(m->gemm, m->mix_out, ly->w_out, m->y, 0, N, H, m->V, s), "gemm out", l);
+        }
+        K_TRY(k_add_rmsnorm(m->x, m->y, ly->post_norm, m->xb, N, H, eps, NULL, 0, s), "add+norm",
+              l);
+        K_TRY(k_gemm(m->gemm, m->xb, ly->w_gate_up, m->proj, 0, N, 2 * I, H, s), "gemm gate_up", l);
+        K_TRY(k_silu_mul(m->proj, m->act, N, I, s), "silu_mul", l);
+        K_TRY(k_gemm(m->gemm, m->act, ly->w_down, m->y, 0, N, H, I, s), "gemm down", l);
+        if (l + 1 < c->num_layers)
+            K_TRY(k_add_rmsnorm(m->x, m->y, m->layers[l + 1].in_norm, m->xb, N, H, eps, NULL, 0, s),
+                  "add+norm", l);
+        else /* final norm only at the last token of every segment */
+            K_TRY(k_add_rmsnorm(m->x, m->y, m->final_norm, m->hsel, N, H, eps, a->rows, B, s),
+                  "final norm", l);
+    }
+    if (a->cand)
+        K_TRY(k_readout(m->hsel, m->lm_head, a->cand, a->ncand, a->maxc, m->d_logits, a->maxc, B,
+                        H, s),
+              "readout", -1);
+    return CUJEV_OK;
+}
+
+/* ---- captured eval forwards ----------------------------------------------
+ * A launch shape is (state, P, N, B, chunks, candidate width). Its first eval
+ * runs eagerly (this also creates the hipBLASLt plans of its GEMM shapes,
+ * which time candidates with host syncs); the second is captured into a HIP
+ * graph and every later one replays it. Graph nodes are kernels only (no
+ * memset nodes). At most CUJEV_GRAPH_SLOTS shapes are kept (least recently
+ * used goes first); a state's graphs are dropped with the state. */
+static int graphs_enabled(void) {
+    static int cached = -1;
+    if (cached < 0) {
+        const char *e = getenv("CUJEV_GRAPHS");
+        cached = !(e && *e == '0');
+    }
+    return cached && !debug_sync_enabled();
+}
+
+void cujev_graphs_forget(cujev_model *m, const struct cujev_state *st) {
+    for (int i = 0; i < CUJEV_GRAPH_SLOTS; i++) {
+        cujev_graph_slot *g = &m->graphs[i];
+        if (g->st && (!st || g->st == st)) {
+            if (g->exec)
+                hipGraphExecDestroy(g->exec);
+            memset(g, 0, sizeof *g);
+        }
+    }
+}
+
+static cujev_status run_eval(cujev_model *m, cujev_state *st, const fwd_launch *a) {
+    if (!graphs_enabled())
+        return launch_all(m, st, a);
+    cujev_graph_slot *g = NULL, *victim = &m->graphs[0];
+    const int has_cand = a->cand != NULL;
+    for (int i = 0; i < CUJEV_GRAPH_SLOTS; i++) {
+        cujev_graph_slot *x = &m->graphs[i];
+        if (x->st == st && x->P == a->P && x->N == a->N && x->B == a->B && x->nc == a->nc &&
+            x->maxc == a->maxc && x->has_cand == has_cand) {
+            g = x;
+            break;
+        }
+        if (!x->st || (victim->st && x->stamp < victim->stamp))
+            victim = x;
+    }
+    if (!g) {
+        if (victim->exec)
+            hipGraphExecDestroy(victim->exec);
+        memset(victim, 0, sizeof *victim);
+        g = victim;
+        g->st = st;
+        g->P = a->P;
+        g->N = a->N;
+        g->B = a->B;
+        g->nc = a->nc;
+        g->maxc = a->maxc;
+        g->has_cand = has_cand;
+    }
+    g->stamp = ++m->graph_clock;
+    if (g->exec) {
+        hipError_t e = hipGraphLaunch(g->exec, m->stream);
+        return e == hipSuccess ? CUJEV_OK
+                               : cujev_fail(CUJEV_ERR_CUDA, "hipGraphLaunch: %s",
+                                            hipGetErrorString(e));
+    }
+    if (g->seen == 0 || g->seen < 0) {
+        if (g->seen == 0)
+            g->seen = 1;
+        return launch_all(m, st, a);
+    }
+    /* second sighting: capture */
+    hipError_t e = hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+        g->seen = -1;
+        return launch_all(m, st, a);
+    }
+    cujev_status s = launch_all(m, st, a);
+    hipGraph_t graph = NULL;
+    e = hipStreamEndCapture(m->stream, &graph);
+    if (s != CUJEV_OK) {
+        if (graph)
+            hipGraphDestroy(graph);
+        return s;
+    }
+    hipGraphExec_t exec = NULL;
+    if (e == hipSuccess)
+        e = hipGraphInstantiate(&exec, graph, NULL, NULL, 0);
+    if (graph)
+        hipGraphDestroy(graph);
+    if (e != hipSuccess) { /* not capturable here: this shape stays eager */
+        cujev_log(1, "eval graph capture failed (%s); shape N=%d B=%d runs eagerly",
+                  hipGetErrorString(e), a->N, a->B);
+        (void)hipGetLastError();
+        g->seen = -1;
+        return launch_all(m, st, a);
+    }
+    g->exec = exec;
+    e = hipGraphLaunch(exec, m->stream);
+    return e == hipSuccess ? CUJEV_OK
+                           : cujev_fail(CUJEV_ERR_CUDA, "hipGraphLaunch: %s", hipGetErrorString(e));
+}
+
 cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
                                            const int32_t *tokens, int N, const int32_t *seg_start,
                                            const int32_t *seg_len, int B, const int32_t *cand,
                                            const int32_t *ncand, int maxc, int32_t **d_cand,
                                            int32_t **d_ncand) {
-    const cujev_config *c = &m->cfg;
-    const int H = c->hidden_size, I = c->intermediate_size;
     const int P = mode == CUJEV_FWD_EVAL ? st->num_tokens : 0;
-    const float eps = c->rms_norm_eps;
-    hipStream_t s = m->stream;
 
     /* ---- metadata: one packed block, one upload ---- */
     int nc = 0;
@@ -93,73 +269,28 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
         memcpy(h + o_cand, cand, (size_t)B * maxc * 4);
         memcpy(h + o_ncand, ncand, (size_t)B * 4);
     }
-    HIP_TRY(hipMemcpyAsync(m->d_meta, h, o * 4, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(m->d_meta, h, o * 4, hipMemcpyHostToDevice, m->stream));
     const int32_t *d = m->d_meta;
     if (d_cand) {
         *d_cand = cand ? m->d_meta + o_cand : NULL;
         *d_ncand = cand ? m->d_meta + o_ncand : NULL;
     }
+    fwd_launch a;
+    a.mode = mode;
+    a.N = N;
+    a.B = B;
+    a.P = P;
+    a.nc = nc;
+    a.maxc = cand ? maxc : 0;
+    a.tok = d + o_tok;
+    a.pos = d + o_pos;
+    a.base = d + o_base;
+    a.rows = d + o_rows;
+    a.cand = cand ? d + o_cand : NULL;
+    a.ncand = cand ? d + o_ncand : NULL;
     const cujev_chunks chunks = {d + o_ctok, d + o_clen, d + o_sc0, d + o_snc, nc, B};
-    const cujev_gdn_scratch gws = cujev_gdn_scratch_carve(m->gdn_scratch, nc, m->Hv);
-    const float q_scale = (1.0f / sqrtf((float)m->D)) * 1.4426950408889634f;
-
-    K_TRY(k_embed(d + o_tok, m->embed, m->x, N, H, s), "embed", -1);
-    K_TRY(k_add_rmsnorm(m->x, NULL, m->layers[0].in_norm, m->xb, N, H, eps, NULL, 0, s), "norm", 0);
-
-    for (int l = 0; l < c->num_layers; l++) {
-        cujev_layer *ly = &m->layers[l];
-        if (ly->type == CUJEV_LAYER_FULL) {
-            K_TRY(k_gemm(m->gemm, m->xb, ly->w_qkv, m->proj, 0, N, m->w_attn, H, s), "gemm qkv", l);
-            bf16_t *kdst, *vdst;
-            int kstride;
-            if (mode == CUJEV_FWD_PREFILL) {
-                kdst = st->kv_k[l];
-                vdst = st->kv_vt[l];
-                kstride = m->state_stride;
-            } else {
-                kdst = m->br_k;
-                vdst = m->br_vt;
-                kstride = m->branch_stride;
-            }
-            K_TRY(k_attn_prep(m->proj, m->w_attn, ly->q_norm, ly->k_norm, d + o_pos, N, m->Hq,
-                              m->Hkv, c->rotary_dim, m->rope, eps, q_scale, m->q, kdst, vdst,
-                              kstride, s),
-                  "attn_prep", l);
-            K_TRY(k_attention(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l], st->kv_vt[l],
-                              P, m->state_stride, kdst, vdst, kstride, d + o_base, N, m->Hq,
-                              m->Hkv, m->mix_out, s),
-                  "attention", l);
-            K_TRY(k_gemm(m->gemm, m->mix_out, ly->w_o, m->y, 0, N, H, m->Hq * m->D, s), "gemm o",
-                  l);
-        } else {
-            K_TRY(k_gemm(m->gemm, m->xb, ly->w_in, m->proj, 0, N, m->w_gdn, H, s), "gemm in", l);
-            const float *conv_in = mode == CUJEV_FWD_EVAL ? st->conv[l] : NULL;
-            float *conv_out = mode == CUJEV_FWD_PREFILL ? st->conv[l] : NULL;
-            K_TRY(k_gdn_conv_prep(m->proj, m->w_gdn, ly->conv_w, conv_in, conv_out, N, d + o_base,
-                                  ly->A_neg_exp, ly->dt_bias, N, m->Hk, m->Hv, m->gq, m->gk, m->gv,
-                                  m->gg, m->gbeta, s),
-                  "gdn_conv_prep", l);
-            const float *S_in = mode == CUJEV_FWD_EVAL ? st->S[l] : NULL;
-            float *S_out = mode == CUJEV_FWD_PREFILL ? st->S[l] : NULL;
-            K_TRY(k_gdn_scan(m->gq, m->gk, m->gv, m->gg, m->gbeta, &chunks, S_in, S_out,
-                             m->proj + m->C, m->w_gdn, ly->g_norm, eps, m->Hk, m->Hv, m->mix_out,
-                             &gws, N, s),
-                  "gdn_scan", l);
-            K_TRY(k_gemm(m->gemm, m->mix_out, ly->w_out, m->y, 0, N, H, m->V, s), "gemm out", l);
-        }
-        K_TRY(k_add_rmsnorm(m->x, m->y, ly->post_norm, m->xb, N, H, eps, NULL, 0, s), "add+norm",
-              l);
-        K_TRY(k_gemm(m->gemm, m->xb, ly->w_gate_up, m->proj, 0, N, 2 * I, H, s), "gemm gate_up", l);
-        K_TRY(k_silu_mul(m->proj, m->act, N, I, s), "silu_mul", l);
-        K_TRY(k_gemm(m->gemm, m->act, ly->w_down, m->y, 0, N, H, I, s), "gemm down", l);
-        if (l + 1 < c->num_layers)
-            K_TRY(k_add_rmsnorm(m->x, m->y, m->layers[l + 1].in_norm, m->xb, N, H, eps, NULL, 0, s),
-                  "add+norm", l);
-        else /* final norm only at the last token of every segment */
-            K_TRY(k_add_rmsnorm(m->x, m->y, m->final_norm, m->hsel, N, H, eps, d + o_rows, B, s),
-                  "final norm", l);
-    }
-    return CUJEV_OK;
+    a.chunks = chunks;
+    return mode == CUJEV_FWD_EVAL ? run_eval(m, st, &a) : launch_all(m, st, &a);
 }
 
 cujev_status cujev_forward(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,

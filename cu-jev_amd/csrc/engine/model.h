@@ -38,6 +38,18 @@ typedef struct cujev_layer {
     bf16_t *w_down;    /* [H, I] */
 } cujev_layer;
 
+/* Captured eval forwards (see forward.c): one executable graph per launch
+ * shape. Everything a launch argument depends on is in the key; the per-call
+ * metadata lives in fixed device buffers, so a replay only needs the upload. */
+#define CUJEV_GRAPH_SLOTS 8
+typedef struct cujev_graph_slot {
+    const struct cujev_state *st;
+    int P, N, B, nc, maxc, has_cand;
+    int seen; /* eager runs so far; -1: capture failed, this key stays eager */
+    hipGraphExec_t exec;
+    unsigned long long stamp;
+} cujev_graph_slot;
+
 struct cujev_model {
     cujev_config cfg;
     cujev_options opts;
@@ -83,6 +95,8 @@ struct cujev_model {
     float *d_logits; /* [B, max_candidates] */
     float *rope;     /* [max positions][rot/2] (cos, sin) */
     int rope_positions;
+    cujev_graph_slot graphs[CUJEV_GRAPH_SLOTS];
+    unsigned long long graph_clock;
 };
 
 struct cujev_state {
@@ -107,12 +121,18 @@ cujev_status cujev_forward(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
                            const int32_t *tokens, int N, const int32_t *seg_start,
                            const int32_t *seg_len, int B);
 /* Same, also uploading candidate ids (host [B][maxc]) and counts (host [B])
- * with the metadata; their device copies are returned in d_cand / d_ncand. */
+ * with the metadata; their device copies are returned in d_cand / d_ncand.
+ * With candidates the readout runs too: d_logits[B][maxc] holds the
+ * candidate logits. EVAL forwards are replayed from captured HIP graphs
+ * once a launch shape repeats (CUJEV_GRAPHS=0 keeps them eager). */
 cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
                                            const int32_t *tokens, int N, const int32_t *seg_start,
                                            const int32_t *seg_len, int B, const int32_t *cand,
                                            const int32_t *ncand, int maxc, int32_t **d_cand,
                                            int32_t **d_ncand);
+
+/* Drop the captured graphs that use `st` (all of them when st is NULL). */
+void cujev_graphs_forget(cujev_model *m, const struct cujev_state *st);
 
 #ifdef __cplusplus
 }

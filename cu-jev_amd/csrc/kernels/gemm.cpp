@@ -64,14 +64,17 @@ extern "C" void cujev_gemm_destroy(cujev_gemm *g) {
     delete g;
 }
 
-/* Heuristic candidates are timed once on the caller's buffers and stream
- * (the output is simply rewritten), and the fastest is kept for the shape.
- * CUJEV_GEMM_TUNE=0 keeps the heuristic's first choice. */
+/* By default a shape keeps the heuristic's first algorithm, so every engine
+ * instance computes a shape the same way (bit-identical results across
+ * processes). CUJEV_GEMM_TUNE=1 instead times the heuristic's candidates once
+ * on the caller's buffers and stream (the output is simply rewritten) and
+ * keeps the fastest; timing noise can then pick different algorithms in
+ * different processes. */
 static int tuning_enabled(void) {
     static int cached = -1;
     if (cached < 0) {
         const char *e = getenv("CUJEV_GEMM_TUNE");
-        cached = !(e && *e == '0');
+        cached = e && *e == '1';
     }
     return cached;
 }
