@@ -22,6 +22,11 @@ the same checkpoint file and the same first request (the HF-batched method
 of the reference's benchmarks/benefit.py:77-92); it is also the parity check
 of the request's decision probabilities.
 
+The request loop runs in a child process that imports only numpy and the
+ctypes binding, as the reference's Python layer does (python/cujev/_lib.py,
+systemone.py): a process that imported torch first would run the engine on
+torch's bundled HIP runtime and hipBLASLt instead of the system ROCm's.
+
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
 from __future__ import annotations
@@ -73,8 +78,6 @@ def run_e2e(ckpt, steps, warmup, seed=0):
     reqs = [make_request(rng, eng.vocab_size) for _ in range(warmup + steps)]
     first_out = None
     wall, gpu = [], []
-    import torch
-    torch.cuda.synchronize()
     for i, (state, brs) in enumerate(reqs):
         t0 = time.perf_counter()
         eng.prefill(state)
@@ -103,6 +106,34 @@ def run_e2e(ckpt, steps, warmup, seed=0):
     eng.close()
     return dict(wall_ms=wall, gpu_ms=gpu, eval_only_ms=ev_only, first_req=reqs[0],
                 first_out=first_out, first_full=first_full, info=info)
+
+
+def e2e_child(a):
+    """--e2e-child: the request loop without torch in the process; prints one
+    JSON line, the full-vocabulary logits go to a .npy file."""
+    assert "torch" not in sys.modules
+    r = run_e2e(a.ckpt, a.steps, a.warmup)
+    np.save(a.full_out, np.asarray(r["first_full"], np.float32), allow_pickle=False)
+    r["first_full"] = None
+    r["first_out"] = [np.asarray(o, np.float64).tolist() for o in r["first_out"]]
+    r["torch_loaded"] = "torch" in sys.modules
+    print(json.dumps(r), flush=True)
+
+
+def run_e2e_in_child(ckpt, steps, warmup):
+    import subprocess
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        full = os.path.join(d, "full.npy")
+        cmd = [sys.executable, str(Path(__file__).resolve()), "--e2e-child", "--ckpt", ckpt,
+               "--steps", str(steps), "--warmup", str(warmup), "--full-out", full]
+        p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=sys.stderr, text=True)
+        if p.returncode != 0:
+            raise SystemExit(f"e2e child failed with status {p.returncode}")
+        r = json.loads(p.stdout.strip().splitlines()[-1])
+        r["first_full"] = np.load(full, allow_pickle=False)
+    r["first_out"] = [np.asarray(o) for o in r["first_out"]]
+    return r
 
 
 # --------------------------------------------------------------------------
@@ -191,7 +222,11 @@ def main():
     ap.add_argument("--ckpt", default=os.environ.get("CUJEV_BENCH_CKPT", "/tmp/cujev_synth_4b"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--e2e-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--full-out", help=argparse.SUPPRESS)
     a = ap.parse_args()
+    if a.e2e_child:
+        return e2e_child(a)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: the engine is single-device (one process, one "
               "stream per model) and this build runs no multi-GPU path; use --gpus 1.",
@@ -207,7 +242,7 @@ def main():
     torch.cuda.empty_cache()
     log(f"checkpoint ready at {ckpt} ({time.perf_counter() - t0:.1f}s)")
 
-    e2e = run_e2e(ckpt, a.steps, a.warmup)
+    e2e = run_e2e_in_child(ckpt, a.steps, a.warmup)
     wall = e2e["wall_ms"]
     ms = statistics.mean(wall)
     p50 = statistics.median(wall)

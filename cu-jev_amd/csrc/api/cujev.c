@@ -2,6 +2,7 @@
  * branch packing, candidate readout, timing. Behaviour of REF
  * src/api/cujev.c:11-327: same validation order and status codes, same
  * capacity rules, one stream per model, every call synchronous. */
+#include <dlfcn.h>
 #include "engine/model.h"
 #include <math.h>
 
@@ -16,6 +17,32 @@ API void cujev_options_default(cujev_options *o) {
     o->max_branch_tokens = 4096;
     o->max_branches = 256;
     o->max_candidates = 256;
+}
+
+/* Tuned hipBLASLt algorithms: CUJEV_GEMM_TABLE, else
+ * gemm_table_gfx950_hipblaslt<version>.txt next to this library, for the
+ * hipBLASLt the process actually loaded (a process that imported torch first
+ * runs on torch's bundled copy, others on the system one). A missing or
+ * foreign-version table leaves every shape on hipBLASLt's heuristic. */
+static void load_gemm_table(cujev_model *m) {
+    char buf[4096];
+    const char *path = getenv("CUJEV_GEMM_TABLE");
+    if (!path) {
+        Dl_info info;
+        if (!dladdr((void *)load_gemm_table, &info) || !info.dli_fname)
+            return;
+        snprintf(buf, sizeof buf, "%s", info.dli_fname);
+        char *slash = strrchr(buf, '/');
+        const size_t dir = slash ? (size_t)(slash - buf + 1) : 0;
+        snprintf(buf + dir, sizeof buf - dir, "gemm_table_gfx950_hipblaslt%d.txt",
+                 cujev_gemm_version(m->gemm));
+        path = buf;
+    }
+    const int n = cujev_gemm_load_table(m->gemm, path);
+    if (n >= 0)
+        cujev_log(m->opts.verbose, "gemm table: %d tuned shapes from %s", n, path);
+    else if (n == -2)
+        cujev_log(1, "gemm table %s was made with another hipBLASLt version; ignored", path);
 }
 
 API void cujev_model_close(cujev_model *m) {
@@ -99,6 +126,8 @@ API cujev_status cujev_model_open(const char *dir, const cujev_options *opts, cu
         s = cujev_model_alloc_workspace(m);
     if (s == CUJEV_OK && cujev_gemm_create(&m->gemm, m->gemm_ws, m->gemm_ws_bytes) != 0)
         s = cujev_fail(CUJEV_ERR_CUDA, "hipblasLtCreate failed");
+    if (s == CUJEV_OK)
+        load_gemm_table(m);
     if (s == CUJEV_OK && (e = hipStreamSynchronize(m->stream)) != hipSuccess)
         s = cujev_fail(CUJEV_ERR_CUDA, "%s", hipGetErrorString(e));
     if (s != CUJEV_OK) {

@@ -173,6 +173,14 @@ int cujev_gemm_create(cujev_gemm **out, void *workspace, size_t ws_bytes);
 void cujev_gemm_destroy(cujev_gemm *g);
 hipError_t k_gemm(cujev_gemm *g, const bf16_t *X, const bf16_t *W, void *Y, int f32out, int N,
                   int M, int K, hipStream_t stream);
+/* Tuned-algorithm table (text file, see gemm.cpp); returns entries loaded,
+ * -1 unreadable, -2 made with another hipBLASLt version. */
+int cujev_gemm_load_table(cujev_gemm *g, const char *path);
+int cujev_gemm_version(cujev_gemm *g);
+/* Exhaustive hipBLASLt search for one shape; records the winner. */
+int cujev_gemm_tune(cujev_gemm *g, const bf16_t *X, const bf16_t *W, void *Y, int f32out, int N,
+                    int M, int K, hipStream_t stream, int *best_index, float *best_us,
+                    float *heuristic_us);
 
 #ifdef __cplusplus
 }

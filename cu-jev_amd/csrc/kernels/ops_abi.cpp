@@ -51,6 +51,34 @@ EXPORT int cujev_op_gemm(const void *X, const void *W, void *Y, int f32out, int 
                            (hipStream_t)stream),
                     "gemm");
 }
+EXPORT int cujev_op_gemm_tune(const void *X, const void *W, void *Y, int f32out, int N, int M,
+                              int K, void *workspace, size_t ws_bytes, void *stream,
+                              int *best_index, float *best_us, float *heuristic_us) {
+    if (N <= 0 || M <= 0 || K <= 0 || !X || !W || !Y || !best_index || !best_us || !heuristic_us)
+        return fail(1, "gemm_tune: bad arguments");
+    if (!g_gemm || g_gemm_ws != workspace) {
+        if (g_gemm)
+            cujev_gemm_destroy(g_gemm);
+        g_gemm = nullptr;
+        if (cujev_gemm_create(&g_gemm, workspace, ws_bytes) != 0)
+            return fail(4, "gemm_tune: hipblasLtCreate failed");
+        g_gemm_ws = workspace;
+    }
+    if (cujev_gemm_tune(g_gemm, (const bf16_t *)X, (const bf16_t *)W, Y, f32out, N, M, K,
+                        (hipStream_t)stream, best_index, best_us, heuristic_us) != 0)
+        return fail(4, "gemm_tune: no supported hipBLASLt algorithm ran");
+    return 0;
+}
+
+EXPORT int cujev_ops_blaslt_version(void) {
+    cujev_gemm *g = nullptr;
+    if (cujev_gemm_create(&g, nullptr, 0) != 0)
+        return -1;
+    const int v = cujev_gemm_version(g);
+    cujev_gemm_destroy(g);
+    return v;
+}
+
 EXPORT const char *cujev_ops_last_error(void) { return g_err; }
 
 EXPORT int cujev_op_rope_table(double theta, int rot, int npos, float *table) {

@@ -57,6 +57,12 @@ def load():
     lib.cujev_ops_last_error.restype = C.c_char_p
     lib.cujev_ops_gdn_scratch_bytes.argtypes = [_I, _I, _I]
     lib.cujev_ops_gdn_scratch_bytes.restype = C.c_size_t
+    lib.cujev_ops_blaslt_version.argtypes = []
+    lib.cujev_ops_blaslt_version.restype = _I
+    lib.cujev_op_gemm_tune.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, _I, _I, _I, _I,
+                                       C.c_void_p, C.c_size_t, C.c_void_p,
+                                       C.POINTER(_I), C.POINTER(C.c_float), C.POINTER(C.c_float)]
+    lib.cujev_op_gemm_tune.restype = _I
     for name, args in _SIGS.items():
         fn = getattr(lib, name)
         fn.argtypes = args
@@ -66,7 +72,8 @@ def load():
 
 
 def exported_symbols():
-    return ["cujev_ops_kv_stride", "cujev_ops_last_error", "cujev_ops_gdn_scratch_bytes", *_SIGS]
+    return ["cujev_ops_kv_stride", "cujev_ops_last_error", "cujev_ops_gdn_scratch_bytes",
+            "cujev_ops_blaslt_version", "cujev_op_gemm_tune", *_SIGS]
 
 
 def _ptr(t):
@@ -167,3 +174,26 @@ def gemm(X, W, Y, f32out=False):
     M = W.shape[0]
     _call("cujev_op_gemm", _ptr(X), _ptr(W), _ptr(Y), int(bool(f32out)), N, M, K, _ptr(_gemm_ws),
           _gemm_ws.numel(), _stream())
+
+
+def blaslt_version() -> int:
+    return load().cujev_ops_blaslt_version()
+
+
+def gemm_tune(X, W, Y, f32out=False):
+    """Exhaustive hipBLASLt search for Y = X W^T: (solution index, best us,
+    heuristic us)."""
+    import torch
+    global _gemm_ws
+    if _gemm_ws is None:
+        _gemm_ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    N, K = X.shape
+    M = W.shape[0]
+    idx, best, heur = _I(0), C.c_float(0), C.c_float(0)
+    lib = load()
+    st = lib.cujev_op_gemm_tune(_ptr(X), _ptr(W), _ptr(Y), int(bool(f32out)), N, M, K,
+                                _ptr(_gemm_ws), _gemm_ws.numel(), _stream(), C.byref(idx),
+                                C.byref(best), C.byref(heur))
+    if st != 0:
+        raise OpsError(f"cujev_op_gemm_tune: status {st}: {lib.cujev_ops_last_error().decode()}")
+    return idx.value, best.value, heur.value

@@ -40,6 +40,18 @@ const char *cujev_ops_last_error(void);
 int cujev_op_gemm(const void *X, const void *W, void *Y, int f32out, int N, int M, int K,
                   void *workspace, size_t ws_bytes, void *stream);
 
+/* No counterpart in the reference (cuBLAS picks its own algorithm there):
+ * times every hipBLASLt solution that supports the cujev_op_gemm problem
+ * (N, M, K, f32out) on these buffers (Y is overwritten) and returns the
+ * fastest one's solution index with its time and the time of hipBLASLt's
+ * heuristic first choice, in microseconds per launch. The indices feed the
+ * tuned-algorithm table the engine reads at model open. */
+int cujev_op_gemm_tune(const void *X, const void *W, void *Y, int f32out, int N, int M, int K,
+                       void *workspace, size_t ws_bytes, void *stream, int *best_index,
+                       float *best_us, float *heuristic_us);
+/* hipBLASLt library version (solution indices are only valid for it). */
+int cujev_ops_blaslt_version(void);
+
 /* Fills the device RoPE table used by cujev_op_attn_prep: table[p][i] =
  * (cos a, sin a), a = fp32(fp32(theta^(-2i/rot)) * p), p < npos, i < rot/2
  * (npos * rot floats). Synchronous. Replaces the reference's per-launch
