@@ -416,16 +416,44 @@ __global__ __launch_bounds__(320) void attn_prep_kernel(
     const bool rotates = lane < 2 * half_lanes;
     const bool first = lane < half_lanes;
     const int fi0 = first ? 4 * lane : 4 * lane - hr;
-    for (int t = 0; t < nt; t++) {
+    /* every load of the 16 tokens is issued up front: the rows, the positions
+     * (lane t holds token t's), and each token's RoPE row one token ahead */
+    const bf16 *src0 = wave < 4 ? proj + (kh * 4 + wave) * 512 : proj + Hq * 512 + kh * 256;
+    bf16x4 raw[PREP_TOK];
+#pragma unroll
+    for (int t = 0; t < PREP_TOK; t++) {
+        raw[t] = bf16x4{};
+        if (t < nt)
+            raw[t] = *(const bf16x4 *)(src0 + (size_t)(n0 + t) * ps + 4 * lane);
+    }
+    const int pos_lane = lane < nt ? pos[n0 + lane] : 0;
+    float2 cs_next[4] = {};
+    auto load_rope = [&](int t, float2 (&c)[4]) {
+        const int p = __shfl(pos_lane, t, 64);
+        if (rotates) {
+            const float2 *row = rope + (size_t)p * hr + fi0;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                c[e] = row[e];
+        }
+    };
+    load_rope(0, cs_next);
+#pragma unroll
+    for (int t = 0; t < PREP_TOK; t++) {
+        if (t >= nt)
+            break;
         const int nn = n0 + t;
-        const bf16 *src = wave < 4 ? proj + (size_t)nn * ps + (kh * 4 + wave) * 512
-                                   : proj + (size_t)nn * ps + Hq * 512 + kh * 256;
-        bf16x4 raw = *(const bf16x4 *)(src + 4 * lane);
+        float2 cs_cur[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            cs_cur[e] = cs_next[e];
+        if (t + 1 < nt)
+            load_rope(t + 1, cs_next);
         float x[4];
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            x[e] = bf2f(raw[e]);
+            x[e] = bf2f(raw[t][e]);
             ss += x[e] * x[e];
         }
         ss = wave_sum(ss);
@@ -438,10 +466,9 @@ __global__ __launch_bounds__(320) void attn_prep_kernel(
         for (int e = 0; e < 4; e++)
             partner[e] = __shfl_xor(x[e], half_lanes, 64);
         if (rotates) {
-            const float2 *cs_row = rope + (size_t)pos[nn] * hr + fi0;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float2 c = cs_row[e];
+                const float2 c = cs_cur[e];
                 x[e] = first ? x[e] * c.x - partner[e] * c.y : x[e] * c.x + partner[e] * c.y;
             }
         }

@@ -36,6 +36,18 @@ DEV float silu_f(float x) { return x / (1.f + fast_exp(-x)); }
 /* log(1+e^x), linear above 20 like torch.nn.functional.softplus. */
 DEV float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 
+/* Workgroup barrier for LDS traffic only: this wave's LDS operations are
+ * complete (so its writes are visible and its reads have returned), then
+ * s_barrier. Unlike __syncthreads() it does not wait for the wave's global
+ * stores to reach memory, so stores issued before it keep streaming. Global
+ * data another wave reads needs __syncthreads(); LDS written by buffer
+ * loads (...lds) needs an explicit vmcnt wait first. */
+DEV void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 /* Wave64 reductions (butterfly over all 64 lanes). */
 DEV float wave_sum(float v) {
 #pragma unroll

@@ -110,12 +110,16 @@ __global__ __launch_bounds__(256) void gdn_conv_prep_kernel(
         dst = vo + (size_t)(head - 2 * Hk) * DV;
     }
     const int tok_stride = head < 2 * Hk ? Hk * DK : Hv * DV;
+    int local_of[PREP_T]; /* all segment offsets fetched up front, not per step */
+#pragma unroll
+    for (int j = 0; j < PREP_T; j++)
+        local_of[j] = n0 + j < N ? n0 + j - own_base[n0 + j] : 0;
 #pragma unroll
     for (int j = 0; j < PREP_T; j++) {
         const int n = n0 + j;
         if (n >= N)
-            break; /* uniform over the group */
-        const int local = n - own_base[n];
+            continue; /* uniform over the group */
+        const int local = local_of[j];
         float y[8];
 #pragma unroll
         for (int e = 0; e < 8; e++)
@@ -239,7 +243,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
         *(bf16x8 *)&sm.Q[t][c8] = qv;
         *(bf16x8 *)&sm.V[t][c8] = vv;
     }
-    __syncthreads();
+    lds_barrier();
     const float Glast = sm.G[CH - 1];
     /* q e^G straight to HBM (16 lanes per row: coalesced) */
     for (int i = tid; i < CH * (DK / 8); i += 256) {
@@ -265,7 +269,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
             sm.Vt[c8 + e][t] = f2bf(bf2f(vv[e]) * sv);
         }
     }
-    __syncthreads(); /* V rows are free from here on: QK^T staging */
+    lds_barrier(); /* V rows are free from here on: QK^T staging */
 
     /* K K^T and Q K^T: wave w owns the 32x32 tile (w>>1, w&1) of both */
     {
@@ -291,7 +295,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
             qks[i * (CH + 8)] = f2bf(i >= j ? qk[r] * dec : 0.f);
         }
     }
-    __syncthreads();
+    lds_barrier();
     /* masked QK^T rows to HBM; T = (I + A)^-1 diagonal blocks by forward
      * substitution (wave w inverts block w, lane c < 16 owns column c) */
     for (int i = tid; i < CH * (CH / 8); i += 256) {
@@ -316,7 +320,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
     /* ... then the strictly lower blocks by distance from the diagonal:
      * T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj */
     for (int lvl = 1; lvl < 4; lvl++) {
-        __syncthreads();
+        lds_barrier();
         const int nb = 4 - lvl;
         for (int e = tid; e < nb * 256; e += 256) {
             const int b = e >> 8, r = (e >> 4) & 15, c = e & 15;
@@ -328,7 +332,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
                     acc += sm.A[16 * bi + r][16 * bk + x] * sm.T[16 * bk + x][16 * bj + c];
             sm.M[b][r][c] = acc;
         }
-        __syncthreads();
+        lds_barrier();
         for (int e = tid; e < nb * 256; e += 256) {
             const int b = e >> 8, r = (e >> 4) & 15, c = e & 15;
             const int bj = b, bi = b + lvl;
@@ -344,7 +348,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
         if ((j >> 4) > (i >> 4))
             sm.T[i][j] = 0.f;
     }
-    __syncthreads();
+    lds_barrier();
 
     /* W = T (beta e^G K), U = T (beta V): wave w owns rows 32(w>>1).. and
      * columns 64(w&1)..+64 of both. W is staged (swapped columns) in the q
@@ -390,7 +394,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
             *(bf16x8 *)(uo + 8) = hi;
         }
     }
-    __syncthreads(); /* everyone is done with Kt; W is staged */
+    lds_barrier(); /* everyone is done with Kt; W is staged */
     for (int i = tid; i < CH * (DK / 8); i += 256) {
         const int t = i >> 4, c8 = (i & 15) * 8;
         *(bf16x8 *)(Wo + cb * CH * DK + t * DK + c8) = *(const bf16x8 *)&sm.Q[t][c8];
@@ -405,7 +409,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
         for (int e = 0; e < 8; e++)
             sm.Kt[c8 + e][ts] = f2bf(bf2f(kv[e]) * ek);
     }
-    __syncthreads();
+    lds_barrier();
     for (int i = tid; i < DK * (CH / 8); i += 256) {
         const int r = i >> 3, c8 = (i & 7) * 8;
         *(bf16x8 *)(KgTo + cb * DK * CH + r * CH + c8) = *(const bf16x8 *)&sm.Kt[r][c8];
@@ -420,31 +424,27 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
 /* One LDS stage holds the shared A operands of one chunk, 16-byte chunks
  * XOR-swizzled per row for conflict-free ds_read_b128:
  *   W   [64][128]  at 0        Qg [64][128] at 16 KiB
- *   QK  [64][64]   at 32 KiB   KgT [128][64] at 40 KiB        (56 KiB) */
-constexpr int B_W = 0, B_QG = 16384, B_QK = 32768, B_KGT = 40960, B_BUF = 57344;
-constexpr int B_CHUNKS = B_BUF / 16;     /* 3584 */
-constexpr int B_PER = B_CHUNKS / 256;    /* 14 per thread */
+ *   QK  [64][64]   at 32 KiB   KgT [128][64] at 40 KiB
+ *   U   wave w's accumulator fragments at 56 KiB + 4 KiB w, as
+ *       [row block][half][lane][8]: 16-byte lane stride      (72 KiB)
+ * A stage moves HBM -> LDS by buffer_load ... lds: lane l of a wave writes
+ * its 16 bytes at LDS base + 16 l, so the swizzle is applied on the global
+ * side (the lane landing on slot p of row r fetches chunk p ^ swz(r)). Wave
+ * w issues 14 loads per stage, load j covering W/Qg rows 4(4j + w)..+3 or
+ * QK/KgT rows 8(4j' + w)..+7; with that numbering every lane's offset inside
+ * a load is the same for all j. Wave w also loads its own 4 KiB of U. */
+constexpr int B_W = 0, B_QG = 16384, B_QK = 32768, B_KGT = 40960, B_U = 57344, B_BUF = 73728;
 
+typedef __attribute__((address_space(3))) void *lds_ptr;
+typedef __attribute__((address_space(3))) const unsigned char lds_u8;
+DEV bf16x8 lds_read16(lds_u8 *base, uint32_t off) {
+    return *(__attribute__((address_space(3))) const bf16x8 *)(base + off);
+}
+DEV __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
 DEV int swz16(int r) { return r & 15; }
 DEV int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-
-/* global source and LDS offset of 16-byte chunk f of one stage */
-DEV void stage_addr(int f, const bf16 *W, const bf16 *Qg, const bf16 *QK, const bf16 *KgT,
-                    const bf16 *&src, int &dst) {
-    if (f < 2048) {
-        const int g = f & 1023, row = g >> 4, c = g & 15;
-        src = (f < 1024 ? W : Qg) + row * DK + c * 8;
-        dst = (f < 1024 ? B_W : B_QG) + row * 256 + ((c ^ swz16(row)) << 4);
-    } else if (f < 2560) {
-        const int g = f - 2048, row = g >> 3, c = g & 7;
-        src = QK + row * CH + c * 8;
-        dst = B_QK + row * 128 + ((c ^ swz8(row)) << 4);
-    } else {
-        const int g = f - 2560, row = g >> 3, c = g & 7;
-        src = KgT + row * CH + c * 8;
-        dst = B_KGT + row * 128 + ((c ^ swz8(row)) << 4);
-    }
-}
 
 DEV bf16x8 acc_as_b(const floatx16 &c, int s) {
     bf16x8 b;
@@ -454,17 +454,29 @@ DEV bf16x8 acc_as_b(const floatx16 &c, int s) {
     return b;
 }
 
+/* Per chunk, wave w (state columns 32w..32w+31) computes, in two straight-line
+ * MFMA blocks with the A operands read from LDS six fragments ahead:
+ *   block 1  V' = U - W S  and  O = (Q e^G) S           (4 chains, 32 MFMAs)
+ *   block 2  O += QKm V'  and  S = e^{G_last} S + (K e^{G_last-G})^T V'
+ *                                                        (6 chains, 24 MFMAs)
+ * while the next chunk's stage streams into the other LDS buffer. */
+constexpr int B_RING = 5;
+constexpr int O_LDS = 136; /* fp32 row pitch of the transposed O tile: rows 4 apart sit 32 banks apart */
+
 __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
     const bf16 *__restrict__ Wi, const bf16 *__restrict__ Qgi, const bf16 *__restrict__ QKi,
     const bf16 *__restrict__ KgTi, const bf16 *__restrict__ Ui, const float *__restrict__ Gli,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
     const int32_t *__restrict__ seg_chunk0, const int32_t *__restrict__ seg_nchunk,
-    const float *__restrict__ S_in, float *__restrict__ S_out, int Hv, float *__restrict__ o) {
+    const float *__restrict__ S_in, float *__restrict__ S_out, int Hv, int num_chunks,
+    float *__restrict__ o) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * B_BUF];
     const int seg = blockIdx.x, hv = blockIdx.y;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, col = lane & 31;
     const int dv = 32 * wave + col; /* this lane's state column */
+    lds_u8 *lds = (lds_u8 *)smem;
 
     floatx16 S[4]; /* S[:, dv], rows 32ti + 8(r/4) + 4h + r%4 */
 #pragma unroll
@@ -477,123 +489,152 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
     }
     const int c0 = seg_chunk0[seg], nc = seg_nchunk[seg];
 
-    u32x4 stage[B_PER];
-    bf16x8 ucur[4], unext[4];
-    auto fetch = [&](int ch) {
-        const size_t cb = (size_t)ch * Hv + hv;
-        const bf16 *W = Wi + cb * CH * DK, *Qg = Qgi + cb * CH * DK, *QK = QKi + cb * CH * CH,
-                   *KgT = KgTi + cb * DK * CH;
-#pragma unroll
-        for (int j = 0; j < B_PER; j++) {
-            const bf16 *src;
-            int dst;
-            stage_addr(tid + 256 * j, W, Qg, QK, KgT, src, dst);
-            stage[j] = *(const u32x4 *)src;
+    /* stage loads: one resource per operand array (all chunks, all heads) */
+    const uint32_t big = (uint32_t)num_chunks * Hv * CH * DK * 2; /* W, Qg, KgT bytes */
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(Wi, big), rQg = make_rsrc(Qgi, big),
+                                 rQK = make_rsrc(QKi, big / 2), rKgT = make_rsrc(KgTi, big);
+    /* U of (chunk, head, wave): [row block mt][lane][16] in HBM; LDS slot
+     * (mt, half, lane) holds elements 8 half .. 8 half + 7 of lane's row */
+    const __amdgpu_buffer_rsrc_t rU = make_rsrc(Ui, big);
+    const int l16 = lane >> 4, l8 = lane >> 3;
+    const uint32_t off16 = l16 * 256 + (((lane & 15) ^ (4 * (wave & 3) + l16)) << 4);
+    const uint32_t off8 = l8 * 128 + (((lane & 7) ^ (l8 ^ (wave & 1))) << 4);
+    /* load j (0..17) of a stage: 14 of W/Qg/QK/KgT, then 4 of U */
+    auto issue_load = [&](int j, int ch, unsigned char *buf) {
+        const uint32_t cb = (uint32_t)(ch * Hv + hv);
+        if (j >= 14) { /* U: j - 14 = 2 mt + half */
+            const int q = j - 14;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rU, (lds_ptr)(buf + B_U + wave * 4096 + q * 1024), 16, lane * 32 + (q & 1) * 16,
+                (cb * 4 + wave) * 4096 + (q >> 1) * 2048, 0, 0);
+            return;
         }
-        const bf16 *up = Ui + (cb * 4 + wave) * 2 * 64 * 16 + lane * 16;
-        unext[0] = ld8(up);
-        unext[1] = ld8(up + 8);
-        unext[2] = ld8(up + 64 * 16);
-        unext[3] = ld8(up + 64 * 16 + 8);
+        {
+            if (j < 8) { /* W (j < 4) or Qg: rows 4 idx .. +3, 1 KiB */
+                const int idx = 4 * (j & 3) + wave;
+                const uint32_t lo = (uint32_t)idx * 1024;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    j < 4 ? rW : rQg, (lds_ptr)(buf + (j < 4 ? B_W : B_QG) + lo), 16, off16,
+                    cb * (CH * DK * 2) + lo, 0, 0);
+            } else { /* QK (j < 10) or KgT: rows 8 idx .. +7, 1 KiB */
+                const int idx = 4 * (j < 10 ? j - 8 : j - 10) + wave;
+                const uint32_t lo = (uint32_t)idx * 1024;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    j < 10 ? rQK : rKgT, (lds_ptr)(buf + (j < 10 ? B_QK : B_KGT) + lo), 16,
+                    off8, cb * (j < 10 ? CH * CH * 2 : DK * CH * 2) + lo, 0, 0);
+            }
+        }
     };
-    auto store = [&](unsigned char *buf) {
-#pragma unroll
-        for (int j = 0; j < B_PER; j++) {
-            const bf16 *src;
-            int dst;
-            stage_addr(tid + 256 * j, nullptr, nullptr, nullptr, nullptr, src, dst);
-            *(u32x4 *)(buf + dst) = stage[j];
+    /* A-operand read sequence of one chunk: 32 block-1 reads (W then Qg of
+     * k-step ks for row blocks 0, 1), then 24 block-2 reads (QK of row blocks
+     * 0, 1 and KgT of row blocks 0..3 for each k-step). */
+    auto addr_of = [&](int i, uint32_t buf) -> uint32_t {
+        if (i < 32) {
+            const int ks = i >> 2, mt = (i >> 1) & 1, q = i & 1; /* q: 0 W, 1 Qg */
+            const int r = 32 * mt + col;
+            return buf + (q ? B_QG : B_W) + r * 256 + (((2 * ks + h) ^ swz16(r)) << 4);
         }
+        const int k = i - 32, ks = k / 6, u = k % 6;
+        if (u < 2) {
+            const int r = 32 * u + col;
+            return buf + B_QK + r * 128 + (((2 * ks + h) ^ swz8(r)) << 4);
+        }
+        const int r = 32 * (u - 2) + col;
+        return buf + B_KGT + r * 128 + (((2 * ks + h) ^ swz8(r)) << 4);
     };
 
     if (nc > 0) {
-        fetch(c0);
-        store(smem);
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            ucur[e] = unext[e];
-        __syncthreads();
+        for (int j = 0; j < 18; j++)
+            issue_load(j, c0, smem);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        lds_barrier();
     }
     for (int ci = 0; ci < nc; ci++) {
         const int ch = c0 + ci;
         const int t0 = chunk_tok0[ch], L = chunk_len[ch];
-        const float Glast = Gli[(size_t)ch * Hv + hv];
+        const float dec = fast_exp(Gli[(size_t)ch * Hv + hv]);
         const bool more = ci + 1 < nc;
-        if (more)
-            fetch(ch + 1);
-        const unsigned char *buf = smem + (ci & 1) * B_BUF;
+        const uint32_t buf = (ci & 1) * B_BUF;
+        unsigned char *nbuf = smem + (buf ^ B_BUF);
 
         bf16x8 Sb[8];
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
             Sb[ks] = acc_as_b(S[ks >> 1], ks & 1);
 
-        /* V' = U - W S   (tokens x dv) */
-        floatx16 Vn[2];
+        bf16x8 ring[B_RING];
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
-            floatx16 acc = {};
-            const int r = 32 * mt + col;
+        for (int i = 0; i < B_RING; i++)
+            ring[i] = lds_read16(lds, addr_of(i, buf));
+        floatx16 Vacc[2] = {}, Oacc[2] = {};
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                bf16x8 a = *(const bf16x8 *)(buf + B_W + r * 256 + (((2 * ks + h) ^ swz16(r)) << 4));
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Sb[ks], acc, 0, 0, 0);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                Vn[mt][e] = bf2f(ucur[2 * mt][e]) - acc[e];
-                Vn[mt][8 + e] = bf2f(ucur[2 * mt + 1][e]) - acc[8 + e];
-            }
+        for (int i = 0; i < 32; i++) {
+            const bf16x8 a = ring[i % B_RING];
+            ring[i % B_RING] = lds_read16(lds, addr_of(i + B_RING, buf));
+            if (i % 3 == 0 && more)
+                issue_load(i / 3, ch + 1, nbuf);
+            const int ks = i >> 2, mt = (i >> 1) & 1;
+            if (i & 1)
+                Oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Sb[ks], Oacc[mt], 0, 0, 0);
+            else
+                Vacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Sb[ks], Vacc[mt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        /* V' = U - W S */
         bf16x8 Vb[4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-            Vb[ks] = acc_as_b(Vn[ks >> 1], ks & 1);
-
-        /* O = (Q e^G) S + QKm V' -> fp32 o[token][hv][dv] */
+        for (int j = 0; j < 4; j++) {
+            const bf16x8 u = lds_read16(lds, buf + B_U + wave * 4096 + j * 1024 + lane * 16);
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                Vb[j][e] = f2bf(bf2f(u[e]) - Vacc[j >> 1][8 * (j & 1) + e]);
+        }
+#pragma unroll
+        for (int ti = 0; ti < 4; ti++)
+            S[ti] = S[ti] * dec;
+#pragma unroll
+        for (int i = 32; i < 56; i++) {
+            const bf16x8 a = ring[i % B_RING];
+            if (i + B_RING < 56)
+                ring[i % B_RING] = lds_read16(lds, addr_of(i + B_RING, buf));
+            if (i % 3 == 0 && i / 3 < 18 && more)
+                issue_load(i / 3, ch + 1, nbuf);
+            const int k = i - 32, ks = k / 6, u = k % 6;
+            if (u < 2)
+                Oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Vb[ks], Oacc[u], 0, 0, 0);
+            else
+                S[u - 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Vb[ks], S[u - 2], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        /* the next stage has landed (waited before the stores below, which
+         * also count against vmcnt) */
+        if (more)
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        /* O -> fp32 o[token][hv][dv], transposed through this chunk's (now
+         * consumed) stage buffer so every store is 16 bytes of a row */
+        lds_barrier();
+        __attribute__((address_space(3))) float *ot =
+            (__attribute__((address_space(3))) float *)(smem + buf);
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) {
-            floatx16 acc = {};
-            const int r = 32 * mt + col;
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                bf16x8 a = *(const bf16x8 *)(buf + B_QG + r * 256 + (((2 * ks + h) ^ swz16(r)) << 4));
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Sb[ks], acc, 0, 0, 0);
-            }
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                bf16x8 a = *(const bf16x8 *)(buf + B_QK + r * 128 + (((2 * ks + h) ^ swz8(r)) << 4));
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Vb[ks], acc, 0, 0, 0);
-            }
 #pragma unroll
             for (int rr = 0; rr < 16; rr++) {
                 const int t = 32 * mt + 8 * (rr >> 2) + 4 * h + (rr & 3);
-                if (t < L)
-                    o[((size_t)(t0 + t) * Hv + hv) * DV + dv] = acc[rr];
+                ot[t * O_LDS + dv] = Oacc[mt][rr];
             }
         }
-
-        /* S = e^{G_last} S + (K e^{G_last - G})^T V' */
-        const float dec = fast_exp(Glast);
+        lds_barrier();
 #pragma unroll
-        for (int ti = 0; ti < 4; ti++) {
-            floatx16 acc = S[ti] * dec;
-            const int r = 32 * ti + col;
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                bf16x8 a = *(const bf16x8 *)(buf + B_KGT + r * 128 + (((2 * ks + h) ^ swz8(r)) << 4));
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Vb[ks], acc, 0, 0, 0);
+        for (int p = 0; p < 8; p++) { /* rows 16 wave + 2p + h, 32 lanes x 16 B */
+            const int t = 16 * wave + 2 * p + h;
+            if (t < L) {
+                const floatx4 v = *(__attribute__((address_space(3))) const floatx4 *)(
+                    ot + t * O_LDS + 4 * col);
+                *(floatx4 *)(o + ((size_t)(t0 + t) * Hv + hv) * DV + 4 * col) = v;
             }
-            S[ti] = acc;
         }
-
-        if (more) {
-            store(smem + ((ci + 1) & 1) * B_BUF);
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                ucur[e] = unext[e];
-        }
-        __syncthreads();
+        lds_barrier(); /* the o stores keep streaming */
     }
     if (S_out && seg == 0) {
 #pragma unroll
@@ -676,7 +717,7 @@ extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t 
                        dim3(256), 0, stream, (const bf16 *)ws->W, (const bf16 *)ws->Qg,
                        (const bf16 *)ws->QK, (const bf16 *)ws->KgT, (const bf16 *)ws->U, ws->Glast,
                        ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk, S_in, S_out,
-                       Hv, ws->O);
+                       Hv, ck->num_chunks, ws->O);
     const int rows = N * Hv;
     hipLaunchKernelGGL(gdn_norm_gate_kernel, dim3((unsigned)CEIL_DIV(rows, 4)), dim3(256), 0,
                        stream, ws->O, (const bf16 *)z, z_stride, norm_w, eps, rows, Hv, (bf16 *)y);
