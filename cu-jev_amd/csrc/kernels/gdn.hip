@@ -180,30 +180,58 @@ __global__ void gdn_conv_tail_kernel(const bf16 *__restrict__ proj, int ps,
 /* ---------------------------------------------------------------------- */
 /* phase A: intra-chunk WY/UT factors, written in phase B's operand layouts */
 /* ---------------------------------------------------------------------- */
-/* Phase B feeds S and V' (accumulators) back into MFMAs as B operands. An
- * accumulator supplies the k values of a 16-wide step in the order
- * 4h+0..3, 8+4h+0..3 (lane half h), so every A operand phase B reads is stored
- * with bits 2 and 3 of its column index swapped inside each 16-column group:
- * the 8 consecutive stored values at 16ks + 8h are then exactly the matching
- * original columns and one 16-byte read fetches them. */
-DEV int swap23(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
-
+/* One workgroup (4 waves) per (chunk, v-head), LDS under 80 KiB so two
+ * share a CU:
+ *   1. q, k (k-head), v rows -> LDS; wave 0 forms G = cumsum g and the
+ *      per-token scales beta e^G, beta, e^{G_last - G}.
+ *   2. K K^T and Q K^T (bf16 MFMA); A = tril(beta_i e^{G_i-G_j} k_i.k_j, -1)
+ *      (fp32) and the masked QK^T (bf16) -> LDS; Q e^G and QK^T leave.
+ *   3. T = (I + A)^-1 in place, fp32: the four 16x16 diagonal blocks by
+ *      forward substitution, then T_10 = -T_11 (A_10 T_00) inside each 32x32
+ *      diagonal block, then the same at 64 with 32x32 blocks.
+ *   4. W = T (beta e^G K), U = T (beta V) on MFMA. Their B operands need
+ *      tokens on the k axis: D = K I (an exact identity product) gives that
+ *      layout in registers, rows in the accumulator order 4h+0..3, 8+4h+0..3
+ *      of every 16, so T is read with its columns in that order. The same
+ *      D tiles scaled by e^{G_last - G} are (k e^{G_last-G})^T, stored
+ *      straight from registers after one cross-half exchange.
+ *   5. W and U staged row-major in the freed q / v rows, then stored in
+ *      fragment order. */
 struct __attribute__((aligned(16))) ChunkA_Smem {
-    bf16 K[CH][DK + 8];  /* k rows                                            */
-    bf16 Q[CH][DK + 8];  /* q rows; later W staged for coalesced stores       */
-    bf16 V[CH][DV + 8];  /* v rows; later masked QK^T staged                  */
-    bf16 Kt[DK][CH + 8]; /* (beta e^G k)^T, later (k e^{Glast-G})^T swapped   */
-    bf16 Vt[DV][CH + 8]; /* (beta v)^T                                        */
-    float A[CH][CH + 1]; /* strictly lower A                                  */
-    float T[CH][CH + 1]; /* (I + A)^-1                                        */
-    float M[3][16][17];  /* block products                                    */
-    float G[CH], B[CH];
+    bf16 K[CH][DK + 8];   /* k rows                     */
+    bf16 Q[CH][DK + 8];   /* q rows, later W            */
+    bf16 V[CH][DV + 8];   /* v rows, later U            */
+    float AT[CH][CH + 4]; /* A, then T in place (rows 16-byte aligned) */
+    bf16 QK[CH][CH + 8];  /* masked QK^T staging        */
+    float G[CH], sK[CH], sKg[CH], sV[CH];
 };
+static_assert(sizeof(ChunkA_Smem) <= 80 * 1024, "two phase-A workgroups per CU");
 
 DEV bf16x8 ld8(const bf16 *p) { return *(const bf16x8 *)p; }
-DEV void st4(bf16 *p, bf16 a, bf16 b, bf16 c, bf16 d) { *(bf16x4 *)p = bf16x4{a, b, c, d}; }
+typedef __attribute__((address_space(3))) float4 lds_f4;
+DEV float4 rd4(const float *p) { return *(const float4 *)p; }
+DEV void wr4(float *p, float4 v) { *(float4 *)p = v; }
+DEV float4 f4fma(float a, float4 b, float4 c) {
+    return make_float4(fmaf(a, b.x, c.x), fmaf(a, b.y, c.y), fmaf(a, b.z, c.z), fmaf(a, b.w, c.w));
+}
 
-__global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
+/* X[r][c0..c0+3] = sum_{k<n} P[r][k] Q[k][c0..c0+3] over fp32 LDS rows of pitch CH+4 */
+template <int n>
+DEV float4 row_times(const float *P, const float *Qm) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k4 = 0; k4 < n; k4 += 4) {
+        const float4 p = rd4(P + k4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float pe = e == 0 ? p.x : e == 1 ? p.y : e == 2 ? p.z : p.w;
+            acc = f4fma(pe, rd4(Qm + (k4 + e) * (CH + 4)), acc);
+        }
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
     const bf16 *__restrict__ qh, const bf16 *__restrict__ kh_, const bf16 *__restrict__ vh,
     const float *__restrict__ g, const float *__restrict__ beta,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len, int Hk, int Hv,
@@ -213,95 +241,102 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
     const int ch = blockIdx.x, hv = blockIdx.y;
     const int hk = hv / (Hv / Hk);
     const int t0 = chunk_tok0[ch], L = chunk_len[ch];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, col = lane & 31;
     const size_t cb = (size_t)ch * Hv + hv;
 
-    /* gates and cumulative log-decay (zero past L, so G stays at G[L-1]) */
-    if (wave == 0) {
-        float gv = lane < L ? g[(size_t)(t0 + lane) * Hv + hv] : 0.f;
-        const float bv = lane < L ? beta[(size_t)(t0 + lane) * Hv + hv] : 0.f;
+    /* ---- 1. rows and gates ---- */
+    {
+        bf16x8 kv[4], qv[4], vv[4];
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const float up = __shfl_up(gv, o, 64);
-            if (lane >= o)
-                gv += up;
+        for (int j = 0; j < 4; j++) {
+            const int i = tid + 256 * j, t = i >> 4, c8 = (i & 15) * 8;
+            kv[j] = qv[j] = vv[j] = bf16x8{};
+            if (t < L) {
+                kv[j] = ld8(kh_ + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
+                qv[j] = ld8(qh + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
+                vv[j] = ld8(vh + ((size_t)(t0 + t) * Hv + hv) * DV + c8);
+            }
         }
-        sm.G[lane] = gv;
-        sm.B[lane] = bv;
-    }
-    /* q, k, v rows (zero past L), 16-byte coalesced */
-    for (int i = tid; i < CH * (DK / 8); i += 256) {
-        const int t = i >> 4, c8 = (i & 15) * 8;
-        bf16x8 kv = {}, qv = {}, vv = {};
-        if (t < L) {
-            kv = ld8(kh_ + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
-            qv = ld8(qh + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
-            vv = ld8(vh + ((size_t)(t0 + t) * Hv + hv) * DV + c8);
+        if (wave == 0) {
+            float gv = lane < L ? g[(size_t)(t0 + lane) * Hv + hv] : 0.f;
+            const float bv = lane < L ? beta[(size_t)(t0 + lane) * Hv + hv] : 0.f;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const float up = __shfl_up(gv, o, 64);
+                if (lane >= o)
+                    gv += up;
+            }
+            const float gl = __shfl(gv, 63, 64);
+            sm.G[lane] = gv;
+            sm.sK[lane] = bv * fast_exp(gv);
+            sm.sKg[lane] = fast_exp(gl - gv);
+            sm.sV[lane] = bv;
+            Glo[cb * 64 + lane] = gl; /* one copy per lane of phase B's waves */
         }
-        *(bf16x8 *)&sm.K[t][c8] = kv;
-        *(bf16x8 *)&sm.Q[t][c8] = qv;
-        *(bf16x8 *)&sm.V[t][c8] = vv;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = tid + 256 * j, t = i >> 4, c8 = (i & 15) * 8;
+            *(bf16x8 *)&sm.K[t][c8] = kv[j];
+            *(bf16x8 *)&sm.Q[t][c8] = qv[j];
+            *(bf16x8 *)&sm.V[t][c8] = vv[j];
+        }
     }
     lds_barrier();
-    const float Glast = sm.G[CH - 1];
-    /* q e^G straight to HBM (16 lanes per row: coalesced) */
-    for (int i = tid; i < CH * (DK / 8); i += 256) {
-        const int t = i >> 4, c8 = (i & 15) * 8;
-        const float eg = fast_exp(sm.G[t]);
-        bf16x8 qv = *(const bf16x8 *)&sm.Q[t][c8];
-        bf16 *qrow = Qgo + cb * CH * DK + t * DK;
-        st4(qrow + swap23(c8), f2bf(bf2f(qv[0]) * eg), f2bf(bf2f(qv[1]) * eg),
-            f2bf(bf2f(qv[2]) * eg), f2bf(bf2f(qv[3]) * eg));
-        st4(qrow + swap23(c8 + 4), f2bf(bf2f(qv[4]) * eg), f2bf(bf2f(qv[5]) * eg),
-            f2bf(bf2f(qv[6]) * eg), f2bf(bf2f(qv[7]) * eg));
-    }
-    /* (beta e^G k)^T and (beta v)^T: consecutive lanes take consecutive
-     * tokens so the transposed 2-byte writes hit consecutive addresses */
-    for (int i = tid; i < CH * (DK / 8); i += 256) {
-        const int t = i & 63, c8 = (i >> 6) * 8;
-        const float sk = sm.B[t] * fast_exp(sm.G[t]), sv = sm.B[t];
-        bf16x8 kv = *(const bf16x8 *)&sm.K[t][c8];
-        bf16x8 vv = *(const bf16x8 *)&sm.V[t][c8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            sm.Kt[c8 + e][t] = f2bf(bf2f(kv[e]) * sk);
-            sm.Vt[c8 + e][t] = f2bf(bf2f(vv[e]) * sv);
-        }
-    }
-    lds_barrier(); /* V rows are free from here on: QK^T staging */
 
-    /* K K^T and Q K^T: wave w owns the 32x32 tile (w>>1, w&1) of both */
+    /* ---- 2. K K^T, Q K^T; wave w owns the 32x32 tile (w>>1, w&1) ---- */
     {
         const int ti = wave >> 1, tj = wave & 1;
         floatx16 kk = {}, qk = {};
+        if (ti >= tj) {
 #pragma unroll
-        for (int ks = 0; ks < DK / 16; ks++) {
-            const int c = 16 * ks + 8 * h;
-            bf16x8 ak = *(const bf16x8 *)&sm.K[32 * ti + col][c];
-            bf16x8 aq = *(const bf16x8 *)&sm.Q[32 * ti + col][c];
-            bf16x8 bk = *(const bf16x8 *)&sm.K[32 * tj + col][c];
-            kk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, bk, kk, 0, 0, 0);
-            qk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, bk, qk, 0, 0, 0);
+            for (int ks = 0; ks < DK / 16; ks++) {
+                const int c = 16 * ks + 8 * h;
+                const bf16x8 ak = *(const bf16x8 *)&sm.K[32 * ti + col][c];
+                const bf16x8 aq = *(const bf16x8 *)&sm.Q[32 * ti + col][c];
+                const bf16x8 bk = *(const bf16x8 *)&sm.K[32 * tj + col][c];
+                kk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, bk, kk, 0, 0, 0);
+                qk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, bk, qk, 0, 0, 0);
+            }
         }
         const int j = 32 * tj + col;
         const float Gj = sm.G[j];
-        bf16 *qks = &sm.V[0][0] + swap23(j); /* [64][72] bf16 staging */
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int i = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
             const float dec = i >= j ? fast_exp(sm.G[i] - Gj) : 0.f;
-            sm.A[i][j] = i > j ? sm.B[i] * kk[r] * dec : 0.f;
-            qks[i * (CH + 8)] = f2bf(i >= j ? qk[r] * dec : 0.f);
+            sm.AT[i][j] = i > j ? sm.sV[i] * kk[r] * dec : 0.f;
+            sm.QK[i][j] = f2bf(i >= j ? qk[r] * dec : 0.f);
         }
     }
     lds_barrier();
-    /* masked QK^T rows to HBM; T = (I + A)^-1 diagonal blocks by forward
-     * substitution (wave w inverts block w, lane c < 16 owns column c) */
-    for (int i = tid; i < CH * (CH / 8); i += 256) {
-        const int r = i >> 3, c8 = (i & 7) * 8;
-        *(bf16x8 *)(QKo + cb * CH * CH + r * CH + c8) = *(const bf16x8 *)(&sm.V[0][0] + r * (CH + 8) + c8);
+    /* q e^G and the masked QK^T leave in 16x16x32 A-fragment order: entry
+     * i = (row block w, k-step s, lane l) holds row 16w + l%16, columns
+     * 32s + 8(l/16)..+7 */
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int i = tid + 256 * j;
+        const int t = 16 * (i >> 8) + (i & 15), c8 = 32 * ((i >> 6) & 3) + 8 * ((i >> 4) & 3);
+        const float eg = fast_exp(sm.G[t]);
+        const bf16x8 qv = *(const bf16x8 *)&sm.Q[t][c8];
+        bf16x8 r;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            r[e] = f2bf(bf2f(qv[e]) * eg);
+        *(bf16x8 *)(Qgo + (cb * 1024 + i) * 8) = r;
     }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int i = tid + 256 * j;
+        const int r = 16 * (i >> 7) + (i & 15), c8 = 32 * ((i >> 6) & 1) + 8 * ((i >> 4) & 3);
+        *(bf16x8 *)(QKo + (cb * 512 + i) * 8) = *(const bf16x8 *)&sm.QK[r][c8];
+    }
+
+    /* ---- 3. T = (I + A)^-1 in place ----
+     * 3a: wave w inverts diagonal block w, lane c < 16 owning column c. Row i
+     * of the block is read (all lanes, broadcast) before any lane writes row
+     * i, and no later step reads it again. */
     if (lane < 16) {
         const int b0 = 16 * wave, c = lane;
         float t[16];
@@ -309,366 +344,391 @@ __global__ __launch_bounds__(256) void gdn_chunk_a_kernel(
         for (int i = 0; i < 16; i++) {
             float acc = 0.f;
 #pragma unroll
-            for (int k = 0; k < i; k++)
-                acc += sm.A[b0 + i][b0 + k] * t[k];
+            for (int k4 = 0; k4 < i; k4 += 4) {
+                const float4 a = rd4(&sm.AT[b0 + i][b0 + k4]);
+                acc = fmaf(a.x, t[k4], acc);
+                if (k4 + 1 < i)
+                    acc = fmaf(a.y, t[k4 + 1], acc);
+                if (k4 + 2 < i)
+                    acc = fmaf(a.z, t[k4 + 2], acc);
+                if (k4 + 3 < i)
+                    acc = fmaf(a.w, t[k4 + 3], acc);
+            }
             t[i] = (i == c ? 1.f : 0.f) - acc;
-        }
-#pragma unroll
-        for (int i = 0; i < 16; i++)
-            sm.T[b0 + i][b0 + c] = t[i];
-    }
-    /* ... then the strictly lower blocks by distance from the diagonal:
-     * T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj */
-    for (int lvl = 1; lvl < 4; lvl++) {
-        lds_barrier();
-        const int nb = 4 - lvl;
-        for (int e = tid; e < nb * 256; e += 256) {
-            const int b = e >> 8, r = (e >> 4) & 15, c = e & 15;
-            const int bj = b, bi = b + lvl;
-            float acc = 0.f;
-            for (int bk = bj; bk < bi; bk++)
-#pragma unroll
-                for (int x = 0; x < 16; x++)
-                    acc += sm.A[16 * bi + r][16 * bk + x] * sm.T[16 * bk + x][16 * bj + c];
-            sm.M[b][r][c] = acc;
-        }
-        lds_barrier();
-        for (int e = tid; e < nb * 256; e += 256) {
-            const int b = e >> 8, r = (e >> 4) & 15, c = e & 15;
-            const int bj = b, bi = b + lvl;
-            float acc = 0.f;
-#pragma unroll
-            for (int x = 0; x < 16; x++)
-                acc += sm.T[16 * bi + r][16 * bi + x] * sm.M[b][x][c];
-            sm.T[16 * bi + r][16 * bj + c] = -acc;
+            if (i >= c)
+                sm.AT[b0 + i][b0 + c] = t[i];
         }
     }
-    for (int e = tid; e < CH * CH; e += 256) {
-        const int i = e >> 6, j = e & 63;
-        if ((j >> 4) > (i >> 4))
-            sm.T[i][j] = 0.f;
+    lds_barrier();
+    /* 3b: inside 32x32 diagonal block p (wave p): T_10 = -T_11 (A_10 T_00),
+     * 16x16 blocks; lane = (row l/4, columns 4(l%4)..+3) */
+    if (wave < 2) {
+        const int p0 = 32 * wave, r = lane >> 2, c0 = 4 * (lane & 3);
+        float *a10 = &sm.AT[p0 + 16 + r][p0];
+        const float4 x = row_times<16>(a10, &sm.AT[p0][p0 + c0]);
+        wr4(a10 + c0, x);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const float4 y = row_times<16>(&sm.AT[p0 + 16 + r][p0 + 16], &sm.AT[p0 + 16][p0 + c0]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wr4(a10 + c0, make_float4(-y.x, -y.y, -y.z, -y.w));
+    }
+    lds_barrier();
+    /* 3c: T_10 = -T_11 (A_10 T_00) with 32x32 blocks; lane = (row 8w + l/8,
+     * columns 4(l%8)..+3) */
+    {
+        const int r = 32 + 8 * wave + (lane >> 3), c0 = 4 * (lane & 7);
+        const float4 x = row_times<32>(&sm.AT[r][0], &sm.AT[0][c0]);
+        lds_barrier();
+        wr4(&sm.AT[r][c0], x);
+        lds_barrier();
+        const float4 y = row_times<32>(&sm.AT[r][32], &sm.AT[32][c0]);
+        lds_barrier();
+        wr4(&sm.AT[r][c0], make_float4(-y.x, -y.y, -y.z, -y.w));
     }
     lds_barrier();
 
-    /* W = T (beta e^G K), U = T (beta V): wave w owns rows 32(w>>1).. and
-     * columns 64(w&1)..+64 of both. W is staged (swapped columns) in the q
-     * rows' LDS for coalesced stores; U goes out in accumulator-fragment
-     * order, i.e. exactly the 16 values lane l of phase B's wave (column
-     * block) needs, contiguous. */
+    /* ---- 4. W = T (beta e^G K), U = T (beta V), (k e^{Glast-G})^T ----
+     * wave w: dk (= dv) block 32w, both 32-row halves of W and U. */
     {
-        const int mi = wave >> 1, nh = wave & 1;
-        floatx16 w[2] = {}, u[2] = {};
+        bf16x8 eye[2]; /* B operand of the identity, k = 16s + 8h + e */
 #pragma unroll
-        for (int ks = 0; ks < CH / 16; ks++) {
-            const int k0 = 16 * ks + 8 * h;
-            bf16x8 a;
+        for (int s = 0; s < 2; s++)
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                a[e] = f2bf(sm.T[32 * mi + col][k0 + e]);
+                eye[s][e] = f2bf(16 * s + 8 * h + e == col ? 1.f : 0.f);
+        floatx16 dK[2], dV[2]; /* D[tb] = rows 32tb.. of K (V), columns 32w.. */
 #pragma unroll
-            for (int nj = 0; nj < 2; nj++) {
-                const int c = 64 * nh + 32 * nj + col;
-                bf16x8 bk = *(const bf16x8 *)&sm.Kt[c][k0];
-                bf16x8 bv = *(const bf16x8 *)&sm.Vt[c][k0];
-                w[nj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bk, w[nj], 0, 0, 0);
-                u[nj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bv, u[nj], 0, 0, 0);
+        for (int tb = 0; tb < 2; tb++) {
+            dK[tb] = dV[tb] = floatx16{};
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const int c = 32 * wave + 16 * s + 8 * h;
+                dK[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    *(const bf16x8 *)&sm.K[32 * tb + col][c], eye[s], dK[tb], 0, 0, 0);
+                dV[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    *(const bf16x8 *)&sm.V[32 * tb + col][c], eye[s], dV[tb], 0, 0, 0);
             }
         }
+        /* token of accumulator slot r of tile tb */
+        auto tok = [&](int tb, int r) { return 32 * tb + 8 * (r >> 2) + 4 * h + (r & 3); };
+        /* per-token scales of this lane's accumulator slots: slot r of tile tb
+         * is token 32tb + 8(r/4) + 4h + r%4, four consecutive tokens a read */
+        float sk[2][16], sv[2][16], skg[2][16];
 #pragma unroll
-        for (int nj = 0; nj < 2; nj++) {
-            const int c = swap23(64 * nh + 32 * nj + col);
+        for (int tb = 0; tb < 2; tb++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int i = 32 * mi + 8 * (r >> 2) + 4 * h + (r & 3);
-                sm.Q[i][c] = f2bf(w[nj][r]);
+            for (int m = 0; m < 4; m++) {
+                const int t = 32 * tb + 8 * m + 4 * h;
+                const float4 a = rd4(&sm.sK[t]), b = rd4(&sm.sV[t]), c = rd4(&sm.sKg[t]);
+                sk[tb][4 * m] = a.x, sk[tb][4 * m + 1] = a.y, sk[tb][4 * m + 2] = a.z, sk[tb][4 * m + 3] = a.w;
+                sv[tb][4 * m] = b.x, sv[tb][4 * m + 1] = b.y, sv[tb][4 * m + 2] = b.z, sv[tb][4 * m + 3] = b.w;
+                skg[tb][4 * m] = c.x, skg[tb][4 * m + 1] = c.y, skg[tb][4 * m + 2] = c.z, skg[tb][4 * m + 3] = c.w;
             }
-            const int wblk = 2 * nh + nj; /* phase B's wave owning these 32 columns */
-            bf16 *uo = Uo + (((cb * 4 + wblk) * 2 + mi) * 64 + lane) * 16;
-            bf16x8 lo, hi;
+        bf16x8 xk[4], xv[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int tb = ks >> 1, r0 = 8 * (ks & 1);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                lo[e] = f2bf(u[nj][e]);
-                hi[e] = f2bf(u[nj][8 + e]);
+                xk[ks][e] = f2bf(dK[tb][r0 + e] * sk[tb][r0 + e]);
+                xv[ks][e] = f2bf(dV[tb][r0 + e] * sv[tb][r0 + e]);
             }
-            *(bf16x8 *)uo = lo;
-            *(bf16x8 *)(uo + 8) = hi;
+        }
+        /* (k e^{Glast-G})^T as 32x32x16 A fragments (row dk = 32w + l%32,
+         * tokens 16s + 8(l/32)..+7): the lane pair (l, l^32) trades halves */
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int tb = s >> 1, r0 = 8 * (s & 1);
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                v[e] = dK[tb][r0 + e] * skg[tb][r0 + e];
+            /* h=0 holds tokens +0..3 | +8..11, h=1 holds +4..7 | +12..15 */
+            uint32_t p0[2], p1[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                p0[e] = __builtin_bit_cast(uint32_t, bf16x2{f2bf(v[2 * e]), f2bf(v[2 * e + 1])});
+                p1[e] = __builtin_bit_cast(uint32_t, bf16x2{f2bf(v[4 + 2 * e]), f2bf(v[5 + 2 * e])});
+            }
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t x1 = (uint32_t)__shfl_xor((int)p1[e], 32, 64);
+                const uint32_t x0 = (uint32_t)__shfl_xor((int)p0[e], 32, 64);
+                o[e] = h ? x1 : p0[e];
+                o[2 + e] = h ? p1[e] : x0;
+            }
+            *(u32x4 *)(KgTo + (cb * 1024 + (wave * 4 + s) * 64 + lane) * 8) =
+                u32x4{o[0], o[1], o[2], o[3]};
+        }
+        floatx16 w[2] = {}, u[2] = {};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                const float *tr = &sm.AT[32 * mi + col][16 * ks + 4 * h];
+                const float4 a0 = rd4(tr), a1 = rd4(tr + 8);
+                const bf16x8 a = {f2bf(a0.x), f2bf(a0.y), f2bf(a0.z), f2bf(a0.w),
+                                  f2bf(a1.x), f2bf(a1.y), f2bf(a1.z), f2bf(a1.w)};
+                w[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xk[ks], w[mi], 0, 0, 0);
+                u[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xv[ks], u[mi], 0, 0, 0);
+            }
+        }
+        lds_barrier(); /* every wave is done with the v rows */
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int i = tok(mi, r);
+                sm.Q[i][32 * wave + col] = f2bf(w[mi][r]);
+                sm.V[i][32 * wave + col] = f2bf(u[mi][r]);
+            }
         }
     }
-    lds_barrier(); /* everyone is done with Kt; W is staged */
-    for (int i = tid; i < CH * (DK / 8); i += 256) {
-        const int t = i >> 4, c8 = (i & 15) * 8;
-        *(bf16x8 *)(Wo + cb * CH * DK + t * DK + c8) = *(const bf16x8 *)&sm.Q[t][c8];
-    }
-    /* (k e^{Glast - G})^T with swapped token columns, then rows to HBM */
-    for (int i = tid; i < CH * (DK / 8); i += 256) {
-        const int t = i & 63, c8 = (i >> 6) * 8;
-        const float ek = fast_exp(Glast - sm.G[t]);
-        bf16x8 kv = *(const bf16x8 *)&sm.K[t][c8];
-        const int ts = swap23(t);
+    lds_barrier();
+    /* ---- 5. W in the fragment order of q e^G; U as 16x16 accumulator
+     * fragments: entry i = (32-column block cbk, row block w, lane l) holds
+     * rows 16w + 4(l/16) + 0..3 of columns 32cbk + l%16 (values 0..3) and
+     * 32cbk + 16 + l%16 (values 4..7) ---- */
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int i = tid + 256 * j;
+        const int t = 16 * (i >> 8) + (i & 15), c8 = 32 * ((i >> 6) & 3) + 8 * ((i >> 4) & 3);
+        *(bf16x8 *)(Wo + (cb * 1024 + i) * 8) = *(const bf16x8 *)&sm.Q[t][c8];
+        const int tu = 16 * ((i >> 6) & 3) + 4 * ((i >> 4) & 3), cu = 32 * (i >> 8) + (i & 15);
+        bf16x8 r;
 #pragma unroll
         for (int e = 0; e < 8; e++)
-            sm.Kt[c8 + e][ts] = f2bf(bf2f(kv[e]) * ek);
+            r[e] = sm.V[tu + (e & 3)][cu + 16 * (e >> 2)];
+        *(bf16x8 *)(Uo + (cb * 1024 + i) * 8) = r;
     }
-    lds_barrier();
-    for (int i = tid; i < DK * (CH / 8); i += 256) {
-        const int r = i >> 3, c8 = (i & 7) * 8;
-        *(bf16x8 *)(KgTo + cb * DK * CH + r * CH + c8) = *(const bf16x8 *)&sm.Kt[r][c8];
-    }
-    if (tid == 0)
-        Glo[cb] = Glast;
 }
 
 /* ---------------------------------------------------------------------- */
 /* phase B: the state recurrence over chunks                                */
 /* ---------------------------------------------------------------------- */
-/* One LDS stage holds the shared A operands of one chunk, 16-byte chunks
- * XOR-swizzled per row for conflict-free ds_read_b128:
- *   W   [64][128]  at 0        Qg [64][128] at 16 KiB
- *   QK  [64][64]   at 32 KiB   KgT [128][64] at 40 KiB
- *   U   wave w's accumulator fragments at 56 KiB + 4 KiB w, as
- *       [row block][half][lane][8]: 16-byte lane stride      (72 KiB)
- * A stage moves HBM -> LDS by buffer_load ... lds: lane l of a wave writes
- * its 16 bytes at LDS base + 16 l, so the swizzle is applied on the global
- * side (the lane landing on slot p of row r fetches chunk p ^ swz(r)). Wave
- * w issues 14 loads per stage, load j covering W/Qg rows 4(4j + w)..+3 or
- * QK/KgT rows 8(4j' + w)..+7; with that numbering every lane's offset inside
- * a load is the same for all j. Wave w also loads its own 4 KiB of U. */
-constexpr int B_W = 0, B_QG = 16384, B_QK = 32768, B_KGT = 40960, B_U = 57344, B_BUF = 73728;
+/* The columns of S evolve independently, so a (segment, v-head) is spread
+ * over NCB workgroups of 32 state columns each, and inside a workgroup the
+ * four waves split rows: wave w holds S rows 32w..32w+31 (fp32, one 32x32
+ * accumulator) and chunk tokens 16w..16w+15. Per chunk:
+ *   S (bf16) -> LDS as S^T; barrier
+ *   V'_w = U_w - W_w S,  O_w = (Q e^G)_w S          (16x16x32, 16 MFMAs)
+ *   V'_w (bf16) -> LDS as V'^T; barrier
+ *   S_w = e^{G_last} S_w + (K e^{G_last-G})^T_w V'  (32x32x16, 4 MFMAs)
+ *   O_w += QKm_w V'                                  (16x16x32, 4 MFMAs)
+ * Phase A stored every operand in fragment order, so each lane loads its
+ * fragments with 16-byte reads straight into registers, two chunks ahead.
+ * The NCB workgroups of one unit share those operands; block numbering puts
+ * them on one XCD (blockIdx % 8 picks the XCD), so their L2 serves the
+ * repeats. */
+constexpr int NCB = DV / 32;
 
-typedef __attribute__((address_space(3))) void *lds_ptr;
-typedef __attribute__((address_space(3))) const unsigned char lds_u8;
-DEV bf16x8 lds_read16(lds_u8 *base, uint32_t off) {
-    return *(__attribute__((address_space(3))) const bf16x8 *)(base + off);
-}
-DEV __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
-}
-DEV int swz16(int r) { return r & 15; }
-DEV int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-
-DEV bf16x8 acc_as_b(const floatx16 &c, int s) {
-    bf16x8 b;
-#pragma unroll
-    for (int e = 0; e < 8; e++)
-        b[e] = f2bf(c[8 * s + e]);
-    return b;
-}
-
-/* Per chunk, wave w (state columns 32w..32w+31) computes, in two straight-line
- * MFMA blocks with the A operands read from LDS six fragments ahead:
- *   block 1  V' = U - W S  and  O = (Q e^G) S           (4 chains, 32 MFMAs)
- *   block 2  O += QKm V'  and  S = e^{G_last} S + (K e^{G_last-G})^T V'
- *                                                        (6 chains, 24 MFMAs)
- * while the next chunk's stage streams into the other LDS buffer. */
-constexpr int B_RING = 5;
-constexpr int O_LDS = 136; /* fp32 row pitch of the transposed O tile: rows 4 apart sit 32 banks apart */
+struct BOps {
+    bf16x8 w[4], qg[4], qk[2], kg[4], u;
+    float gl;
+};
 
 __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
-    const bf16 *__restrict__ Wi, const bf16 *__restrict__ Qgi, const bf16 *__restrict__ QKi,
-    const bf16 *__restrict__ KgTi, const bf16 *__restrict__ Ui, const float *__restrict__ Gli,
+    const bf16x8 *__restrict__ Wi, const bf16x8 *__restrict__ Qgi, const bf16x8 *__restrict__ QKi,
+    const bf16x8 *__restrict__ KgTi, const bf16x8 *__restrict__ Ui, const float *__restrict__ Gli,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
     const int32_t *__restrict__ seg_chunk0, const int32_t *__restrict__ seg_nchunk,
-    const float *__restrict__ S_in, float *__restrict__ S_out, int Hv, int num_chunks,
-    float *__restrict__ o) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * B_BUF];
-    const int seg = blockIdx.x, hv = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = lane >> 5, col = lane & 31;
-    const int dv = 32 * wave + col; /* this lane's state column */
-    lds_u8 *lds = (lds_u8 *)smem;
+    const float *__restrict__ S_in, float *__restrict__ S_out, int Hv, int units,
+    bf16 *__restrict__ o) {
+    __shared__ __attribute__((aligned(16))) bf16 sT[32][DK + 8];  /* S^T [column][dk]     */
+    __shared__ __attribute__((aligned(16))) bf16 vT[32][CH + 8];  /* V'^T [column][token] */
+    __shared__ __attribute__((aligned(16))) bf16 ost[4][16][40];  /* per-wave O tile      */
 
-    floatx16 S[4]; /* S[:, dv], rows 32ti + 8(r/4) + 4h + r%4 */
+    const int bid = blockIdx.x;
+    const int u = (bid & 7) + 8 * ((bid >> 3) / NCB), cbk = (bid >> 3) % NCB;
+    if (u >= units)
+        return;
+    const int seg = u / Hv, hv = u - seg * Hv;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane >> 5, c32 = lane & 31, q4 = lane >> 4, c16 = lane & 15;
+    const int col0 = 32 * cbk;
+
+    floatx16 S; /* rows 32 wave + 8(r/4) + 4h + r%4, column col0 + c32 */
 #pragma unroll
-    for (int ti = 0; ti < 4; ti++) {
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int dk = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
-            S[ti][r] = S_in ? S_in[((size_t)hv * DK + dk) * DV + dv] : 0.f;
-        }
+    for (int r = 0; r < 16; r++) {
+        const int dk = 32 * wave + 8 * (r >> 2) + 4 * h + (r & 3);
+        S[r] = S_in ? S_in[((size_t)hv * DK + dk) * DV + col0 + c32] : 0.f;
     }
+    /* consume S here, before any operand prefetch is in flight: S then enters
+     * the chunk loop as a VALU result, and the loop's waits only cover the
+     * operand set a step uses (a pending load there would turn the loop-head
+     * wait into vmcnt(0), draining the prefetches every round) */
+#pragma unroll
+    for (int r = 0; r < 16; r++)
+        S[r] += 0.f;
     const int c0 = seg_chunk0[seg], nc = seg_nchunk[seg];
 
-    /* stage loads: one resource per operand array (all chunks, all heads) */
-    const uint32_t big = (uint32_t)num_chunks * Hv * CH * DK * 2; /* W, Qg, KgT bytes */
-    const __amdgpu_buffer_rsrc_t rW = make_rsrc(Wi, big), rQg = make_rsrc(Qgi, big),
-                                 rQK = make_rsrc(QKi, big / 2), rKgT = make_rsrc(KgTi, big);
-    /* U of (chunk, head, wave): [row block mt][lane][16] in HBM; LDS slot
-     * (mt, half, lane) holds elements 8 half .. 8 half + 7 of lane's row */
-    const __amdgpu_buffer_rsrc_t rU = make_rsrc(Ui, big);
-    const int l16 = lane >> 4, l8 = lane >> 3;
-    const uint32_t off16 = l16 * 256 + (((lane & 15) ^ (4 * (wave & 3) + l16)) << 4);
-    const uint32_t off8 = l8 * 128 + (((lane & 7) ^ (l8 ^ (wave & 1))) << 4);
-    /* load j (0..17) of a stage: 14 of W/Qg/QK/KgT, then 4 of U */
-    auto issue_load = [&](int j, int ch, unsigned char *buf) {
-        const uint32_t cb = (uint32_t)(ch * Hv + hv);
-        if (j >= 14) { /* U: j - 14 = 2 mt + half */
-            const int q = j - 14;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rU, (lds_ptr)(buf + B_U + wave * 4096 + q * 1024), 16, lane * 32 + (q & 1) * 16,
-                (cb * 4 + wave) * 4096 + (q >> 1) * 2048, 0, 0);
-            return;
+    auto load = [&](int ch, BOps &op) {
+        const size_t cb = (size_t)ch * Hv + hv;
+        const bf16x8 *w = Wi + cb * 1024 + wave * 256 + lane;
+        const bf16x8 *qg = Qgi + cb * 1024 + wave * 256 + lane;
+        const bf16x8 *kg = KgTi + cb * 1024 + wave * 256 + lane;
+        const bf16x8 *qk = QKi + cb * 512 + wave * 128 + lane;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            op.w[s] = w[64 * s];
+            op.kg[s] = kg[64 * s];
         }
-        {
-            if (j < 8) { /* W (j < 4) or Qg: rows 4 idx .. +3, 1 KiB */
-                const int idx = 4 * (j & 3) + wave;
-                const uint32_t lo = (uint32_t)idx * 1024;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    j < 4 ? rW : rQg, (lds_ptr)(buf + (j < 4 ? B_W : B_QG) + lo), 16, off16,
-                    cb * (CH * DK * 2) + lo, 0, 0);
-            } else { /* QK (j < 10) or KgT: rows 8 idx .. +7, 1 KiB */
-                const int idx = 4 * (j < 10 ? j - 8 : j - 10) + wave;
-                const uint32_t lo = (uint32_t)idx * 1024;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    j < 10 ? rQK : rKgT, (lds_ptr)(buf + (j < 10 ? B_QK : B_KGT) + lo), 16,
-                    off8, cb * (j < 10 ? CH * CH * 2 : DK * CH * 2) + lo, 0, 0);
-            }
-        }
-    };
-    /* A-operand read sequence of one chunk: 32 block-1 reads (W then Qg of
-     * k-step ks for row blocks 0, 1), then 24 block-2 reads (QK of row blocks
-     * 0, 1 and KgT of row blocks 0..3 for each k-step). */
-    auto addr_of = [&](int i, uint32_t buf) -> uint32_t {
-        if (i < 32) {
-            const int ks = i >> 2, mt = (i >> 1) & 1, q = i & 1; /* q: 0 W, 1 Qg */
-            const int r = 32 * mt + col;
-            return buf + (q ? B_QG : B_W) + r * 256 + (((2 * ks + h) ^ swz16(r)) << 4);
-        }
-        const int k = i - 32, ks = k / 6, u = k % 6;
-        if (u < 2) {
-            const int r = 32 * u + col;
-            return buf + B_QK + r * 128 + (((2 * ks + h) ^ swz8(r)) << 4);
-        }
-        const int r = 32 * (u - 2) + col;
-        return buf + B_KGT + r * 128 + (((2 * ks + h) ^ swz8(r)) << 4);
+        op.u = Ui[cb * 1024 + (cbk * 4 + wave) * 64 + lane];
+        op.gl = Gli[cb * 64 + lane];
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+            op.qg[s] = qg[64 * s];
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+            op.qk[s] = qk[64 * s];
     };
 
+    /* A segment's chunks are consecutive 64-token slices: token offsets
+     * follow from the first chunk, the length from the last. The log-decay
+     * travels with the operand set (phase A stores it once per lane). */
+    const int tok_seg = nc > 0 ? chunk_tok0[c0] : 0;
+    const int len_last = nc > 0 ? chunk_len[c0 + nc - 1] : 0;
+
+    auto step = [&](int ch, const BOps &op) {
+        const int ci = ch - c0;
+        const int t0 = tok_seg + CH * ci, L = ci + 1 < nc ? CH : len_last;
+        const float dec = fast_exp(op.gl);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *(bf16x4 *)&sT[c32][32 * wave + 8 * j + 4 * h] =
+                bf16x4{f2bf(S[4 * j]), f2bf(S[4 * j + 1]), f2bf(S[4 * j + 2]), f2bf(S[4 * j + 3])};
+        lds_barrier();
+        /* every LDS operand of a stage is read before its MFMAs: one wait */
+        bf16x8 sb[4][2];
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int jb = 0; jb < 2; jb++)
+                sb[s][jb] = *(const bf16x8 *)&sT[16 * jb + c16][32 * s + 8 * q4];
+        floatx4 V[2] = {}, O[2] = {};
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int jb = 0; jb < 2; jb++)
+                V[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.w[s], sb[s][jb], V[jb], 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int jb = 0; jb < 2; jb++)
+                O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qg[s], sb[s][jb], O[jb], 0, 0, 0);
+#pragma unroll
+        for (int jb = 0; jb < 2; jb++) {
+            bf16x4 p;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                p[i] = f2bf(bf2f(op.u[4 * jb + i]) - V[jb][i]);
+            *(bf16x4 *)&vT[16 * jb + c16][16 * wave + 4 * q4] = p;
+        }
+        lds_barrier();
+        bf16x8 vb[4], vb2[2][2];
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+            vb[s] = *(const bf16x8 *)&vT[c32][16 * s + 8 * h];
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int jb = 0; jb < 2; jb++)
+                vb2[s][jb] = *(const bf16x8 *)&vT[16 * jb + c16][32 * s + 8 * q4];
+        S = S * dec;
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+            S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kg[s], vb[s], S, 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int jb = 0; jb < 2; jb++)
+                O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qk[s], vb2[s][jb], O[jb], 0, 0, 0);
+        /* O (bf16) through this wave's LDS tile: 16-byte stores, 64 bytes a row */
+#pragma unroll
+        for (int jb = 0; jb < 2; jb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                ost[wave][4 * q4 + i][16 * jb + c16] = f2bf(O[jb][i]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int r = lane >> 2, c8 = 8 * (lane & 3);
+        const bf16x8 ov = *(const bf16x8 *)&ost[wave][r][c8];
+        if (16 * wave + r < L)
+            *(bf16x8 *)(o + ((size_t)(t0 + 16 * wave + r) * Hv + hv) * DV + col0 + c8) = ov;
+    };
+
+    /* three operand sets in rotation: chunk ci + 2 loads while ci runs. The
+     * loads are unconditional (past the end they repeat the last chunk) so
+     * the compiler's wait counts stay exact: a load skipped on one path makes
+     * the next use wait for every load in flight. */
     if (nc > 0) {
-#pragma unroll
-        for (int j = 0; j < 18; j++)
-            issue_load(j, c0, smem);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        lds_barrier();
-    }
-    for (int ci = 0; ci < nc; ci++) {
-        const int ch = c0 + ci;
-        const int t0 = chunk_tok0[ch], L = chunk_len[ch];
-        const float dec = fast_exp(Gli[(size_t)ch * Hv + hv]);
-        const bool more = ci + 1 < nc;
-        const uint32_t buf = (ci & 1) * B_BUF;
-        unsigned char *nbuf = smem + (buf ^ B_BUF);
-
-        bf16x8 Sb[8];
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++)
-            Sb[ks] = acc_as_b(S[ks >> 1], ks & 1);
-
-        bf16x8 ring[B_RING];
-#pragma unroll
-        for (int i = 0; i < B_RING; i++)
-            ring[i] = lds_read16(lds, addr_of(i, buf));
-        floatx16 Vacc[2] = {}, Oacc[2] = {};
-#pragma unroll
-        for (int i = 0; i < 32; i++) {
-            const bf16x8 a = ring[i % B_RING];
-            ring[i % B_RING] = lds_read16(lds, addr_of(i + B_RING, buf));
-            if (i % 3 == 0 && more)
-                issue_load(i / 3, ch + 1, nbuf);
-            const int ks = i >> 2, mt = (i >> 1) & 1;
-            if (i & 1)
-                Oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Sb[ks], Oacc[mt], 0, 0, 0);
-            else
-                Vacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Sb[ks], Vacc[mt], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
+        auto cl = [&](int ci) { return c0 + min(ci, nc - 1); };
+        BOps A, B, C;
+        load(cl(0), A);
+        load(cl(1), B);
+        for (int ci = 0; ci < nc; ci += 3) {
+            load(cl(ci + 2), C);
+            step(c0 + ci, A);
+            if (ci + 1 >= nc)
+                break;
+            load(cl(ci + 3), A);
+            step(c0 + ci + 1, B);
+            if (ci + 2 >= nc)
+                break;
+            load(cl(ci + 4), B);
+            step(c0 + ci + 2, C);
         }
-        /* V' = U - W S */
-        bf16x8 Vb[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const bf16x8 u = lds_read16(lds, buf + B_U + wave * 4096 + j * 1024 + lane * 16);
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                Vb[j][e] = f2bf(bf2f(u[e]) - Vacc[j >> 1][8 * (j & 1) + e]);
-        }
-#pragma unroll
-        for (int ti = 0; ti < 4; ti++)
-            S[ti] = S[ti] * dec;
-#pragma unroll
-        for (int i = 32; i < 56; i++) {
-            const bf16x8 a = ring[i % B_RING];
-            if (i + B_RING < 56)
-                ring[i % B_RING] = lds_read16(lds, addr_of(i + B_RING, buf));
-            if (i % 3 == 0 && i / 3 < 18 && more)
-                issue_load(i / 3, ch + 1, nbuf);
-            const int k = i - 32, ks = k / 6, u = k % 6;
-            if (u < 2)
-                Oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Vb[ks], Oacc[u], 0, 0, 0);
-            else
-                S[u - 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, Vb[ks], S[u - 2], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        /* the next stage has landed (waited before the stores below, which
-         * also count against vmcnt) */
-        if (more)
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        /* O -> fp32 o[token][hv][dv], transposed through this chunk's (now
-         * consumed) stage buffer so every store is 16 bytes of a row */
-        lds_barrier();
-        __attribute__((address_space(3))) float *ot =
-            (__attribute__((address_space(3))) float *)(smem + buf);
-#pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
-#pragma unroll
-            for (int rr = 0; rr < 16; rr++) {
-                const int t = 32 * mt + 8 * (rr >> 2) + 4 * h + (rr & 3);
-                ot[t * O_LDS + dv] = Oacc[mt][rr];
-            }
-        }
-        lds_barrier();
-#pragma unroll
-        for (int p = 0; p < 8; p++) { /* rows 16 wave + 2p + h, 32 lanes x 16 B */
-            const int t = 16 * wave + 2 * p + h;
-            if (t < L) {
-                const floatx4 v = *(__attribute__((address_space(3))) const floatx4 *)(
-                    ot + t * O_LDS + 4 * col);
-                *(floatx4 *)(o + ((size_t)(t0 + t) * Hv + hv) * DV + 4 * col) = v;
-            }
-        }
-        lds_barrier(); /* the o stores keep streaming */
     }
     if (S_out && seg == 0) {
 #pragma unroll
-        for (int ti = 0; ti < 4; ti++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int dk = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
-                S_out[((size_t)hv * DK + dk) * DV + dv] = S[ti][r];
-            }
+        for (int r = 0; r < 16; r++) {
+            const int dk = 32 * wave + 8 * (r >> 2) + 4 * h + (r & 3);
+            S_out[((size_t)hv * DK + dk) * DV + col0 + c32] = S[r];
         }
     }
 }
 
-/* y = bf16( w * bf16(o * rsqrt(mean o^2 + eps)) * silu(z) ): one wave per
- * (token, v-head) row, lane = 2 columns. REF src/kernels/gdn.cu:193-216. */
-__global__ __launch_bounds__(256) void gdn_norm_gate_kernel(const float *__restrict__ o,
+/* y = bf16( w * bf16(o * rsqrt(mean o^2 + eps)) * silu(z) ): 16 lanes per
+ * (token, v-head) row, 8 columns a lane. REF src/kernels/gdn.cu:193-216. */
+template <bool VEC>
+__global__ __launch_bounds__(256) void gdn_norm_gate_kernel(const bf16 *__restrict__ o,
                                                             const bf16 *__restrict__ z, int zs,
                                                             const float *__restrict__ w, float eps,
                                                             int rows, int Hv,
                                                             bf16 *__restrict__ y) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int s = threadIdx.x & 15;
     if (row >= rows)
-        return;
-    const int n = row / Hv, hv = row % Hv;
-    const float2 v = *(const float2 *)(o + (size_t)row * DV + 2 * lane);
-    const float ss = wave_sum(v.x * v.x + v.y * v.y);
+        return; /* whole 16-lane groups leave together */
+    const int n = row / Hv, hv = row - n * Hv;
+    const bf16x8 ov = *(const bf16x8 *)(o + (size_t)row * DV + 8 * s);
+    const bf16 *zr = z + (size_t)n * zs + hv * DV + 8 * s;
+    bf16x8 zv;
+    if constexpr (VEC) {
+        zv = *(const bf16x8 *)zr;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            zv[e] = zr[e];
+    }
+    float wl[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        wl[e] = w[8 * s + e];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        ss += bf2f(ov[e]) * bf2f(ov[e]);
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1)
+        ss += __shfl_xor(ss, m, 64);
     const float inv = rsqrtf(ss * (1.f / DV) + eps);
-    const bf16 *zr = z + (size_t)n * zs + hv * DV + 2 * lane;
-    const float n0 = bf2f(f2bf(v.x * inv)) * w[2 * lane];
-    const float n1 = bf2f(f2bf(v.y * inv)) * w[2 * lane + 1];
-    bf16 *yr = y + (size_t)row * DV + 2 * lane;
-    yr[0] = f2bf(n0 * silu_f(bf2f(zr[0])));
-    yr[1] = f2bf(n1 * silu_f(bf2f(zr[1])));
+    bf16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        r[e] = f2bf(bf2f(f2bf(bf2f(ov[e]) * inv)) * wl[e] * silu_f(bf2f(zv[e])));
+    *(bf16x8 *)(y + (size_t)row * DV + 8 * s) = r;
 }
 
 } // namespace
@@ -713,13 +773,17 @@ extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t 
                        0, stream, (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, g, beta,
                        ck->chunk_tok0, ck->chunk_len, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->Qg,
                        (bf16 *)ws->QK, (bf16 *)ws->KgT, (bf16 *)ws->U, ws->Glast);
-    hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)ck->num_segments, (unsigned)Hv),
-                       dim3(256), 0, stream, (const bf16 *)ws->W, (const bf16 *)ws->Qg,
-                       (const bf16 *)ws->QK, (const bf16 *)ws->KgT, (const bf16 *)ws->U, ws->Glast,
-                       ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk, S_in, S_out,
-                       Hv, ck->num_chunks, ws->O);
+    const int units = ck->num_segments * Hv;
+    hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)(NCB * CEIL_DIV(units, 8) * 8)),
+                       dim3(256), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
+                       (const bf16x8 *)ws->QK, (const bf16x8 *)ws->KgT, (const bf16x8 *)ws->U,
+                       ws->Glast, ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk,
+                       S_in, S_out, Hv, units, (bf16 *)ws->O);
     const int rows = N * Hv;
-    hipLaunchKernelGGL(gdn_norm_gate_kernel, dim3((unsigned)CEIL_DIV(rows, 4)), dim3(256), 0,
-                       stream, ws->O, (const bf16 *)z, z_stride, norm_w, eps, rows, Hv, (bf16 *)y);
+    const bool zvec = z_stride % 8 == 0 && ((uintptr_t)z & 15) == 0;
+    hipLaunchKernelGGL(zvec ? gdn_norm_gate_kernel<true> : gdn_norm_gate_kernel<false>,
+                       dim3((unsigned)CEIL_DIV(rows, 16)), dim3(256), 0, stream,
+                       (const bf16 *)ws->O, (const bf16 *)z, z_stride, norm_w, eps, rows, Hv,
+                       (bf16 *)y);
     return hipGetLastError();
 }

@@ -92,25 +92,30 @@ typedef struct cujev_chunks {
 } cujev_chunks;
 
 /* Scratch of the chunked scan. Per (chunk, v-head), written by the parallel
- * first phase in the operand layouts of the sequential second phase:
- * W, q e^G, masked QK^T and (k e^{Glast-G})^T as bf16 (columns permuted),
- * U in accumulator-fragment order, and the chunk's total log-decay. O is the
- * unnormalised output [N][Hv][128] fp32 before the gated norm. */
+ * first phase in the MFMA operand-fragment order of the sequential second
+ * phase, so each of its lanes reads 16 contiguous bytes per fragment and a
+ * wave reads 1 KiB runs:
+ *   W, q e^G   [64][128] as 16x16x32 A fragments (4 row blocks x 4 k-steps)
+ *   QK^T masked [64][64] as 16x16x32 A fragments (4 x 2)
+ *   (k e^{Glast-G})^T [128][64] as 32x32x16 A fragments (4 x 4)
+ *   U          [64][128] as 16x16 accumulator fragments per 32-column block
+ * all bf16, plus the chunk's total log-decay (one copy per lane). O is the unnormalised output
+ * [N][Hv][128] bf16 before the gated norm. */
 typedef struct cujev_gdn_scratch {
-    void *W;      /* bf16 [chunks][Hv][64][128]  */
-    void *Qg;     /* bf16 [chunks][Hv][64][128]  */
-    void *QK;     /* bf16 [chunks][Hv][64][64]   */
-    void *KgT;    /* bf16 [chunks][Hv][128][64]  */
-    void *U;      /* bf16 [chunks][Hv][4][2][64][16] */
-    float *Glast; /* [chunks][Hv] */
-    float *O;     /* [N][Hv][128] */
+    void *W;      /* bf16 [chunks][Hv][1024][8] */
+    void *Qg;     /* bf16 [chunks][Hv][1024][8] */
+    void *QK;     /* bf16 [chunks][Hv][512][8]  */
+    void *KgT;    /* bf16 [chunks][Hv][1024][8] */
+    void *U;      /* bf16 [chunks][Hv][1024][8] */
+    float *Glast; /* [chunks][Hv][64] (64 equal copies) */
+    void *O;      /* bf16 [N][Hv][128] */
 } cujev_gdn_scratch;
 
 static inline size_t cujev_align256(size_t x) { return (x + 255) / 256 * 256; }
 static inline size_t cujev_gdn_scratch_bytes(int num_chunks, int Hv, int N) {
     const size_t ch = (size_t)num_chunks * Hv;
     return 4 * cujev_align256(ch * 64 * 128 * 2) + cujev_align256(ch * 64 * 64 * 2) +
-           cujev_align256(ch * 4) + cujev_align256((size_t)N * Hv * 128 * 4);
+           cujev_align256(ch * 64 * 4) + cujev_align256((size_t)N * Hv * 128 * 2);
 }
 /* Carve the scratch of cujev_gdn_scratch_bytes() starting at `base`. */
 static inline cujev_gdn_scratch cujev_gdn_scratch_carve(void *base, int num_chunks, int Hv) {
@@ -128,8 +133,8 @@ static inline cujev_gdn_scratch cujev_gdn_scratch_carve(void *base, int num_chun
     s.QK = p;
     p += cujev_align256(ch * 64 * 64 * 2);
     s.Glast = (float *)p;
-    p += cujev_align256(ch * 4);
-    s.O = (float *)p;
+    p += cujev_align256(ch * 64 * 4);
+    s.O = p;
     return s;
 }
 
