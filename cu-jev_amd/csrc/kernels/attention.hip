@@ -415,40 +415,40 @@ __global__ __launch_bounds__(320) void attn_prep_kernel(
         wl[e] = w[4 * lane + e];
     const bool rotates = lane < 2 * half_lanes;
     const bool first = lane < half_lanes;
-    const int fi0 = first ? 4 * lane : 4 * lane - hr;
-    /* every load of the 16 tokens is issued up front: the rows, the positions
-     * (lane t holds token t's), and each token's RoPE row one token ahead */
+    const int fi0 = rotates ? (first ? 4 * lane : 4 * lane - hr) : 0;
+    /* Every load is issued before any math, unconditionally (token indices
+     * clamped into the block; a load skipped on some path would make each
+     * later use wait for all loads in flight): the 16 rows, the positions
+     * (lane t holds token t's), each token's 4 (cos, sin) pairs, and the V
+     * rows of the transpose. */
     const bf16 *src0 = wave < 4 ? proj + (kh * 4 + wave) * 512 : proj + Hq * 512 + kh * 256;
     bf16x4 raw[PREP_TOK];
 #pragma unroll
+    for (int t = 0; t < PREP_TOK; t++)
+        raw[t] = *(const bf16x4 *)(src0 + (size_t)(n0 + min(t, nt - 1)) * ps + 4 * lane);
+    const int pos_lane = pos[n0 + min(lane, nt - 1)];
+    float4 rc[PREP_TOK][2]; /* (cos, sin) of dims fi0 .. fi0 + 3 */
+#pragma unroll
     for (int t = 0; t < PREP_TOK; t++) {
-        raw[t] = bf16x4{};
-        if (t < nt)
-            raw[t] = *(const bf16x4 *)(src0 + (size_t)(n0 + t) * ps + 4 * lane);
+        const int p = __builtin_amdgcn_readlane(pos_lane, t);
+        const float4 *row = (const float4 *)(rope + (size_t)p * hr + fi0);
+        rc[t][0] = row[0];
+        rc[t][1] = row[1];
     }
-    const int pos_lane = lane < nt ? pos[n0 + lane] : 0;
-    float2 cs_next[4] = {};
-    auto load_rope = [&](int t, float2 (&c)[4]) {
-        const int p = __shfl(pos_lane, t, 64);
-        if (rotates) {
-            const float2 *row = rope + (size_t)p * hr + fi0;
+    bf16x8 vrow[2]; /* V transpose items idx = tid, tid + 320 */
+    const bf16 *vsrc = proj + Hq * 512 + Hkv * 256 + kh * 256;
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                c[e] = row[e];
-        }
-    };
-    load_rope(0, cs_next);
+    for (int k = 0; k < 2; k++) {
+        const int idx = min((int)threadIdx.x + 320 * k, PREP_TOK * 32 - 1);
+        const int t = min(idx >> 5, nt - 1), c = idx & 31;
+        vrow[k] = *(const bf16x8 *)(vsrc + (size_t)(n0 + t) * ps + 8 * c);
+    }
+
 #pragma unroll
     for (int t = 0; t < PREP_TOK; t++) {
-        if (t >= nt)
-            break;
+        if (t >= nt) /* no break: the loop must unroll so raw[t], rc[t] stay in registers */
+            continue;
         const int nn = n0 + t;
-        float2 cs_cur[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            cs_cur[e] = cs_next[e];
-        if (t + 1 < nt)
-            load_rope(t + 1, cs_next);
         float x[4];
         float ss = 0.f;
 #pragma unroll
@@ -466,10 +466,12 @@ __global__ __launch_bounds__(320) void attn_prep_kernel(
         for (int e = 0; e < 4; e++)
             partner[e] = __shfl_xor(x[e], half_lanes, 64);
         if (rotates) {
+            const float cz[8] = {rc[t][0].x, rc[t][0].y, rc[t][0].z, rc[t][0].w,
+                                 rc[t][1].x, rc[t][1].y, rc[t][1].z, rc[t][1].w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float2 c = cs_cur[e];
-                x[e] = first ? x[e] * c.x - partner[e] * c.y : x[e] * c.x + partner[e] * c.y;
+                const float c = cz[2 * e], sn = cz[2 * e + 1];
+                x[e] = first ? x[e] * c - partner[e] * sn : x[e] * c + partner[e] * sn;
             }
         }
         bf16x4 o;
@@ -487,14 +489,14 @@ __global__ __launch_bounds__(320) void attn_prep_kernel(
     }
 
     /* V: [16 tokens][256] -> LDS [256][16] -> 256 vt rows of 16 columns */
-    for (int idx = threadIdx.x; idx < PREP_TOK * 32; idx += 320) {
-        const int t = idx >> 5, c = idx & 31;
-        if (t < nt) {
-            bf16x8 v = *(const bf16x8 *)(proj + (size_t)(n0 + t) * ps + Hq * 512 + Hkv * 256 +
-                                         kh * 256 + 8 * c);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int idx = threadIdx.x + 320 * k;
+        if (idx < PREP_TOK * 32) {
+            const int t = idx >> 5, c = idx & 31;
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                vs[8 * c + e][t] = v[e];
+                vs[8 * c + e][t] = vrow[k][e];
         }
     }
     __syncthreads();

@@ -32,8 +32,10 @@ DEV bf16 f2bf(float x) { return (bf16)x; } /* round to nearest even */
 /* 2^x on the transcendental unit; exact -inf -> 0. */
 DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 DEV float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * CUJEV_LOG2E); }
-DEV float sigmoid_f(float x) { return 1.f / (1.f + fast_exp(-x)); }
-DEV float silu_f(float x) { return x / (1.f + fast_exp(-x)); }
+/* 1/(1+e^-x) with the hardware reciprocal (v_rcp_f32, about 1 ulp) rather
+ * than an IEEE division sequence. */
+DEV float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.f + fast_exp(-x)); }
+DEV float silu_f(float x) { return x * __builtin_amdgcn_rcpf(1.f + fast_exp(-x)); }
 /* log(1+e^x), linear above 20 like torch.nn.functional.softplus. */
 DEV float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 

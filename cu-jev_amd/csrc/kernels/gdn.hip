@@ -41,14 +41,16 @@ constexpr int CH = 64;  /* chunk length   */
 /* conv + gates                                                            */
 /* ---------------------------------------------------------------------- */
 /* One group of 16 lanes = one 128-channel head slice of PREP_T consecutive
- * tokens; lane s holds channels 8s..8s+7. The PREP_T + 3 pre-conv rows the
- * group needs are loaded once (16 bytes per lane and row when the projection
- * rows allow it) and the 4-tap window slides over them in registers. Groups
- * are numbered token block fastest, 16 per 256-thread workgroup. Groups of
- * head h < Hv also produce g and beta of v-head h for their tokens. */
+ * tokens; lane s holds channels 8s..8s+7. Every load the group needs (the
+ * PREP_T + 3 pre-conv rows, conv weights, the state's conv tail, segment
+ * starts, b and a) is issued first, unconditionally (row indices clamped
+ * into the batch; a load skipped on some path would make every later use
+ * wait for all loads in flight), then the 4-tap window slides over the rows
+ * in registers. Groups are numbered token block fastest, 16 per 256-thread
+ * workgroup. Groups of head h < Hv also produce g and beta of v-head h. */
 constexpr int PREP_T = 8;
 
-template <bool VEC>
+template <bool VEC, bool TAIL>
 __global__ __launch_bounds__(256) void gdn_conv_prep_kernel(
     const bf16 *__restrict__ proj, int ps, const float *__restrict__ conv_w,
     const float *__restrict__ conv_in, const int32_t *__restrict__ own_base,
@@ -65,39 +67,48 @@ __global__ __launch_bounds__(256) void gdn_conv_prep_kernel(
     const int C = nheads * DK;
     const int c0 = head * DK + 8 * s;
 
-    if (head < Hv && s < PREP_T && n0 + s < N) {
-        const int n = n0 + s;
-        const bf16 *ab = proj + (size_t)n * ps + C + Hv * DV; /* b then a */
-        const float bv = bf2f(ab[head]), av = bf2f(ab[Hv + head]);
-        bo[(size_t)n * Hv + head] = sigmoid_f(bv);
-        go[(size_t)n * Hv + head] = A_neg_exp[head] * softplus_f(av + dt_bias[head]);
+    /* ---- loads ---- */
+    bf16x8 x[PREP_T + 3];
+#pragma unroll
+    for (int r = 0; r < PREP_T + 3; r++) {
+        const int row = min(max(n0 - 3 + r, 0), N - 1);
+        const bf16 *src = proj + (size_t)row * ps + c0;
+        if constexpr (VEC) {
+            x[r] = *(const bf16x8 *)src;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                x[r][e] = src[e];
+        }
     }
-
     float w[8][4];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
         const float4 t = *(const float4 *)(conv_w + (size_t)(c0 + e) * 4);
-        w[e][0] = t.x;
-        w[e][1] = t.y;
-        w[e][2] = t.z;
-        w[e][3] = t.w;
+        w[e][0] = t.x, w[e][1] = t.y, w[e][2] = t.z, w[e][3] = t.w;
     }
-    bf16x8 x[PREP_T + 3];
+    float tail[24]; /* conv_in[c0 + e][j] at 3e + j */
+    if constexpr (TAIL) {
 #pragma unroll
-    for (int r = 0; r < PREP_T + 3; r++) {
-        const int row = n0 - 3 + r;
-        x[r] = bf16x8{};
-        if (row >= 0 && row < N) {
-            const bf16 *src = proj + (size_t)row * ps + c0;
-            if constexpr (VEC) {
-                x[r] = *(const bf16x8 *)src;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    x[r][e] = src[e];
-            }
+        for (int i = 0; i < 6; i++) {
+            const float4 t = *(const float4 *)(conv_in + (size_t)c0 * 3 + 4 * i);
+            tail[4 * i] = t.x, tail[4 * i + 1] = t.y, tail[4 * i + 2] = t.z, tail[4 * i + 3] = t.w;
         }
     }
+    const int nt = min(n0 + (s & (PREP_T - 1)), N - 1); /* lane s: token n0 + s%8 */
+    const int base_s = own_base[nt];
+    const int hg = min(head, Hv - 1);
+    const bf16 *ab = proj + (size_t)nt * ps + C + Hv * DV; /* b then a */
+    const float bv = bf2f(ab[hg]), av = bf2f(ab[Hv + hg]);
+    const float aneg = A_neg_exp[hg], dtb = dt_bias[hg];
+
+    /* ---- gates ---- */
+    if (head < Hv && s < PREP_T && n0 + s < N) {
+        bo[(size_t)(n0 + s) * Hv + head] = sigmoid_f(bv);
+        go[(size_t)(n0 + s) * Hv + head] = aneg * softplus_f(av + dtb);
+    }
+
+    /* ---- conv + SiLU (+ l2 norm) ---- */
     bf16 *dst;
     float scale = 1.f;
     const bool norm = head < 2 * Hk;
@@ -110,31 +121,37 @@ __global__ __launch_bounds__(256) void gdn_conv_prep_kernel(
         dst = vo + (size_t)(head - 2 * Hk) * DV;
     }
     const int tok_stride = head < 2 * Hk ? Hk * DK : Hv * DV;
-    int local_of[PREP_T]; /* all segment offsets fetched up front, not per step */
-#pragma unroll
-    for (int j = 0; j < PREP_T; j++)
-        local_of[j] = n0 + j < N ? n0 + j - own_base[n0 + j] : 0;
+    const int gl0 = threadIdx.x & 48; /* first lane of this group */
 #pragma unroll
     for (int j = 0; j < PREP_T; j++) {
         const int n = n0 + j;
+        const int local = n - __shfl(base_s, gl0 + j, 64);
         if (n >= N)
-            continue; /* uniform over the group */
-        const int local = local_of[j];
+            continue; /* uniform over the group; no loads below */
         float y[8];
 #pragma unroll
         for (int e = 0; e < 8; e++)
             y[e] = 0.f;
+        if (local >= 3) { /* every tap inside the segment */
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int tau = local - 3 + i; /* local index of the tap */
-            if (tau >= 0) {
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    y[e] += w[e][i] * bf2f(x[j + i][e]);
-            } else if (conv_in) {
+            for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int e = 0; e < 8; e++)
-                    y[e] += w[e][i] * conv_in[(size_t)(c0 + e) * 3 + tau + 3];
+                    y[e] = fmaf(w[e][i], bf2f(x[j + i][e]), y[e]);
+        } else { /* taps before the segment start: the state's tail or 0 */
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tau = local - 3 + i; /* local index of the tap */
+                const float mx = tau >= 0 ? 1.f : 0.f;
+                const float m0 = tau == -3 ? 1.f : 0.f, m1 = tau == -2 ? 1.f : 0.f,
+                            m2 = tau == -1 ? 1.f : 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float xi = mx * bf2f(x[j + i][e]);
+                    if constexpr (TAIL)
+                        xi += m0 * tail[3 * e] + m1 * tail[3 * e + 1] + m2 * tail[3 * e + 2];
+                    y[e] = fmaf(w[e][i], xi, y[e]);
+                }
             }
         }
         float ss = 0.f;
@@ -302,11 +319,21 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
         }
         const int j = 32 * tj + col;
         const float Gj = sm.G[j];
+        /* rows i = 32ti + 8m + 4h + 0..3: their G and beta four at a time,
+         * read unconditionally (a read under the mask becomes a branch) */
+        float Gi[16], Bi[16];
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const float4 a = rd4(&sm.G[32 * ti + 8 * m + 4 * h]);
+            const float4 b = rd4(&sm.sV[32 * ti + 8 * m + 4 * h]);
+            Gi[4 * m] = a.x, Gi[4 * m + 1] = a.y, Gi[4 * m + 2] = a.z, Gi[4 * m + 3] = a.w;
+            Bi[4 * m] = b.x, Bi[4 * m + 1] = b.y, Bi[4 * m + 2] = b.z, Bi[4 * m + 3] = b.w;
+        }
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int i = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
-            const float dec = i >= j ? fast_exp(sm.G[i] - Gj) : 0.f;
-            sm.AT[i][j] = i > j ? sm.sV[i] * kk[r] * dec : 0.f;
+            const float dec = fast_exp(fminf(Gi[r] - Gj, 0.f));
+            sm.AT[i][j] = i > j ? Bi[r] * kk[r] * dec : 0.f;
             sm.QK[i][j] = f2bf(i >= j ? qk[r] * dec : 0.f);
         }
     }
@@ -334,9 +361,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
     }
 
     /* ---- 3. T = (I + A)^-1 in place ----
-     * 3a: wave w inverts diagonal block w, lane c < 16 owning column c. Row i
-     * of the block is read (all lanes, broadcast) before any lane writes row
-     * i, and no later step reads it again. */
+     * 3a: wave w inverts diagonal block w, lane c < 16 owning column c; the
+     * block is read (all lanes, broadcast) before any lane writes it. */
     if (lane < 16) {
         const int b0 = 16 * wave, c = lane;
         float t[16];
@@ -355,9 +381,13 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
                     acc = fmaf(a.w, t[k4 + 3], acc);
             }
             t[i] = (i == c ? 1.f : 0.f) - acc;
+        }
+        /* stores only after every read of the block: the reads can all be
+         * issued up front (a store in the loop would keep them in order) */
+#pragma unroll
+        for (int i = 0; i < 16; i++)
             if (i >= c)
                 sm.AT[b0 + i][b0 + c] = t[i];
-        }
     }
     lds_barrier();
     /* 3b: inside 32x32 diagonal block p (wave p): T_10 = -T_11 (A_10 T_00),
@@ -748,7 +778,8 @@ extern "C" hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const
     const int nheads = 2 * Hk + Hv;
     const int groups = CEIL_DIV(N, PREP_T) * nheads;
     const bool vec = proj_stride % 8 == 0 && ((uintptr_t)proj & 15) == 0;
-    auto kern = vec ? gdn_conv_prep_kernel<true> : gdn_conv_prep_kernel<false>;
+    auto kern = vec ? (conv_in ? gdn_conv_prep_kernel<true, true> : gdn_conv_prep_kernel<true, false>)
+                    : (conv_in ? gdn_conv_prep_kernel<false, true> : gdn_conv_prep_kernel<false, false>);
     hipLaunchKernelGGL(kern, dim3((unsigned)CEIL_DIV(groups, 16)), dim3(256), 0, stream,
                        (const bf16 *)proj, proj_stride, conv_w, conv_in, own_base, A_neg_exp,
                        dt_bias, N, Hk, Hv, (bf16 *)q, (bf16 *)k, (bf16 *)v, g, beta);
