@@ -282,6 +282,7 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
         {(void **)&m->xb, N * H * 2},
         {(void **)&m->proj, N * (size_t)m->w_proj * 2},
         {(void **)&m->y, N * H * 2},
+        {(void **)&m->ypart, (size_t)CUJEV_GEMM_SMALL_MAX_SPLITS * CUJEV_GEMM_SMALL_MAX_N * H * 4},
         {(void **)&m->q, N * (size_t)m->Hq * m->D * 2},
         {(void **)&m->mix_out, mix * 2},
         {(void **)&m->br_k, br_kv},

@@ -78,6 +78,7 @@ struct cujev_model {
     bf16_t *xb;      /* [N,H] normed input */
     bf16_t *proj;    /* [N, w_proj] */
     bf16_t *y;       /* [N,H] */
+    float *ypart;    /* [CUJEV_GEMM_SMALL_MAX_SPLITS][CUJEV_GEMM_SMALL_MAX_N][H]: split-K partials of the few-token GEMMs */
     bf16_t *q;       /* [N,Hq,256] prescaled */
     bf16_t *mix_out; /* [N, max(Hq*256, V)] */
     bf16_t *br_k, *br_vt;

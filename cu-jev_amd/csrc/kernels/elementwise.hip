@@ -26,55 +26,90 @@ __global__ __launch_bounds__(NT) void embed_kernel(const int32_t *__restrict__ t
 }
 
 /* One block per output row r (source row rows ? rows[r] : r):
- *   v = x[src] (+ y[src] if y);  if (y && !rows) x[src] = v;
- *   out[r] = bf16(v * rsqrt(mean v^2 + eps) * w) */
+ *   v = x[src] + d (d from bf16 y, or bf16 of the split-K partial sum of yp);
+ *   x[src] = v when there is a d and !rows;
+ *   out[r] = bf16(v * rsqrt(mean v^2 + eps) * w)
+ * Thread t holds the float4 groups t + 256k (k < 4, H <= 4096). Every load
+ * (x, the added term, w) is issued before the reduction, with indices clamped
+ * into the row: one memory round trip per row. */
+constexpr int RN_K = 4;
+template <int SPLITS> /* 0: bf16 y or nothing; > 0: that many fp32 partials, all loads up front */
 __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(float *__restrict__ x,
                                                          const bf16 *__restrict__ y,
+                                                         const float *__restrict__ yp, int splits,
+                                                         size_t split_stride,
                                                          const float *__restrict__ w,
                                                          bf16 *__restrict__ out, int H, float eps,
                                                          const int32_t *__restrict__ rows) {
     __shared__ float scratch[NT / 64];
     const int r = blockIdx.x;
     const int src = rows ? rows[r] : r;
+    const int ng = H / 4;
     float *xr = x + (size_t)src * H;
-    const bf16 *yr = y ? y + (size_t)src * H : nullptr;
-    const bool write_back = y && !rows;
-    /* H <= 16 * 4 * NT: keep the row in registers */
-    float4 v[16];
+    float4 v[RN_K], ww[RN_K];
+#pragma unroll
+    for (int k = 0; k < RN_K; k++) {
+        const int g = min((int)threadIdx.x + k * NT, ng - 1);
+        v[k] = *(const float4 *)(xr + 4 * g);
+        ww[k] = *(const float4 *)(w + 4 * g);
+    }
+    const bool add = y || yp;
+    if (add) {
+        float4 d[RN_K];
+        if (y) {
+#pragma unroll
+            for (int k = 0; k < RN_K; k++) {
+                const int g = min((int)threadIdx.x + k * NT, ng - 1);
+                const bf16x4 b = *(const bf16x4 *)(y + (size_t)src * H + 4 * g);
+                d[k] = make_float4(bf2f(b[0]), bf2f(b[1]), bf2f(b[2]), bf2f(b[3]));
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < RN_K; k++)
+                d[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 t[SPLITS > 0 ? SPLITS : 1][RN_K];
+#pragma unroll
+            for (int sp = 0; sp < SPLITS; sp++)
+#pragma unroll
+                for (int k = 0; k < RN_K; k++) {
+                    const int g = min((int)threadIdx.x + k * NT, ng - 1);
+                    t[sp][k] = *(const float4 *)(yp + sp * split_stride + (size_t)src * H + 4 * g);
+                }
+#pragma unroll
+            for (int sp = 0; sp < SPLITS; sp++) /* split order: deterministic */
+#pragma unroll
+                for (int k = 0; k < RN_K; k++)
+                    d[k].x += t[sp][k].x, d[k].y += t[sp][k].y, d[k].z += t[sp][k].z,
+                        d[k].w += t[sp][k].w;
+#pragma unroll
+            for (int k = 0; k < RN_K; k++) /* the GEMM output's bf16 rounding */
+                d[k] = make_float4(bf2f(f2bf(d[k].x)), bf2f(f2bf(d[k].y)), bf2f(f2bf(d[k].z)),
+                                   bf2f(f2bf(d[k].w)));
+        }
+#pragma unroll
+        for (int k = 0; k < RN_K; k++)
+            v[k].x += d[k].x, v[k].y += d[k].y, v[k].z += d[k].z, v[k].w += d[k].w;
+    }
     float ss = 0.f;
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const int i = (threadIdx.x + k * NT) * 4;
-        if (i < H) {
-            float4 a = *(const float4 *)(xr + i);
-            if (yr) {
-                bf16x4 b = *(const bf16x4 *)(yr + i);
-                a.x += bf2f(b[0]);
-                a.y += bf2f(b[1]);
-                a.z += bf2f(b[2]);
-                a.w += bf2f(b[3]);
-                if (write_back)
-                    *(float4 *)(xr + i) = a;
-            }
-            v[k] = a;
-            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    for (int k = 0; k < RN_K; k++) {
+        const int g = threadIdx.x + k * NT;
+        if (g < ng) {
+            ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
+            if (add && !rows)
+                *(float4 *)(xr + 4 * g) = v[k];
         }
     }
     ss = block_sum(ss, scratch);
     const float inv = rsqrtf(ss / H + eps);
     bf16 *orow = out + (size_t)r * H;
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const int i = (threadIdx.x + k * NT) * 4;
-        if (i < H) {
-            const float4 ww = *(const float4 *)(w + i);
-            bf16x4 o;
-            o[0] = f2bf(v[k].x * inv * ww.x);
-            o[1] = f2bf(v[k].y * inv * ww.y);
-            o[2] = f2bf(v[k].z * inv * ww.z);
-            o[3] = f2bf(v[k].w * inv * ww.w);
-            *(bf16x4 *)(orow + i) = o;
-        }
+    for (int k = 0; k < RN_K; k++) {
+        const int g = threadIdx.x + k * NT;
+        if (g < ng)
+            *(bf16x4 *)(orow + 4 * g) =
+                bf16x4{f2bf(v[k].x * inv * ww[k].x), f2bf(v[k].y * inv * ww[k].y),
+                       f2bf(v[k].z * inv * ww[k].z), f2bf(v[k].w * inv * ww[k].w)};
     }
 }
 
@@ -135,15 +170,30 @@ extern "C" hipError_t k_embed(const int32_t *tokens, const bf16_t *E, float *x, 
     return hipGetLastError();
 }
 
-extern "C" hipError_t k_add_rmsnorm(float *x, const bf16_t *y, const float *w, bf16_t *out, int N,
-                                    int H, float eps, const int32_t *rows, int R, hipStream_t s) {
+extern "C" hipError_t k_add_rmsnorm(float *x, const bf16_t *y, const float *yp, int splits,
+                                    const float *w, bf16_t *out, int N, int H, float eps,
+                                    const int32_t *rows, int R, hipStream_t s) {
     const int nrows = rows ? R : N;
     if (nrows <= 0)
         return hipSuccess;
-    if (H % 4 || H > 16 * 4 * NT)
+    if (H % 4 || H > RN_K * 4 * NT || (yp && (y || splits < 1)))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)nrows), dim3(NT), 0, s, x,
-                       (const bf16 *)y, w, (bf16 *)out, H, eps, rows);
+#define CUJEV_RN_LAUNCH(S)                                                                   \
+    hipLaunchKernelGGL(add_rmsnorm_kernel<S>, dim3((unsigned)nrows), dim3(NT), 0, s, x,       \
+                       (const bf16 *)y, yp, splits, (size_t)N * H, w, (bf16 *)out, H, eps, rows)
+    switch (yp ? splits : 0) {
+    case 0: CUJEV_RN_LAUNCH(0); break;
+    case 1: CUJEV_RN_LAUNCH(1); break;
+    case 2: CUJEV_RN_LAUNCH(2); break;
+    case 3: CUJEV_RN_LAUNCH(3); break;
+    case 4: CUJEV_RN_LAUNCH(4); break;
+    case 5: CUJEV_RN_LAUNCH(5); break;
+    case 6: CUJEV_RN_LAUNCH(6); break;
+    case 7: CUJEV_RN_LAUNCH(7); break;
+    case 8: CUJEV_RN_LAUNCH(8); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef CUJEV_RN_LAUNCH
     return hipGetLastError();
 }
 

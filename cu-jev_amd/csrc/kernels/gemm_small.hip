@@ -1,0 +1,268 @@
+/* Weight-streaming GEMM for few tokens (gfx950): Y[N, M] = X[N, K] . W[M, K]^T
+ * with N <= 96, bf16 in, fp32 accumulate. This is the eval-time shape of
+ * every projection (the reference runs them through cuBLAS GemmEx,
+ * src/kernels/elementwise.cu:56-75): the weights are read exactly once and
+ * the time is the HBM stream of W, so the kernel is built around keeping
+ * that stream full rather than around MFMA tiling.
+ *
+ *  - A workgroup owns 64 consecutive rows of W (16 per wave) and a K range;
+ *    every wave streams its 16 rows straight from HBM into registers, three
+ *    128-wide K chunks ahead of the MFMAs (v_mfma_f32_16x16x32_bf16 with W
+ *    as the A operand, 16 tokens per B fragment).
+ *  - X (tiny, L2-resident) goes to an LDS ring by buffer DMA, the same three
+ *    chunks ahead, and is shared by the four waves. Loads complete in issue
+ *    order, so every wait is for loads issued three steps earlier.
+ *  - A lane's 16 A-operand values for one 64-wide k step are 32 contiguous
+ *    bytes of its W row (k = 64j + 16(l/16) + 0..15); the two MFMAs of the
+ *    step take the halves, and the B fragments are read from LDS with the
+ *    same k assignment, so the product is the plain dot product.
+ *  - Short M (the 2560-wide outputs) splits K over blockIdx.y. Splits write
+ *    fp32 partials P[split][N][M] that the consumer (the residual add +
+ *    RMSNorm) sums in a fixed order: results are deterministic, and the sum
+ *    is rounded to bf16 like a bf16-output GEMM.
+ *  - GATED=true is the fused gate|up projection (W rows [gate I | up I]):
+ *    a workgroup takes 32 gate rows and the same 32 up rows (waves 0-1 and
+ *    2-3), the up accumulators cross to the gate waves through LDS, and the
+ *    output is act = bf16(silu(bf16 gate) * bf16 up) [N][I] directly, the
+ *    rounding points of a bf16 GEMM followed by the activation pass.
+ * All loads are unconditional (indices clamped into range): a load skipped
+ * on one path would make the next use wait for every load in flight. */
+#include "common.h"
+#include "kernels.h"
+
+namespace CUJEV_KNS {
+namespace {
+
+constexpr int SG_BM = 64;  /* W rows per workgroup */
+constexpr int SG_KC = 128; /* K per chunk          */
+constexpr int SG_NS = 4;   /* pipeline depth: chunk c + 3 loads while c computes */
+
+DEV bf16x8 ldg8(const bf16 *p) { return *(const bf16x8 *)p; }
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+/* Target builtins live in plain device functions: a template kernel that
+ * names them directly gets no host-side launch stub. */
+/* s_waitcnt with only the vector-memory count constrained (gfx9 encoding:
+ * vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima). The
+ * counts used are 4 + 2 (NB + 4), NB = 1..6; others wait for everything. */
+#define SG_VM(v) __builtin_amdgcn_s_waitcnt(((v) & 15) | (((v) >> 4) << 14) | (7 << 4) | (15 << 8))
+DEV void sg_wait_vm(int vm) {
+    switch (vm) {
+    case 14: SG_VM(14); break;
+    case 16: SG_VM(16); break;
+    case 18: SG_VM(18); break;
+    case 20: SG_VM(20); break;
+    case 22: SG_VM(22); break;
+    case 24: SG_VM(24); break;
+    default: SG_VM(0); break;
+    }
+}
+#undef SG_VM
+/* 16 bytes per lane from base + voff + soff into LDS at dst + 16 * lane;
+ * bytes past `bytes` read as zero */
+DEV void sg_dma16(const void *base, uint32_t bytes, unsigned char *dst, uint32_t voff, int soff) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, voff, soff, 0, 0);
+}
+DEV bf16x8 sg_lds16(const unsigned char *base, uint32_t off) {
+    return *(__attribute__((address_space(3))) const bf16x8 *)(
+        (__attribute__((address_space(3))) const unsigned char *)base + off);
+}
+
+template <int NB, bool GATED, bool PART>
+__global__ __launch_bounds__(256, 2) void gemm_small_kernel(const bf16 *__restrict__ X, int ldx,
+                                                            const bf16 *__restrict__ W, int N,
+                                                            int K, int KS, bf16 *__restrict__ Y,
+                                                            int ldy, float *__restrict__ P, int M) {
+    /* X ring: SG_NS stages of NB*16 token rows x 128 k, rows of 256 bytes
+     * with the 16-byte slots XOR-swizzled by (row & 15) */
+    constexpr int XSTAGE = NB * 16 * 256;
+    __shared__ __attribute__((aligned(1024))) unsigned char xs[SG_NS * XSTAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4, c16 = lane & 15;
+    const int split = blockIdx.y;
+    const int kb = split * KS, nch = KS / SG_KC;
+    /* this wave's first W row (GATED: M = 2I, 32 gate rows + the same 32 up rows) */
+    const int wr0 = GATED ? blockIdx.x * 32 + 16 * (wave & 1) + (wave >> 1) * (M / 2)
+                          : blockIdx.x * SG_BM + 16 * wave;
+
+    const bf16 *wrow = W + (size_t)(wr0 + c16) * K + kb + 16 * q;
+    auto load_w = [&](int c, bf16x8 (&wf)[4]) {
+        const bf16 *p = wrow + SG_KC * min(c, nch - 1);
+        wf[0] = ldg8(p);
+        wf[1] = ldg8(p + 8);
+        wf[2] = ldg8(p + 64);
+        wf[3] = ldg8(p + 72);
+    };
+    /* X chunk -> LDS by buffer DMA: instruction i of wave w fills token rows
+     * 16i + 4w + 0..3; lane l lands on slot l%16 of row 16i + 4w + l/16 and
+     * fetches the chunk's 16-byte piece (l%16) ^ (row & 15). Rows >= N lie
+     * past the buffer's range and read as zeros. */
+    const uint32_t xbytes = (uint32_t)N * ldx * 2;
+    uint32_t xoff[NB];
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        const int r = 16 * i + 4 * wave + (lane >> 4);
+        xoff[i] = (uint32_t)r * ldx * 2 + (uint32_t)(((lane & 15) ^ (r & 15)) * 16);
+    }
+    auto load_x = [&](int c) {
+        unsigned char *st = xs + (c % SG_NS) * XSTAGE;
+        const int kbyte = (kb + SG_KC * min(c, nch - 1)) * 2;
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+            sg_dma16(X, xbytes, st + (16 * i + 4 * wave) * 256, xoff[i], kbyte);
+    };
+
+    floatx4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
+        acc[nb] = floatx4{};
+    auto compute = [&](int c, const bf16x8 (&wf)[4]) {
+        const uint32_t st = (c % SG_NS) * XSTAGE + c16 * 256;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                const uint32_t slot = (uint32_t)(((8 * j + 2 * q + hf) ^ c16) << 4);
+                bf16x8 b[NB];
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+                    b[nb] = sg_lds16(xs, st + nb * 16 * 256 + slot);
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[2 * j + hf], b[nb],
+                                                                      acc[nb], 0, 0, 0);
+            }
+    };
+
+    /* Each step c: wait for chunk c's X (its DMA was issued 3 steps ago;
+     * after it came W of c and the X and W of c+1, c+2: 4 + 2 (NB + 4) vector
+     * memory operations), barrier, refill the stage chunk c-1 used with
+     * chunk c+3, load W of c+3, compute c. W lives in the register ring
+     * w0..w3 (slot c % 4). Whole rounds of 4 steps, no early exit: past the
+     * end the loads repeat the last chunk and only the MFMAs are skipped. */
+    bf16x8 w0[4], w1[4], w2[4], w3[4];
+    load_x(0);
+    load_w(0, w0);
+    load_x(1);
+    load_w(1, w1);
+    load_x(2);
+    load_w(2, w2);
+    auto step = [&](int c, const bf16x8 (&wcur)[4], bf16x8 (&wfill)[4]) {
+        sg_wait_vm(4 + 2 * (NB + 4));
+        lds_barrier();
+        load_x(c + 3);
+        load_w(c + 3, wfill);
+        __builtin_amdgcn_sched_barrier(0); /* keep the prefetches here */
+        if (c < nch)
+            compute(c, wcur);
+    };
+    for (int c = 0; c < nch; c += 4) {
+        step(c, w0, w3);
+        step(c + 1, w1, w0);
+        step(c + 2, w2, w1);
+        step(c + 3, w3, w2);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* no DMA into LDS outlives the kernel */
+
+    /* acc[nb]: token 16 nb + c16, rows wr0 + 4q .. +3 */
+    if constexpr (GATED) {
+        /* up waves (2, 3) hand their accumulators to the gate waves (0, 1) */
+        lds_barrier();
+        floatx4 *xch = (floatx4 *)xs; /* [2][NB][64] */
+        if (wave >= 2) {
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+                xch[((wave - 2) * NB + nb) * 64 + lane] = acc[nb];
+        }
+        lds_barrier();
+        if (wave < 2) {
+            const int m = blockIdx.x * 32 + 16 * wave + 4 * q;
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                const int n = 16 * nb + c16;
+                const floatx4 u = xch[(wave * NB + nb) * 64 + lane];
+                bf16x4 a;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    a[e] = f2bf(silu_f(bf2f(f2bf(acc[nb][e]))) * bf2f(f2bf(u[e])));
+                if (n < N)
+                    *(bf16x4 *)(Y + (size_t)n * ldy + m) = a;
+            }
+        }
+        return;
+    }
+    const int m = wr0 + 4 * q;
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        const int n = 16 * nb + c16;
+        if (n >= N)
+            continue;
+        if constexpr (PART) {
+            *(floatx4 *)(P + ((size_t)split * N + n) * M + m) = acc[nb];
+        } else {
+            *(bf16x4 *)(Y + (size_t)n * ldy + m) =
+                bf16x4{f2bf(acc[nb][0]), f2bf(acc[nb][1]), f2bf(acc[nb][2]), f2bf(acc[nb][3])};
+        }
+    }
+}
+
+template <bool GATED, bool PART>
+hipError_t launch_nb(int NB, dim3 grid, hipStream_t s, const bf16 *X, int ldx, const bf16 *W,
+                     int N, int K, int KS, bf16 *Y, int ldy, float *P, int M) {
+#define CUJEV_SG_CASE(nb)                                                                    \
+    case nb:                                                                                 \
+        hipLaunchKernelGGL((gemm_small_kernel<nb, GATED, PART>), grid, dim3(256), 0, s, X, ldx, \
+                           W, N, K, KS, Y, ldy, P, M);                                        \
+        break;
+    switch (NB) {
+        CUJEV_SG_CASE(1)
+        CUJEV_SG_CASE(2)
+        CUJEV_SG_CASE(3)
+        CUJEV_SG_CASE(4)
+        CUJEV_SG_CASE(5)
+        CUJEV_SG_CASE(6)
+    default:
+        return hipErrorInvalidValue;
+    }
+#undef CUJEV_SG_CASE
+    return hipGetLastError();
+}
+
+} // namespace
+} // namespace CUJEV_KNS
+using namespace CUJEV_KNS;
+
+extern "C" int cujev_gemm_small_splits(int M, int K) {
+    if (M <= 0 || K <= 0 || M % SG_BM || K % SG_KC)
+        return 0;
+    const int rowblocks = M / SG_BM, chunks = K / SG_KC;
+    int s = (256 + rowblocks / 2) / rowblocks;
+    s = s < 1 ? 1 : s > chunks ? chunks : s;
+    s = s > CUJEV_GEMM_SMALL_MAX_SPLITS ? CUJEV_GEMM_SMALL_MAX_SPLITS : s;
+    while (chunks % s)
+        s--;
+    return s;
+}
+
+extern "C" hipError_t k_gemm_small(const bf16_t *X, int ldx, const bf16_t *W, int N, int M, int K,
+                                   int gated, int splits, bf16_t *Y, int ldy, float *P,
+                                   hipStream_t stream) {
+    if (N <= 0)
+        return hipSuccess;
+    if (N > CUJEV_GEMM_SMALL_MAX_N || M % SG_BM || K % SG_KC || splits < 1 ||
+        (K / SG_KC) % splits || (splits > 1 && (!P || gated)) || (splits == 1 && !Y))
+        return hipErrorInvalidValue;
+    const int NB = (N + 15) / 16, KS = K / splits;
+    const dim3 grid((unsigned)(M / SG_BM), (unsigned)splits);
+    const bf16 *x = (const bf16 *)X, *w = (const bf16 *)W;
+    if (splits > 1)
+        return launch_nb<false, true>(NB, grid, stream, x, ldx, w, N, K, KS, nullptr, 0, P, M);
+    if (gated)
+        return launch_nb<true, false>(NB, grid, stream, x, ldx, w, N, K, KS, (bf16 *)Y, ldy,
+                                      nullptr, M);
+    return launch_nb<false, false>(NB, grid, stream, x, ldx, w, N, K, KS, (bf16 *)Y, ldy, nullptr,
+                                   M);
+}

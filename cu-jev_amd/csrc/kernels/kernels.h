@@ -154,12 +154,16 @@ hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const f
 hipError_t k_embed(const int32_t *tokens, const bf16_t *E, float *x, int N, int H, hipStream_t s);
 
 /* Fused residual add + RMSNorm (REF elementwise.cu:13-40). Output row r reads
- * source row src = rows ? rows[r] : r (R rows, else N):
- *   v = x[src] + (y ? y[src] : 0);  x[src] = v when y && !rows;
+ * source row src = rows ? rows[r] : r (R rows, else N). The added term is
+ *   d = y[src]                                  (y != NULL, bf16), or
+ *   d = bf16(sum_{s < splits} yp[s][src])        (yp != NULL: fp32 split-K
+ *       partials [splits][N][H] of k_gemm_small, splits <= 8, summed in split order);
+ *   v = x[src] + d;  x[src] = v when there is a d and !rows;
  *   out[r] = bf16(v * rsqrt(mean v^2 + eps) * w)   (w holds 1 + weight).
- * H must be a multiple of 4 and at most 16384. */
-hipError_t k_add_rmsnorm(float *x, const bf16_t *y, const float *w, bf16_t *out, int N, int H,
-                         float eps, const int32_t *rows, int R, hipStream_t s);
+ * H must be a multiple of 4 and at most 4096. */
+hipError_t k_add_rmsnorm(float *x, const bf16_t *y, const float *yp, int splits, const float *w,
+                         bf16_t *out, int N, int H, float eps, const int32_t *rows, int R,
+                         hipStream_t s);
 
 /* act[N,I] = bf16(silu(gu[:, :I]) * gu[:, I:])  (REF elementwise.cu:42-54). */
 hipError_t k_silu_mul(const bf16_t *gu, bf16_t *act, int N, int I, hipStream_t s);
@@ -168,6 +172,19 @@ hipError_t k_silu_mul(const bf16_t *gu, bf16_t *act, int N, int I, hipStream_t s
  * (REF elementwise.cu:78-97). h bf16 [B,H], fp32 accumulation. */
 hipError_t k_readout(const bf16_t *h, const bf16_t *E, const int32_t *cand, const int32_t *ncand,
                      int cand_ld, float *logits, int ld, int B, int H, hipStream_t s);
+
+/* ---- weight-streaming GEMM for few tokens (gemm_small.hip) ---------------
+ * Y[N, M] = X[N, K] . W[M, K]^T for N <= CUJEV_GEMM_SMALL_MAX_N, M % 64 == 0,
+ * K % 128 == 0, X rows of stride ldx. splits == 1 writes bf16 Y (row stride
+ * ldy); splits > 1 (K / 128 divisible by splits) writes fp32 partial sums
+ * P[splits][N][M] instead, to be summed by the consumer in split order.
+ * gated (splits == 1): W is the fused [gate I | up I] (M = 2I) and Y gets
+ * act[N][I] = bf16(silu(bf16 gate) * bf16 up). */
+#define CUJEV_GEMM_SMALL_MAX_N 96 /* 6 token blocks of 16: register budget without spills */
+#define CUJEV_GEMM_SMALL_MAX_SPLITS 8
+int cujev_gemm_small_splits(int M, int K); /* suggested split count (<= MAX_SPLITS), 0 = shape unsupported */
+hipError_t k_gemm_small(const bf16_t *X, int ldx, const bf16_t *W, int N, int M, int K, int gated,
+                        int splits, bf16_t *Y, int ldy, float *P, hipStream_t stream);
 
 /* ---- projection GEMMs (hipBLASLt) ------------------------------------------
  * Y[N,M] = X[N,K] . W[M,K]^T, bf16 in, fp32 accumulate, bf16 (f32out = 0) or

@@ -70,6 +70,29 @@ EXPORT int cujev_op_gemm_tune(const void *X, const void *W, void *Y, int f32out,
     return 0;
 }
 
+EXPORT int cujev_ops_gemm_small_splits(int M, int K) { return cujev_gemm_small_splits(M, K); }
+
+EXPORT int cujev_op_gemm_small(const void *X, int ldx, const void *W, int N, int M, int K,
+                               int gated, int splits, void *Y, int ldy, float *P, void *stream) {
+    if (N < 0 || N > CUJEV_GEMM_SMALL_MAX_N || M <= 0 || K <= 0 || !X || !W ||
+        splits > CUJEV_GEMM_SMALL_MAX_SPLITS || ldx < K ||
+        (splits == 1 && ldy < (gated ? M / 2 : M)))
+        return fail(1, "gemm_small: bad arguments");
+    return launched(k_gemm_small((const bf16_t *)X, ldx, (const bf16_t *)W, N, M, K, gated, splits,
+                                 (bf16_t *)Y, ldy, P, (hipStream_t)stream),
+                    "gemm_small");
+}
+
+EXPORT int cujev_op_add_rmsnorm(float *x, const void *y, const float *yp, int splits,
+                                const float *w, void *out, int N, int H, float eps,
+                                const int32_t *rows, int R, void *stream) {
+    if (N < 0 || H <= 0 || !x || !w || !out || (rows && R < 0))
+        return fail(1, "add_rmsnorm: bad arguments");
+    return launched(k_add_rmsnorm(x, (const bf16_t *)y, yp, splits, w, (bf16_t *)out, N, H, eps,
+                                  rows, R, (hipStream_t)stream),
+                    "add_rmsnorm");
+}
+
 EXPORT int cujev_ops_blaslt_version(void) {
     cujev_gemm *g = nullptr;
     if (cujev_gemm_create(&g, nullptr, 0) != 0)

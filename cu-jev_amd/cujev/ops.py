@@ -34,6 +34,8 @@ _SIGS = {
     "cujev_op_attention": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P],
     "cujev_op_gdn_conv_prep": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P,
                                _P, _P],
+    "cujev_op_gemm_small": [_P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _P],
+    "cujev_op_add_rmsnorm": [_P, _P, _P, _I, _P, _P, _I, _I, _F, _P, _I, _P],
     "cujev_op_gdn_scan": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _F, _I,
                           _I, _I, _P, _P, _P],
 }
@@ -57,6 +59,8 @@ def load():
     lib.cujev_ops_last_error.restype = C.c_char_p
     lib.cujev_ops_gdn_scratch_bytes.argtypes = [_I, _I, _I]
     lib.cujev_ops_gdn_scratch_bytes.restype = C.c_size_t
+    lib.cujev_ops_gemm_small_splits.argtypes = [_I, _I]
+    lib.cujev_ops_gemm_small_splits.restype = _I
     lib.cujev_ops_blaslt_version.argtypes = []
     lib.cujev_ops_blaslt_version.restype = _I
     lib.cujev_op_gemm_tune.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, _I, _I, _I, _I,
@@ -73,6 +77,7 @@ def load():
 
 def exported_symbols():
     return ["cujev_ops_kv_stride", "cujev_ops_last_error", "cujev_ops_gdn_scratch_bytes",
+            "cujev_ops_gemm_small_splits",
             "cujev_ops_blaslt_version", "cujev_op_gemm_tune", *_SIGS]
 
 
@@ -174,6 +179,28 @@ def gemm(X, W, Y, f32out=False):
     M = W.shape[0]
     _call("cujev_op_gemm", _ptr(X), _ptr(W), _ptr(Y), int(bool(f32out)), N, M, K, _ptr(_gemm_ws),
           _gemm_ws.numel(), _stream())
+
+
+def gemm_small_splits(M, K) -> int:
+    return int(load().cujev_ops_gemm_small_splits(int(M), int(K)))
+
+
+def gemm_small(X, W, Y=None, P=None, splits=1, gated=False, N=None, K=None):
+    """Few-token GEMM: Y[N,M] = X[N,K] . W[M,K]^T (splits == 1, bf16 Y; gated:
+    Y = act[N, M/2]) or fp32 partials P[splits][N][M] (splits > 1)."""
+    N = X.shape[0] if N is None else N
+    K = W.shape[1] if K is None else K
+    M = W.shape[0]
+    _call("cujev_op_gemm_small", _ptr(X), X.stride(0), _ptr(W), int(N), int(M), int(K),
+          int(bool(gated)), int(splits), _ptr(Y), Y.stride(0) if Y is not None else 0, _ptr(P),
+          _stream())
+
+
+def add_rmsnorm(x, w, out, eps, y=None, yp=None, splits=0, rows=None):
+    N, H = x.shape
+    R = rows.shape[0] if rows is not None else 0
+    _call("cujev_op_add_rmsnorm", _ptr(x), _ptr(y), _ptr(yp), int(splits), _ptr(w), _ptr(out),
+          N, H, float(eps), _ptr(rows), R, _stream())
 
 
 def blaslt_version() -> int:

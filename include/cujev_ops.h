@@ -49,6 +49,30 @@ int cujev_op_gemm(const void *X, const void *W, void *Y, int f32out, int N, int 
 int cujev_op_gemm_tune(const void *X, const void *W, void *Y, int f32out, int N, int M, int K,
                        void *workspace, size_t ws_bytes, void *stream, int *best_index,
                        float *best_us, float *heuristic_us);
+/* Replaces reference src/kernels/kernels.h:50-53 (k_gemm_bf16) for few
+ * tokens, the eval-time shape: Y[N,M] = X[N,K] . W[M,K]^T with N <= 96,
+ * M % 64 == 0, K % 128 == 0, X rows of stride ldx, bf16 in, fp32
+ * accumulation, weights streamed once by a hand-written kernel.
+ *   splits == 1: bf16 Y, row stride ldy.
+ *   splits > 1 (K/128 divisible by splits, at most 8): fp32 partial sums
+ *     P[splits][N][M] (no Y); sum them in split order (cujev_op_add_rmsnorm).
+ *   gated (splits == 1): W is the fused [gate I | up I] weight (M = 2I) and
+ *     Y receives act[N][I] = bf16(silu(bf16 gate) * bf16 up), which is the
+ *     reference's GEMM + silu_mul pair (src/kernels/elementwise.cu:42-54). */
+int cujev_op_gemm_small(const void *X, int ldx, const void *W, int N, int M, int K, int gated,
+                        int splits, void *Y, int ldy, float *P, void *stream);
+/* Split count the engine uses for an (M, K) few-token GEMM; 0 = unsupported shape. */
+int cujev_ops_gemm_small_splits(int M, int K);
+
+/* Replaces reference src/kernels/kernels.h:40-43 (k_rmsnorm, k_add) fused:
+ * row r reads source row src = rows ? rows[r] : r (R rows, else N);
+ * v = x[src] + (y ? y[src] : yp ? bf16(sum_s yp[s][src]) : 0), written back
+ * to x when something was added and rows == NULL; out[r] = bf16(v *
+ * rsqrt(mean v^2 + eps) * w). y is bf16 [N][H]; yp is fp32 [splits][N][H]. */
+int cujev_op_add_rmsnorm(float *x, const void *y, const float *yp, int splits, const float *w,
+                         void *out, int N, int H, float eps, const int32_t *rows, int R,
+                         void *stream);
+
 /* hipBLASLt library version (solution indices are only valid for it). */
 int cujev_ops_blaslt_version(void);
 

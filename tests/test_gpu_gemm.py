@@ -1,0 +1,121 @@
+"""GPU parity of the few-token weight-streaming GEMM (cujev_op_gemm_small) and
+of the residual add + RMSNorm that consumes its split-K partials, through the
+operator C ABI, against float32 references of the same bf16 inputs.
+
+The GEMM replaces the reference's cuBLAS call (src/kernels/elementwise.cu:56-75)
+at eval shapes; the gated form replaces GEMM + silu_mul (:42-54). Tolerance:
+the only rounding besides fp32 accumulation order is the bf16 output, so
+max |gpu - ref| / max |ref| <= 1e-2.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def ops():
+    from cujev import ops as o
+    o.load()
+    return o
+
+
+def rel(a, b):
+    a = a.double().cpu()
+    b = b.double().cpu()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+def rand_bf16(*shape, seed, scale=1.0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return (torch.randn(*shape, device="cuda", generator=g) * scale).to(torch.bfloat16)
+
+
+# (N, M, K): eval shapes of the 4B model (qkv, in_proj) and edge token counts
+@pytest.mark.parametrize("N,M,K", [(80, 10240, 2560), (80, 12352, 2560), (1, 2560, 2560),
+                                   (17, 640, 384), (96, 256, 1024), (33, 4160, 2560)])
+def test_gemm_small_matches_fp32(N, M, K):
+    o = ops()
+    print(f"gemm_small N={N} M={M} K={K}", flush=True)
+    X = rand_bf16(N, K, seed=1)
+    W = rand_bf16(M, K, seed=2, scale=0.02)
+    Y = torch.empty(N, M, dtype=torch.bfloat16, device="cuda")
+    o.gemm_small(X, W, Y=Y)
+    torch.cuda.synchronize()
+    ref = X.float() @ W.float().t()
+    e = rel(Y.float(), ref)
+    print(f"rel err {e:.3e}")
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("N,I,H", [(80, 9216, 2560), (5, 128, 256), (96, 512, 640)])
+def test_gemm_small_gated_is_silu_mul(N, I, H):
+    o = ops()
+    print(f"gated N={N} I={I} H={H}", flush=True)
+    X = rand_bf16(N, H, seed=3)
+    W = rand_bf16(2 * I, H, seed=4, scale=0.05)
+    act = torch.empty(N, I, dtype=torch.bfloat16, device="cuda")
+    o.gemm_small(X, W, Y=act, gated=True)
+    torch.cuda.synchronize()
+    gu = (X.float() @ W.float().t()).to(torch.bfloat16).float()  # the GEMM's bf16 output
+    ref = torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]
+    e = rel(act.float(), ref)
+    print(f"rel err {e:.3e}")
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("N,H,K", [(80, 2560, 9216), (80, 2560, 4096), (7, 2560, 2560),
+                                   (96, 1024, 1024)])
+def test_split_partials_feed_add_rmsnorm(N, H, K):
+    """splits > 1: fp32 partials summed in split order by add_rmsnorm equal the
+    bf16-output path (GEMM into y, then the add) up to the bf16 rounding of y."""
+    o = ops()
+    sp = o.gemm_small_splits(H, K)
+    print(f"split N={N} H={H} K={K} splits={sp}", flush=True)
+    assert sp >= 1
+    X = rand_bf16(N, K, seed=5)
+    W = rand_bf16(H, K, seed=6, scale=0.02)
+    w = (1.0 + 0.1 * torch.randn(H, device="cuda")).float()
+    g = torch.Generator(device="cuda").manual_seed(7)
+    x0 = torch.randn(N, H, device="cuda", generator=g)
+    P = torch.empty(max(sp, 1), N, H, dtype=torch.float32, device="cuda")
+    out = torch.empty(N, H, dtype=torch.bfloat16, device="cuda")
+    x = x0.clone()
+    if sp > 1:
+        o.gemm_small(X, W, P=P, splits=sp)
+        o.add_rmsnorm(x, w, out, 1e-6, yp=P, splits=sp)
+    else:
+        y = torch.empty(N, H, dtype=torch.bfloat16, device="cuda")
+        o.gemm_small(X, W, Y=y)
+        o.add_rmsnorm(x, w, out, 1e-6, y=y)
+    torch.cuda.synchronize()
+    y_ref = (X.float() @ W.float().t()).to(torch.bfloat16).float()
+    v = x0 + y_ref
+    ref = v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + 1e-6) * w
+    assert rel(x, v) <= TOL          # residual written back
+    e = rel(out.float(), ref)
+    print(f"rel err {e:.3e}")
+    assert e <= TOL
+    if sp > 1:  # deterministic: a second run is bit-identical
+        x2, out2 = x0.clone(), torch.empty_like(out)
+        o.gemm_small(X, W, P=P, splits=sp)
+        o.add_rmsnorm(x2, w, out2, 1e-6, yp=P, splits=sp)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out2) and torch.equal(x, x2)
+
+
+def test_gemm_small_rejects_unsupported_shapes():
+    o = ops()
+    X = rand_bf16(8, 100, seed=8)
+    W = rand_bf16(64, 100, seed=9)
+    Y = torch.empty(8, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(o.OpsError):
+        o.gemm_small(X, W, Y=Y)           # K not a multiple of 128
+    X = rand_bf16(97, 128, seed=8)
+    W = rand_bf16(64, 128, seed=9)
+    Y = torch.empty(97, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(o.OpsError):
+        o.gemm_small(X, W, Y=Y)           # more than 96 tokens
+    assert o.gemm_small_splits(100, 256) == 0
