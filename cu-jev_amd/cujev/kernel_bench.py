@@ -22,8 +22,8 @@ import sys
 COPY_SCALE = {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0}
 MEASURED_KIB = {
     "attention": {"FETCH_SIZE": 115282.3, "WRITE_SIZE": 32872.3},
-    "gdn": {"FETCH_SIZE": 17640.4 + 36.5 + 16995.0 + 37040.1 + 24594.2,
-            "WRITE_SIZE": 33280.1 + 96.0 + 73734.8 + 34816.0 + 16384.0},
+    "gdn": {"FETCH_SIZE": 17519.0 + 36.5 + 16937.6 + 37053.2 + 16398.7,
+            "WRITE_SIZE": 33296.6 + 96.0 + 73984.0 + 18432.0 + 16384.0},
 }
 
 
