@@ -27,9 +27,10 @@
  *    double buffers: while a wave runs the softmax of tile i interleaved with
  *    the S^T MFMAs of tile i+1 and then the PV MFMAs of tile i, the V^T of
  *    tile i+1 and the K of tile i+2 are in flight. One barrier per tile.
- *  - S accumulators start at -m (the running max), so scores arrive shifted;
- *    m only moves when a tile's max exceeds it by more than 2^8, which after
- *    the first tiles is rare, and then the O/l rescale runs.
+ *  - The softmax shift mu stays 0 while the running max is within 2^+-64
+ *    of it, so S accumulators start at the MFMA's inline zero and scores need
+ *    no per-tile shift; only rows whose scores leave that range pay for a
+ *    subtraction (and, when mu moves, the O/l rescale).
  *  - blockIdx -> (kv-head, token tile) is XCD-aware: the 8 XCDs (own L2 each)
  *    are split among the kv-heads so the WGs sharing an L2 stream the same
  *    K/V. Tiles run last-to-first so the longest causal rows start first. */
@@ -49,13 +50,12 @@ constexpr int V_BYTES = D * BK * 2; /* 32 KiB: V^T tile [256][64]  */
 /* LDS: V^T buffers first, K buffers after, so every ds_read offset of a
  * buffer fits the 16-bit immediate from one per-lane base register. */
 constexpr int V_OFF = 0, K_OFF = 2 * V_BYTES, LDS_BYTES = 2 * V_BYTES + 2 * K_BYTES;
-/* Lazy rescale: the running max only moves when a tile's max exceeds it by
- * more than 2^TAU, so p <= 2^TAU; the softmax is exact for any reference m
- * (it cancels in o / l) and p keeps its bf16 rounding. */
-#ifndef CUJEV_ATTN_TAU
-#define CUJEV_ATTN_TAU 8.f
-#endif
-constexpr float TAU = CUJEV_ATTN_TAU;
+/* Shift of the base-2 softmax: p = 2^(s - mu) for any reference mu is exact
+ * (mu cancels in o / l, and bf16/fp32 rounding of p commute with powers of
+ * two), so mu only has to keep p in range. It stays 0 while the running max m
+ * is within +-SHIFT_RANGE of it (p <= 2^64, the largest p >= 2^-64) and moves
+ * to m when m leaves that window, rescaling o and l. */
+constexpr float SHIFT_RANGE = 64.f;
 
 /* 16-byte chunk swizzles: the 16 lanes of one ds_read_b128 phase hit 16
  * distinct 16-byte bank groups (and any 8 consecutive lanes 8 distinct ones). */
@@ -92,25 +92,48 @@ DEV __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
 
+DEV void issue_k1(const TileSrc &s, unsigned char *kbuf, const uint32_t (&koff)[2], int wave, int j) {
+    const int r0 = 8 * j + 2 * wave;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.k, (lds_ptr)(kbuf + r0 * 512), 16, koff[j & 1],
+                                             (s.kbase + r0) * 512, 0, 0);
+}
+
+DEV void issue_v1(const TileSrc &s, unsigned char *vbuf, int wave, int j) {
+    const int d0 = 8 * (4 * j + wave);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.vt, (lds_ptr)(vbuf + d0 * 128), 16, s.voff,
+                                             d0 * s.vrow_bytes + s.kbase * 2, 0, 0);
+}
+
 DEV void issue_k(const TileSrc &s, unsigned char *kbuf, const uint32_t (&koff)[2], int wave) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int r0 = 8 * j + 2 * wave;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(s.k, (lds_ptr)(kbuf + r0 * 512), 16, koff[j & 1],
-                                                 (s.kbase + r0) * 512, 0, 0);
-    }
+    for (int j = 0; j < 8; j++)
+        issue_k1(s, kbuf, koff, wave, j);
 }
 
 DEV void issue_v(const TileSrc &s, unsigned char *vbuf, int wave) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int d0 = 8 * (4 * j + wave);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(s.vt, (lds_ptr)(vbuf + d0 * 128), 16, s.voff,
-                                                 d0 * s.vrow_bytes + s.kbase * 2, 0, 0);
-    }
+    for (int j = 0; j < 8; j++)
+        issue_v1(s, vbuf, wave, j);
 }
 
 DEV void wait_tile_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+/* s_waitcnt on the LDS count alone (gfx9 encoding: lgkmcnt in bits 11:8,
+ * vmcnt and expcnt at their maxima): one wait covers the operands of two
+ * MFMAs, so the compiler adds none of its own before the second. */
+#define WAIT_LGKM_(n) __builtin_amdgcn_s_waitcnt(0xC07F | ((n) << 8))
+DEV void wait_lgkm(int n) { /* n is a constant once the loops are unrolled */
+    switch (n) {
+    case 0: WAIT_LGKM_(0); break;
+    case 1: WAIT_LGKM_(1); break;
+    case 2: WAIT_LGKM_(2); break;
+    case 3: WAIT_LGKM_(3); break;
+    case 4: WAIT_LGKM_(4); break;
+    case 5: WAIT_LGKM_(5); break;
+    case 6: WAIT_LGKM_(6); break;
+    default: WAIT_LGKM_(0); break;
+    }
+}
 
 /* One workgroup = 4 waves = the 4 q-heads of kv-head kh x 32 packed tokens.
  * Per key tile i the loop overlaps, in each wave, the S^T MFMAs of tile i+1
@@ -206,9 +229,7 @@ __global__ __launch_bounds__(256) void attention_kernel(
 #pragma unroll
     for (int i = 0; i < 8; i++)
         o[i] = floatx16{};
-    /* m_run: running max (log2 units); S accumulators start at -mu, mu being
-     * the running max when the tile's S^T began (0 before any key), so the
-     * scores reach the softmax already shifted. sbase_* tracks that shift. */
+    /* m_run: running max of the scores (log2 units); mu_run: the shift */
     float m_run = -INFINITY, l_run = 0.f, mu_run = 0.f;
 
     constexpr int QD = 3; /* S^T A-operand reads in flight, in k-steps */
@@ -224,7 +245,6 @@ __global__ __launch_bounds__(256) void attention_kernel(
     wait_tile_loads();
     __syncthreads();
     floatx16 sa0 = floatx16{}, sa1 = floatx16{}, sb0, sb1;
-    float sbase_a = 0.f, sbase_b = 0.f;
 #pragma unroll
     for (int ks = 0; ks < 16; ks++) {
         sa0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_read16(lds, kaddr(ks, 0)), qf[ks], sa0, 0, 0, 0);
@@ -233,18 +253,27 @@ __global__ __launch_bounds__(256) void attention_kernel(
     }
     __syncthreads(); /* K buffer 0 is refilled in the first step */
 
-    /* One key tile i with scores S = (s0, s1) shifted by sbase. With a next
-     * tile, its S^T MFMAs run in the same straight-line block as this tile's
+    /* One key tile i with unshifted scores S = (s0, s1). With a next tile,
+     * its S^T MFMAs run in the same straight-line block as this tile's
      * softmax: per k-step two MFMAs, the LDS reads QD k-steps ahead and a
      * slice of the softmax VALU work, pinned in that order by scheduling
      * barriers. The PV MFMAs of tile i follow with their reads VD ahead. */
-    auto step = [&](auto has_next, int i, floatx16 &s0, floatx16 &s1, float &sbase, floatx16 &n0_,
-                    floatx16 &n1_, float &nbase, int kbuf_next, int vbuf) {
+    auto step = [&](auto has_next, int i, floatx16 &s0, floatx16 &s1, floatx16 &n0_, floatx16 &n1_,
+                    int kbuf_next, int vbuf) {
         constexpr bool NEXT = decltype(has_next)::value;
-        if (NEXT)
-            issue_v(src_of(i + 1), smem + V_OFF + (vbuf ^ 1) * V_BYTES, wave);
-        if (i + 2 < ntl)
-            issue_k(src_of(i + 2), smem + K_OFF + (kbuf_next ^ 1) * K_BYTES, koff, wave);
+        /* This step's tile loads go out one per k-step of the S^T loop below,
+         * between its MFMAs: K of tile i+2 (source clamped to the last tile;
+         * past the end the load refills a buffer that is not read again) and
+         * V^T of tile i+1. Both target buffers were last read before the
+         * barrier that ended the previous step. An LDS read issued after a
+         * buffer_load ... lds of the same wave completes only once that load
+         * has landed; in this loop the operand reads run QD k-steps ahead of
+         * their MFMAs, which hides most of that (the PV reads, VD MFMAs
+         * ahead, would not). */
+        const TileSrc sk = src_of(min(i + 2, ntl - 1));
+        const TileSrc sv = src_of(min(i + 1, ntl - 1));
+        unsigned char *const kdst = smem + K_OFF + (kbuf_next ^ 1) * K_BYTES;
+        unsigned char *const vdst = smem + V_OFF + (vbuf ^ 1) * V_BYTES;
 
         /* mask: key of accumulator slot r of block t is 32t + 16(r>>3) + 8h + (r&7) */
         const bool own = i >= nst;
@@ -262,18 +291,36 @@ __global__ __launch_bounds__(256) void attention_kernel(
 
         bf16x8 r0[QD], r1[QD];
         if constexpr (NEXT) {
-            nbase = mu_run;
-#pragma unroll
-            for (int e = 0; e < 16; e++)
-                n0_[e] = n1_[e] = -mu_run;
 #pragma unroll
             for (int ks = 0; ks < QD; ks++) {
                 r0[ks] = lds_read16(lds, kaddr(ks, kbuf_next));
                 r1[ks] = lds_read16(lds, kaddr(ks, kbuf_next) + 16384);
             }
         }
+        /* Softmax of tile i with the exponentials taken for the shift 0 (the
+         * common case): score pairs 0-7 (P blocks 0 and 1) between the S^T
+         * MFMAs of tile i+1, pairs 8-15 (blocks 2 and 3) between the PV MFMAs
+         * of tile i ahead of their use, and the max of the raw scores along
+         * the S^T loop. Whether the scores need a shift is decided after that
+         * loop, when the max is long complete; only then (rarely) are they
+         * shifted in place and pairs 0-7 redone; pairs 8-15 read the shifted
+         * scores anyway. */
         float mx = -INFINITY, lsum = 0.f;
         bf16x8 pf[4];
+        /* The empty asm keeps each pair in its slot: the compiler would
+         * otherwise sink the exponentials towards their first use. */
+        auto pair = [&](int q2) {
+            const int v = 2 * q2;
+            const float x0 = v < 16 ? s0[v] : s1[v - 16];
+            const float x1 = v < 16 ? s0[v + 1] : s1[v - 15];
+            const float p0 = fast_exp2(x0), p1 = fast_exp2(x1);
+            lsum += p0 + p1;
+            bf16x2 pk = {f2bf(p0), f2bf(p1)};
+            asm volatile("" : "+v"(pk), "+v"(lsum));
+            const int blk = (v < 16 ? 0 : 2) + ((v & 15) >> 3), e = v & 7;
+            pf[blk][e] = pk[0];
+            pf[blk][e + 1] = pk[1];
+        };
 #pragma unroll
         for (int ks = 0; ks < 16; ks++) {
             if constexpr (NEXT) {
@@ -282,56 +329,49 @@ __global__ __launch_bounds__(256) void attention_kernel(
                     r0[ks % QD] = lds_read16(lds, kaddr(ks + QD, kbuf_next));
                     r1[ks % QD] = lds_read16(lds, kaddr(ks + QD, kbuf_next) + 16384);
                 }
-                n0_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], n0_, 0, 0, 0);
-                n1_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[ks], n1_, 0, 0, 0);
+                wait_lgkm(2 * ((ks + QD < 16 ? ks + QD : 15) - ks));
+                n0_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], ks == 0 ? floatx16{} : n0_, 0, 0, 0);
+                n1_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[ks], ks == 0 ? floatx16{} : n1_, 0, 0, 0);
+                if (ks < 8)
+                    issue_k1(sk, kdst, koff, wave, ks);
+                else
+                    issue_v1(sv, vdst, wave, ks - 8);
             }
-            if (ks < 4) { /* row max, 8 scores per k-step */
-#pragma unroll
-                for (int r = 4 * ks; r < 4 * ks + 4; r++)
-                    mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-            } else if (ks == 4) {
-                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx),
-                                                                 __float_as_uint(mx), false, false);
-                mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-                const float m_true = mx + sbase;
-                const bool grow = m_true > m_run + TAU;
-                const float m_new = grow ? m_true : m_run;
-                const float mu_new = m_new == -INFINITY ? 0.f : m_new;
-                const float dshift = mu_new - sbase;
-                if (__any(dshift != 0.f)) { /* rare: the max moved, or S predates a move */
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        s0[r] -= dshift;
-                        s1[r] -= dshift;
-                    }
-                    const float alpha = grow ? fast_exp2(m_run - m_new) : 1.f;
-                    if (__any(grow)) {
-                        l_run *= alpha;
-#pragma unroll
-                        for (int dt = 0; dt < 8; dt++)
-                            o[dt] *= alpha;
-                    }
-                }
-                m_run = m_new;
-                mu_run = mu_new;
-                sbase = mu_new;
-            } else { /* exponentials: score pairs (2q, 2q+1), q in [lo, hi) */
-                const int lo = (ks - 5) * 16 / 11, hi = (ks - 4) * 16 / 11;
-#pragma unroll
-                for (int q2 = lo; q2 < hi; q2++) {
-                    const int v = 2 * q2;
-                    const float x0 = v < 16 ? s0[v] : s1[v - 16];
-                    const float x1 = v < 16 ? s0[v + 1] : s1[v - 15];
-                    const float p0 = fast_exp2(x0), p1 = fast_exp2(x1);
-                    lsum += p0 + p1;
-                    const int blk = (v < 16 ? 0 : 2) + ((v & 15) >> 3), e = v & 7;
-                    pf[blk][e] = f2bf(p0);
-                    pf[blk][e + 1] = f2bf(p1);
-                }
-            }
+            mx = fmaxf(mx, fmaxf(s0[ks], s1[ks]));
+            if ((ks & 1) == 0)
+                pair(ks >> 1);
             __builtin_amdgcn_sched_barrier(0);
         }
-        l_run += lsum;
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                             false, false);
+            mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+            const float m_new = fmaxf(m_run, mx);
+            const bool move = m_new != -INFINITY && fabsf(m_new - mu_run) > SHIFT_RANGE;
+            const float mu_new = move ? m_new : mu_run;
+            if (__builtin_expect(__any(move || mu_new != 0.f), 0)) {
+                /* rare: scores out of range of 2^0 */
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    s0[r] -= mu_new;
+                    s1[r] -= mu_new;
+                }
+                lsum = 0.f;
+#pragma unroll
+                for (int q2 = 0; q2 < 8; q2++)
+                    pair(q2);
+                /* a move down only happens before any key counted (l = o = 0) */
+                const float alpha = fast_exp2(fminf(mu_run - mu_new, 0.f));
+                if (__any(move)) {
+                    l_run *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < 8; dt++)
+                        o[dt] *= alpha;
+                }
+            }
+            m_run = m_new;
+            mu_run = mu_new;
+        }
 
         /* O^T += V^T P^T */
         bf16x8 vr[VD];
@@ -343,9 +383,14 @@ __global__ __launch_bounds__(256) void attention_kernel(
             const bf16x8 a = vr[t % VD];
             if (t + VD < 32)
                 vr[t % VD] = lds_read16(lds, vaddr(t + VD, vbuf));
+            if ((t & 1) == 0)
+                wait_lgkm((t + VD < 32 ? t + VD : 31) - t - 1);
             o[t & 7] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[t >> 3], o[t & 7], 0, 0, 0);
+            if (t < 16 && (t & 1) == 0)
+                pair(8 + (t >> 1));
             __builtin_amdgcn_sched_barrier(0);
         }
+        l_run += lsum;
         wait_tile_loads();
         __syncthreads();
     };
@@ -356,14 +401,14 @@ __global__ __launch_bounds__(256) void attention_kernel(
     const std::false_type last{};
     int i = 0;
     for (; i + 2 < ntl; i += 2) {
-        step(more, i, sa0, sa1, sbase_a, sb0, sb1, sbase_b, 1, 0);
-        step(more, i + 1, sb0, sb1, sbase_b, sa0, sa1, sbase_a, 0, 1);
+        step(more, i, sa0, sa1, sb0, sb1, 1, 0);
+        step(more, i + 1, sb0, sb1, sa0, sa1, 0, 1);
     }
     if (ntl - i == 2) {
-        step(more, i, sa0, sa1, sbase_a, sb0, sb1, sbase_b, 1, 0);
-        step(last, i + 1, sb0, sb1, sbase_b, sa0, sa1, sbase_a, 0, 1);
+        step(more, i, sa0, sa1, sb0, sb1, 1, 0);
+        step(last, i + 1, sb0, sb1, sa0, sa1, 0, 1);
     } else {
-        step(last, i, sa0, sa1, sbase_a, sb0, sb1, sbase_b, 1, 0);
+        step(last, i, sa0, sa1, sb0, sb1, 1, 0);
     }
 
     /* ---- epilogue: normalise, gate, store ---- */
