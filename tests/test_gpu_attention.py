@@ -126,6 +126,54 @@ def test_attention_branch_isolation():
     assert rel_err(alone, both[sl]) <= 1e-2
 
 
+@pytest.mark.parametrize("seed,q_scale", [(31, 40.0), (32, 120.0)])
+def test_attention_scores_beyond_shift_range(seed, q_scale):
+    """Scores of tens to hundreds in log2 units, growing along the keys: the
+    kernel's softmax shift (0 while the running max stays within 2^+-64)
+    moves several times, each move rescaling o and l, and the exponentials
+    taken for shift 0 overflow and are redone."""
+    o = ops()
+    Hq, Hkv, P = 8, 2, 300
+    q, gate, ks, vs, ko, vo, ob = make_case(seed, Hq, Hkv, P, [3, 40, 21])
+    q = orc.bf16_round(q * (q_scale / 0.6))
+    ks = orc.bf16_round(ks * (1.0 + np.arange(P, dtype=np.float32) / 40.0)[:, None, None])
+    got, qd = run_attention(o, q, gate, ks, vs, ko, vo, ob, Hq, Hkv)
+    smax = float(np.abs(np.einsum("nhd,phd->nhp", qd[:, ::Hq // Hkv], ks)).max())
+    print(f"case seed={seed} q_scale={q_scale}: max |score| {smax:.0f} (log2 units)", flush=True)
+    assert smax > 4 * 64
+    ref = oracle_attention(qd, gate, ks, vs, ko, vo, ob)
+    err = rel_err(got, ref)
+    print(f"rel err {err:.3e}")
+    assert err <= TOL
+
+
+def test_attention_scores_far_below_zero():
+    """Every score near -230 in log2 units: the shift moves down to the first
+    tile's max before any key is counted, and every later tile is shifted."""
+    o = ops()
+    rng = np.random.default_rng(41)
+    Hq, Hkv, P, segs = 8, 2, 200, [9, 30]
+    N = sum(segs)
+    u = rng.standard_normal((Hkv, D)).astype(np.float32)
+    ks = orc.bf16_round(u[None] + 0.05 * rng.standard_normal((P, Hkv, D)).astype(np.float32))
+    ko = orc.bf16_round(u[None] + 0.05 * rng.standard_normal((N, Hkv, D)).astype(np.float32))
+    vs = orc.bf16_round(rng.standard_normal((P, Hkv, D)).astype(np.float32))
+    vo = orc.bf16_round(rng.standard_normal((N, Hkv, D)).astype(np.float32))
+    gate = orc.bf16_round(rng.standard_normal((N, Hq, D)).astype(np.float32))
+    heads = np.arange(Hq) // (Hq // Hkv)
+    q = orc.bf16_round(-10.0 * u[heads][None] +
+                       0.05 * rng.standard_normal((N, Hq, D)).astype(np.float32))
+    ob = np.concatenate([np.full(L, s, np.int32) for s, L in zip(np.cumsum([0] + segs[:-1]), segs)])
+    got, qd = run_attention(o, q, gate, ks, vs, ko, vo, ob, Hq, Hkv)
+    smax = float(np.einsum("nhd,phd->nhp", qd[:, ::Hq // Hkv], ks).max())
+    print(f"largest score {smax:.0f} (log2 units)", flush=True)
+    assert smax < -2 * 64
+    ref = oracle_attention(qd, gate, ks, vs, ko, vo, ob)
+    err = rel_err(got, ref)
+    print(f"rel err {err:.3e}")
+    assert err <= TOL
+
+
 def test_attn_prep_matches_oracle():
     o = ops()
     rng = np.random.default_rng(21)
