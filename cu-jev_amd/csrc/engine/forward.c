@@ -49,11 +49,11 @@ typedef struct {
     cujev_chunks chunks;
 } fwd_launch;
 
-/* Projection GEMMs Y[N,M] = X[N,K] W^T. Measured on MI355X at the 4B eval
- * shape (N = 80), the hand-written few-token kernel beats hipBLASLt's tuned
- * choice on the K-heavy, H-wide outputs that feed the residual (o_proj,
- * out_proj, down_proj: split-K, 30-40 % faster) but not on the wide
- * projections (qkv, in_proj, gate_up), which stay on hipBLASLt. */
+/* Projection GEMMs Y[N,M] = X[N,K] W^T. For few tokens (the eval, N <= 96)
+ * the hand-written weight-streaming kernel reads the pre-tiled copy of the
+ * weight (its time is the HBM stream of W); larger N (the prefill) goes to
+ * hipBLASLt on the plain rows. CUJEV_SMALL_GEMM=0 sends everything to
+ * hipBLASLt. */
 static int small_gemm_ok(int N, int M, int K) {
     static int cached = -1;
     if (cached < 0) {
@@ -63,29 +63,32 @@ static int small_gemm_ok(int N, int M, int K) {
     return cached && N <= CUJEV_GEMM_SMALL_MAX_N && cujev_gemm_small_splits(M, K) > 0;
 }
 
-static hipError_t proj_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, bf16_t *Y, int N,
-                            int M, int K) {
+static hipError_t proj_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, const bf16_t *Wt,
+                            bf16_t *Y, int N, int M, int K) {
+    if (Wt && small_gemm_ok(N, M, K))
+        return k_gemm_small(X, K, Wt, N, M, K, 0, 1, Y, M, NULL, m->stream);
     return k_gemm(m->gemm, X, W, Y, 0, N, M, K, m->stream);
 }
 
 /* A projection whose output feeds the residual add (o_proj, out_proj,
  * down_proj: M = H). Returns through *y / *yp / *splits what the following
  * k_add_rmsnorm reads: bf16 rows, or the few-token GEMM's split-K partials. */
-static hipError_t resid_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, int N, int M,
-                             int K, const bf16_t **y, const float **yp, int *splits) {
-    if (small_gemm_ok(N, M, K)) {
+static hipError_t resid_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, const bf16_t *Wt,
+                             int N, int M, int K, const bf16_t **y, const float **yp,
+                             int *splits) {
+    if (Wt && small_gemm_ok(N, M, K)) {
         const int sp = cujev_gemm_small_splits(M, K);
         if (sp > 1) {
             *y = NULL;
             *yp = m->ypart;
             *splits = sp;
-            return k_gemm_small(X, K, W, N, M, K, 0, sp, NULL, 0, m->ypart, m->stream);
+            return k_gemm_small(X, K, Wt, N, M, K, 0, sp, NULL, 0, m->ypart, m->stream);
         }
     }
     *y = m->y;
     *yp = NULL;
     *splits = 0;
-    return proj_gemm(m, X, W, m->y, N, M, K);
+    return proj_gemm(m, X, W, Wt, m->y, N, M, K);
 }
 
 /* The kernels of one forward (and the candidate readout); no host sync. */
@@ -108,7 +111,8 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
         const float *ryp;
         int rsp;
         if (ly->type == CUJEV_LAYER_FULL) {
-            K_TRY(proj_gemm(m, m->xb, ly->w_qkv, m->proj, N, m->w_attn, H), "gemm qkv", l);
+            K_TRY(proj_gemm(m, m->xb, ly->w_qkv, ly->wt_qkv, m->proj, N, m->w_attn, H), "gemm qkv",
+                  l);
             bf16_t *kdst, *vdst;
             int kstride;
             if (mode == CUJEV_FWD_PREFILL) {
@@ -128,10 +132,11 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
                               P, m->state_stride, kdst, vdst, kstride, a->base, N, m->Hq,
                               m->Hkv, m->mix_out, s),
                   "attention", l);
-            K_TRY(resid_gemm(m, m->mix_out, ly->w_o, N, H, m->Hq * m->D, &ry, &ryp, &rsp),
+            K_TRY(resid_gemm(m, m->mix_out, ly->w_o, ly->wt_o, N, H, m->Hq * m->D, &ry, &ryp,
+                             &rsp),
                   "gemm o", l);
         } else {
-            K_TRY(proj_gemm(m, m->xb, ly->w_in, m->proj, N, m->w_gdn, H), "gemm in", l);
+            K_TRY(proj_gemm(m, m->xb, ly->w_in, ly->wt_in, m->proj, N, m->w_gdn, H), "gemm in", l);
             const float *conv_in = mode == CUJEV_FWD_EVAL ? st->conv[l] : NULL;
             float *conv_out = mode == CUJEV_FWD_PREFILL ? st->conv[l] : NULL;
             K_TRY(k_gdn_conv_prep(m->proj, m->w_gdn, ly->conv_w, conv_in, conv_out, N, a->base,
@@ -144,14 +149,21 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
                              m->proj + m->C, m->w_gdn, ly->g_norm, eps, m->Hk, m->Hv, m->mix_out,
                              &gws, N, s),
                   "gdn_scan", l);
-            K_TRY(resid_gemm(m, m->mix_out, ly->w_out, N, H, m->V, &ry, &ryp, &rsp), "gemm out",
-                  l);
+            K_TRY(resid_gemm(m, m->mix_out, ly->w_out, ly->wt_out, N, H, m->V, &ry, &ryp, &rsp),
+                  "gemm out", l);
         }
         K_TRY(k_add_rmsnorm(m->x, ry, ryp, rsp, ly->post_norm, m->xb, N, H, eps, NULL, 0, s),
               "add+norm", l);
-        K_TRY(proj_gemm(m, m->xb, ly->w_gate_up, m->proj, N, 2 * I, H), "gemm gate_up", l);
-        K_TRY(k_silu_mul(m->proj, m->act, N, I, s), "silu_mul", l);
-        K_TRY(resid_gemm(m, m->act, ly->w_down, N, H, I, &ry, &ryp, &rsp), "gemm down", l);
+        if (ly->wt_gate_up && small_gemm_ok(N, 2 * I, H)) { /* GEMM + silu_mul in one */
+            K_TRY(k_gemm_small(m->xb, H, ly->wt_gate_up, N, 2 * I, H, 1, 1, m->act, I, NULL, s),
+                  "gemm gate_up", l);
+        } else {
+            K_TRY(proj_gemm(m, m->xb, ly->w_gate_up, NULL, m->proj, N, 2 * I, H), "gemm gate_up",
+                  l);
+            K_TRY(k_silu_mul(m->proj, m->act, N, I, s), "silu_mul", l);
+        }
+        K_TRY(resid_gemm(m, m->act, ly->w_down, ly->wt_down, N, H, I, &ry, &ryp, &rsp),
+              "gemm down", l);
         if (l + 1 < c->num_layers)
             K_TRY(k_add_rmsnorm(m->x, ry, ryp, rsp, m->layers[l + 1].in_norm, m->xb, N, H, eps,
                                 NULL, 0, s),

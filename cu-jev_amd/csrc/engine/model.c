@@ -139,6 +139,23 @@ static cujev_status upload_fused(loader *L, const st_tensor **parts, int nparts,
 }
 
 /* Small fp32 vector, optionally +add or -exp(x). */
+/* The tiled copy of an uploaded projection that the few-token GEMM streams
+ * (one contiguous 4 KiB block per 16 rows x 128 k), for the shapes it
+ * supports; *out stays NULL otherwise. */
+static cujev_status upload_tiled(loader *L, const bf16_t *w, int M, int K, bf16_t **out) {
+    *out = NULL;
+    if (cujev_gemm_small_splits(M, K) <= 0)
+        return CUJEV_OK;
+    bf16_t *d = (bf16_t *)take(L, (size_t)M * K * 2);
+    if (L->dry)
+        return CUJEV_OK;
+    if (!d)
+        return cujev_fail(CUJEV_ERR_OOM, "weight arena exhausted");
+    HIP_TRY(k_gemm_small_tile(w, M, K, d, L->m->stream));
+    *out = d;
+    return CUJEV_OK;
+}
+
 static cujev_status upload_f32(loader *L, const st_tensor *t, float add, int negexp, size_t expect,
                                float **out) {
     const size_t n = st_numel(t);
@@ -202,8 +219,10 @@ static cujev_status walk(loader *L) {
                 parts[2]->shape[0] != (int64_t)m->Hkv * m->D)
                 return cujev_fail(CUJEV_ERR_FORMAT, "layer %d: attention projection shapes", l);
             CUJEV_TRY(upload_fused(L, parts, 3, H, &ly->w_qkv));
+            CUJEV_TRY(upload_tiled(L, ly->w_qkv, m->w_attn, H, &ly->wt_qkv));
             CUJEV_TRY(want(L, "layers.%d.self_attn.o_proj.weight", l, &t));
             CUJEV_TRY(upload_fused(L, &t, 1, m->Hq * m->D, &ly->w_o));
+            CUJEV_TRY(upload_tiled(L, ly->w_o, H, m->Hq * m->D, &ly->wt_o));
             CUJEV_TRY(want(L, "layers.%d.self_attn.q_norm.weight", l, &t));
             CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)m->D, &ly->q_norm));
             CUJEV_TRY(want(L, "layers.%d.self_attn.k_norm.weight", l, &t));
@@ -217,8 +236,10 @@ static cujev_status walk(loader *L) {
                 parts[2]->shape[0] != m->Hv || parts[3]->shape[0] != m->Hv)
                 return cujev_fail(CUJEV_ERR_FORMAT, "layer %d: GDN projection shapes", l);
             CUJEV_TRY(upload_fused(L, parts, 4, H, &ly->w_in));
+            CUJEV_TRY(upload_tiled(L, ly->w_in, m->w_gdn, H, &ly->wt_in));
             CUJEV_TRY(want(L, "layers.%d.linear_attn.out_proj.weight", l, &t));
             CUJEV_TRY(upload_fused(L, &t, 1, m->V, &ly->w_out));
+            CUJEV_TRY(upload_tiled(L, ly->w_out, H, m->V, &ly->wt_out));
             CUJEV_TRY(want(L, "layers.%d.linear_attn.conv1d.weight", l, &t));
             CUJEV_TRY(upload_f32(L, t, 0.f, 0, (size_t)m->C * 4, &ly->conv_w));
             CUJEV_TRY(want(L, "layers.%d.linear_attn.A_log", l, &t));
@@ -233,8 +254,10 @@ static cujev_status walk(loader *L) {
         if (parts[0]->shape[0] != c->intermediate_size || parts[1]->shape[0] != c->intermediate_size)
             return cujev_fail(CUJEV_ERR_FORMAT, "layer %d: MLP shapes", l);
         CUJEV_TRY(upload_fused(L, parts, 2, H, &ly->w_gate_up));
+        CUJEV_TRY(upload_tiled(L, ly->w_gate_up, 2 * c->intermediate_size, H, &ly->wt_gate_up));
         CUJEV_TRY(want(L, "layers.%d.mlp.down_proj.weight", l, &t));
         CUJEV_TRY(upload_fused(L, &t, 1, c->intermediate_size, &ly->w_down));
+        CUJEV_TRY(upload_tiled(L, ly->w_down, H, c->intermediate_size, &ly->wt_down));
     }
     return CUJEV_OK;
 }
@@ -259,6 +282,8 @@ cujev_status cujev_model_load_weights(cujev_model *m, const char *dir) {
         L.dry = 0;
         s = walk(&L);
     }
+    if (s == CUJEV_OK && hipStreamSynchronize(m->stream) != hipSuccess) /* the tiling kernels */
+        s = cujev_fail(CUJEV_ERR_CUDA, "weight tiling failed");
     free(L.conv);
     st_bundle_close(&b);
     return s;

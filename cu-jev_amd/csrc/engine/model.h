@@ -36,6 +36,9 @@ typedef struct cujev_layer {
     /* mlp */
     bf16_t *w_gate_up; /* [2I, H] row-fused gate|up */
     bf16_t *w_down;    /* [H, I] */
+    /* the same projections tiled for the few-token GEMM (k_gemm_small_tile),
+     * which streams them at the eval shapes; NULL where it does not apply */
+    bf16_t *wt_qkv, *wt_o, *wt_in, *wt_out, *wt_gate_up, *wt_down;
 } cujev_layer;
 
 /* Captured eval forwards (see forward.c): one executable graph per launch

@@ -9,9 +9,18 @@
  *    every wave streams its 16 rows straight from HBM into registers, three
  *    128-wide K chunks ahead of the MFMAs (v_mfma_f32_16x16x32_bf16 with W
  *    as the A operand, 16 tokens per B fragment).
+ *  - W comes pre-tiled (k_gemm_small_tile, once per weight): the 16 rows x
+ *    128 k of one wave and chunk are one contiguous 4 KiB block laid out in
+ *    the order the wave's four 16-byte loads consume it, so every load
+ *    instruction reads 1 KiB of consecutive bytes. Streaming the plain
+ *    [M][K] rows (16 rows x 64 bytes per instruction) runs at two thirds of
+ *    that rate.
  *  - X (tiny, L2-resident) goes to an LDS ring by buffer DMA, the same three
- *    chunks ahead, and is shared by the four waves. Loads complete in issue
- *    order, so every wait is for loads issued three steps earlier.
+ *    chunks ahead, and is shared by the four waves. A fifth wave issues all
+ *    of those DMAs and waits for them before each step's barrier: an LDS
+ *    read completes only after every buffer_load ... lds its own wave issued
+ *    earlier has landed, so DMAs issued by the computing waves would hold
+ *    their B-operand reads behind each prefetch.
  *  - A lane's 16 A-operand values for one 64-wide k step are 32 contiguous
  *    bytes of its W row (k = 64j + 16(l/16) + 0..15); the two MFMAs of the
  *    step take the halves, and the B fragments are read from LDS with the
@@ -44,16 +53,16 @@ typedef __attribute__((address_space(3))) void *lds_ptr;
  * names them directly gets no host-side launch stub. */
 /* s_waitcnt with only the vector-memory count constrained (gfx9 encoding:
  * vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima). The
- * counts used are 4 + 2 (NB + 4), NB = 1..6; others wait for everything. */
+ * counts used are 8 NB, NB = 1..6; others wait for everything. */
 #define SG_VM(v) __builtin_amdgcn_s_waitcnt(((v) & 15) | (((v) >> 4) << 14) | (7 << 4) | (15 << 8))
 DEV void sg_wait_vm(int vm) {
     switch (vm) {
-    case 14: SG_VM(14); break;
+    case 8: SG_VM(8); break;
     case 16: SG_VM(16); break;
-    case 18: SG_VM(18); break;
-    case 20: SG_VM(20); break;
-    case 22: SG_VM(22); break;
     case 24: SG_VM(24); break;
+    case 32: SG_VM(32); break;
+    case 40: SG_VM(40); break;
+    case 48: SG_VM(48); break;
     default: SG_VM(0); break;
     }
 }
@@ -70,8 +79,10 @@ DEV bf16x8 sg_lds16(const unsigned char *base, uint32_t off) {
         (__attribute__((address_space(3))) const unsigned char *)base + off);
 }
 
+constexpr int SG_THREADS = 320; /* 4 computing waves + the X loader wave */
+
 template <int NB, bool GATED, bool PART>
-__global__ __launch_bounds__(256, 2) void gemm_small_kernel(const bf16 *__restrict__ X, int ldx,
+__global__ __launch_bounds__(SG_THREADS, 2) void gemm_small_kernel(const bf16 *__restrict__ X, int ldx,
                                                             const bf16 *__restrict__ W, int N,
                                                             int K, int KS, bf16 *__restrict__ Y,
                                                             int ldy, float *__restrict__ P, int M) {
@@ -88,32 +99,53 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const bf16 *__restri
     const int wr0 = GATED ? blockIdx.x * 32 + 16 * (wave & 1) + (wave >> 1) * (M / 2)
                           : blockIdx.x * SG_BM + 16 * wave;
 
-    const bf16 *wrow = W + (size_t)(wr0 + c16) * K + kb + 16 * q;
+    /* tiled W: block (row group wr0/16, chunk) of 2048 elements; load i of
+     * lane l is elements 512 i + 8 l .. +7 of the block */
+    const bf16 *wblk = W + ((size_t)(wr0 >> 4) * (K / SG_KC) + kb / SG_KC) * 2048 + lane * 8;
     auto load_w = [&](int c, bf16x8 (&wf)[4]) {
-        const bf16 *p = wrow + SG_KC * min(c, nch - 1);
-        wf[0] = ldg8(p);
-        wf[1] = ldg8(p + 8);
-        wf[2] = ldg8(p + 64);
-        wf[3] = ldg8(p + 72);
-    };
-    /* X chunk -> LDS by buffer DMA: instruction i of wave w fills token rows
-     * 16i + 4w + 0..3; lane l lands on slot l%16 of row 16i + 4w + l/16 and
-     * fetches the chunk's 16-byte piece (l%16) ^ (row & 15). Rows >= N lie
-     * past the buffer's range and read as zeros. */
-    const uint32_t xbytes = (uint32_t)N * ldx * 2;
-    uint32_t xoff[NB];
+        const bf16 *p = wblk + (size_t)2048 * min(c, nch - 1);
 #pragma unroll
-    for (int i = 0; i < NB; i++) {
-        const int r = 16 * i + 4 * wave + (lane >> 4);
-        xoff[i] = (uint32_t)r * ldx * 2 + (uint32_t)(((lane & 15) ^ (r & 15)) * 16);
+        for (int i = 0; i < 4; i++)
+            wf[i] = ldg8(p + 512 * i);
+    };
+    /* the number of steps (one barrier each), rounds of 4 */
+    const int nsteps = (nch + 3) / 4 * 4;
+    if (wave == 4) {
+        /* X loader. A chunk -> LDS by buffer DMA: instruction i fills token
+         * rows 4i + 0..3; lane l lands on slot l%16 of row 4i + l/16 and
+         * fetches the chunk's 16-byte piece (l%16) ^ (row & 15). Rows >= N
+         * lie past the buffer's range and read as zeros. Step c: wait for
+         * chunk c (chunks c+1 and c+2, 8 NB DMAs, may stay in flight), the
+         * barrier, then chunk c+3 into the stage chunk c-1 used. */
+        const uint32_t xbytes = (uint32_t)N * ldx * 2;
+        uint32_t xoff[4 * NB];
+#pragma unroll
+        for (int i = 0; i < 4 * NB; i++) {
+            const int r = 4 * i + (lane >> 4);
+            xoff[i] = (uint32_t)r * ldx * 2 + (uint32_t)(((lane & 15) ^ (r & 15)) * 16);
+        }
+        auto load_x = [&](int c) {
+            unsigned char *st = xs + (c % SG_NS) * XSTAGE;
+            const int kbyte = (kb + SG_KC * min(c, nch - 1)) * 2;
+#pragma unroll
+            for (int i = 0; i < 4 * NB; i++)
+                sg_dma16(X, xbytes, st + 4 * i * 256, xoff[i], kbyte);
+        };
+        load_x(0);
+        load_x(1);
+        load_x(2);
+        for (int c = 0; c < nsteps; c++) {
+            sg_wait_vm(8 * NB);
+            lds_barrier();
+            load_x(c + 3);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* no DMA into LDS outlives the kernel */
+        if constexpr (GATED) { /* the epilogue's two barriers */
+            lds_barrier();
+            lds_barrier();
+        }
+        return;
     }
-    auto load_x = [&](int c) {
-        unsigned char *st = xs + (c % SG_NS) * XSTAGE;
-        const int kbyte = (kb + SG_KC * min(c, nch - 1)) * 2;
-#pragma unroll
-        for (int i = 0; i < NB; i++)
-            sg_dma16(X, xbytes, st + (16 * i + 4 * wave) * 256, xoff[i], kbyte);
-    };
 
     floatx4 acc[NB];
 #pragma unroll
@@ -137,35 +169,29 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const bf16 *__restri
             }
     };
 
-    /* Each step c: wait for chunk c's X (its DMA was issued 3 steps ago;
-     * after it came W of c and the X and W of c+1, c+2: 4 + 2 (NB + 4) vector
-     * memory operations), barrier, refill the stage chunk c-1 used with
-     * chunk c+3, load W of c+3, compute c. W lives in the register ring
-     * w0..w3 (slot c % 4). Whole rounds of 4 steps, no early exit: past the
-     * end the loads repeat the last chunk and only the MFMAs are skipped. */
+    /* Each step c: the barrier (after it chunk c's X is in LDS and the
+     * stage chunk c-1 used is free), load W of c+3, compute c. W lives in
+     * the register ring w0..w3 (slot c % 4); the compiler waits for each W
+     * register before its MFMA. Whole rounds of 4 steps, no early exit: past
+     * the end the loads repeat the last chunk and only the MFMAs are
+     * skipped. */
     bf16x8 w0[4], w1[4], w2[4], w3[4];
-    load_x(0);
     load_w(0, w0);
-    load_x(1);
     load_w(1, w1);
-    load_x(2);
     load_w(2, w2);
     auto step = [&](int c, const bf16x8 (&wcur)[4], bf16x8 (&wfill)[4]) {
-        sg_wait_vm(4 + 2 * (NB + 4));
         lds_barrier();
-        load_x(c + 3);
         load_w(c + 3, wfill);
         __builtin_amdgcn_sched_barrier(0); /* keep the prefetches here */
         if (c < nch)
             compute(c, wcur);
     };
-    for (int c = 0; c < nch; c += 4) {
+    for (int c = 0; c < nsteps; c += 4) {
         step(c, w0, w3);
         step(c + 1, w1, w0);
         step(c + 2, w2, w1);
         step(c + 3, w3, w2);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* no DMA into LDS outlives the kernel */
 
     /* acc[nb]: token 16 nb + c16, rows wr0 + 4q .. +3 */
     if constexpr (GATED) {
@@ -209,12 +235,32 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const bf16 *__restri
     }
 }
 
+/* W [M][K] -> the tiled layout the kernel streams: block b = (g, c), g = row
+ * group of 16, c = 128-wide K chunk, at b = g (K/128) + c; element 512 i +
+ * 8 l + e of the block is W[16 g + l%16][128 c + 64 (i/2) + 16 (l/16) +
+ * 8 (i%2) + e] (the A operand of lane l = row l%16, k 16 (l/16) + 8 hf.., for
+ * the two MFMAs of k step 64 j, i = 2 j + hf). One thread per 16 bytes. */
+__global__ __launch_bounds__(256) void gemm_small_tile_kernel(const bf16 *__restrict__ W, int M,
+                                                              int K, bf16 *__restrict__ Wt) {
+    const size_t piece = (size_t)blockIdx.x * 256 + threadIdx.x; /* 8 elements each */
+    const size_t total = (size_t)M * K / 8;
+    if (piece >= total)
+        return;
+    const int l = (int)(piece & 63), i = (int)((piece >> 6) & 3);
+    const size_t b = piece >> 8;
+    const int nchunk = K / SG_KC;
+    const int g = (int)(b / nchunk), c = (int)(b % nchunk);
+    const int row = 16 * g + (l & 15);
+    const int k = SG_KC * c + 64 * (i >> 1) + 16 * (l >> 4) + 8 * (i & 1);
+    *(bf16x8 *)(Wt + piece * 8) = ldg8(W + (size_t)row * K + k);
+}
+
 template <bool GATED, bool PART>
 hipError_t launch_nb(int NB, dim3 grid, hipStream_t s, const bf16 *X, int ldx, const bf16 *W,
                      int N, int K, int KS, bf16 *Y, int ldy, float *P, int M) {
 #define CUJEV_SG_CASE(nb)                                                                    \
     case nb:                                                                                 \
-        hipLaunchKernelGGL((gemm_small_kernel<nb, GATED, PART>), grid, dim3(256), 0, s, X, ldx, \
+        hipLaunchKernelGGL((gemm_small_kernel<nb, GATED, PART>), grid, dim3(SG_THREADS), 0, s, X, ldx, \
                            W, N, K, KS, Y, ldy, P, M);                                        \
         break;
     switch (NB) {
@@ -245,6 +291,16 @@ extern "C" int cujev_gemm_small_splits(int M, int K) {
     while (chunks % s)
         s--;
     return s;
+}
+
+extern "C" hipError_t k_gemm_small_tile(const bf16_t *W, int M, int K, bf16_t *Wt,
+                                        hipStream_t stream) {
+    if (M <= 0 || K <= 0 || M % 16 || K % SG_KC || W == Wt)
+        return hipErrorInvalidValue;
+    const size_t pieces = (size_t)M * K / 8;
+    hipLaunchKernelGGL(gemm_small_tile_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256),
+                       0, stream, (const bf16 *)W, M, K, (bf16 *)Wt);
+    return hipGetLastError();
 }
 
 extern "C" hipError_t k_gemm_small(const bf16_t *X, int ldx, const bf16_t *W, int N, int M, int K,

@@ -175,7 +175,8 @@ hipError_t k_readout(const bf16_t *h, const bf16_t *E, const int32_t *cand, cons
 
 /* ---- weight-streaming GEMM for few tokens (gemm_small.hip) ---------------
  * Y[N, M] = X[N, K] . W[M, K]^T for N <= CUJEV_GEMM_SMALL_MAX_N, M % 64 == 0,
- * K % 128 == 0, X rows of stride ldx. splits == 1 writes bf16 Y (row stride
+ * K % 128 == 0, X rows of stride ldx, W given in the tiled layout that
+ * k_gemm_small_tile writes (same size as W). splits == 1 writes bf16 Y (row stride
  * ldy); splits > 1 (K / 128 divisible by splits) writes fp32 partial sums
  * P[splits][N][M] instead, to be summed by the consumer in split order.
  * gated (splits == 1): W is the fused [gate I | up I] (M = 2I) and Y gets
@@ -185,6 +186,9 @@ hipError_t k_readout(const bf16_t *h, const bf16_t *E, const int32_t *cand, cons
 int cujev_gemm_small_splits(int M, int K); /* suggested split count (<= MAX_SPLITS), 0 = shape unsupported */
 hipError_t k_gemm_small(const bf16_t *X, int ldx, const bf16_t *W, int N, int M, int K, int gated,
                         int splits, bf16_t *Y, int ldy, float *P, hipStream_t stream);
+/* W [M, K] (M % 16 == 0, K % 128 == 0) -> Wt, the tiled copy k_gemm_small
+ * streams: one contiguous 4 KiB block per 16 rows x 128 k. */
+hipError_t k_gemm_small_tile(const bf16_t *W, int M, int K, bf16_t *Wt, hipStream_t stream);
 
 /* ---- projection GEMMs (hipBLASLt) ------------------------------------------
  * Y[N,M] = X[N,K] . W[M,K]^T, bf16 in, fp32 accumulate, bf16 (f32out = 0) or

@@ -83,6 +83,13 @@ EXPORT int cujev_op_gemm_small(const void *X, int ldx, const void *W, int N, int
                     "gemm_small");
 }
 
+EXPORT int cujev_op_gemm_small_tile(const void *W, int M, int K, void *Wt, void *stream) {
+    if (!W || !Wt || W == Wt || M <= 0 || K <= 0 || M % 16 || K % 128)
+        return fail(1, "gemm_small_tile: bad arguments");
+    return launched(k_gemm_small_tile((const bf16_t *)W, M, K, (bf16_t *)Wt, (hipStream_t)stream),
+                    "gemm_small_tile");
+}
+
 EXPORT int cujev_op_add_rmsnorm(float *x, const void *y, const float *yp, int splits,
                                 const float *w, void *out, int N, int H, float eps,
                                 const int32_t *rows, int R, void *stream) {

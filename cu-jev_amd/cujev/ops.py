@@ -35,6 +35,7 @@ _SIGS = {
     "cujev_op_gdn_conv_prep": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P,
                                _P, _P],
     "cujev_op_gemm_small": [_P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _P],
+    "cujev_op_gemm_small_tile": [_P, _I, _I, _P, _P],
     "cujev_op_add_rmsnorm": [_P, _P, _P, _I, _P, _P, _I, _I, _F, _P, _I, _P],
     "cujev_op_gdn_scan": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _F, _I,
                           _I, _I, _P, _P, _P],
@@ -185,9 +186,20 @@ def gemm_small_splits(M, K) -> int:
     return int(load().cujev_ops_gemm_small_splits(int(M), int(K)))
 
 
+def gemm_small_tile(W):
+    """The tiled copy of W [M, K] that gemm_small reads (same shape and dtype;
+    the content is permuted into one 4 KiB block per 16 rows x 128 k)."""
+    import torch
+    Wt = torch.empty_like(W)
+    M, K = W.shape
+    _call("cujev_op_gemm_small_tile", _ptr(W), int(M), int(K), _ptr(Wt), _stream())
+    return Wt
+
+
 def gemm_small(X, W, Y=None, P=None, splits=1, gated=False, N=None, K=None):
     """Few-token GEMM: Y[N,M] = X[N,K] . W[M,K]^T (splits == 1, bf16 Y; gated:
-    Y = act[N, M/2]) or fp32 partials P[splits][N][M] (splits > 1)."""
+    Y = act[N, M/2]) or fp32 partials P[splits][N][M] (splits > 1). W is the
+    tiled copy from gemm_small_tile."""
     N = X.shape[0] if N is None else N
     K = W.shape[1] if K is None else K
     M = W.shape[0]

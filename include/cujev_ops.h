@@ -61,6 +61,12 @@ int cujev_op_gemm_tune(const void *X, const void *W, void *Y, int f32out, int N,
  *     reference's GEMM + silu_mul pair (src/kernels/elementwise.cu:42-54). */
 int cujev_op_gemm_small(const void *X, int ldx, const void *W, int N, int M, int K, int gated,
                         int splits, void *Y, int ldy, float *P, void *stream);
+/* The weight layout cujev_op_gemm_small reads: Wt (M*K bf16, distinct from W)
+ * receives W [M][K] (M % 16 == 0, K % 128 == 0) as one contiguous 4 KiB
+ * block per 16 rows x 128 k, in the order the kernel's loads consume it.
+ * Run once per weight; no counterpart in the reference, whose cuBLAS calls
+ * read the plain rows. */
+int cujev_op_gemm_small_tile(const void *W, int M, int K, void *Wt, void *stream);
 /* Split count the engine uses for an (M, K) few-token GEMM; 0 = unsupported shape. */
 int cujev_ops_gemm_small_splits(int M, int K);
 

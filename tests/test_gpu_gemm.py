@@ -42,7 +42,7 @@ def test_gemm_small_matches_fp32(N, M, K):
     X = rand_bf16(N, K, seed=1)
     W = rand_bf16(M, K, seed=2, scale=0.02)
     Y = torch.empty(N, M, dtype=torch.bfloat16, device="cuda")
-    o.gemm_small(X, W, Y=Y)
+    o.gemm_small(X, o.gemm_small_tile(W), Y=Y)
     torch.cuda.synchronize()
     ref = X.float() @ W.float().t()
     e = rel(Y.float(), ref)
@@ -57,7 +57,7 @@ def test_gemm_small_gated_is_silu_mul(N, I, H):
     X = rand_bf16(N, H, seed=3)
     W = rand_bf16(2 * I, H, seed=4, scale=0.05)
     act = torch.empty(N, I, dtype=torch.bfloat16, device="cuda")
-    o.gemm_small(X, W, Y=act, gated=True)
+    o.gemm_small(X, o.gemm_small_tile(W), Y=act, gated=True)
     torch.cuda.synchronize()
     gu = (X.float() @ W.float().t()).to(torch.bfloat16).float()  # the GEMM's bf16 output
     ref = torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]
@@ -83,12 +83,13 @@ def test_split_partials_feed_add_rmsnorm(N, H, K):
     P = torch.empty(max(sp, 1), N, H, dtype=torch.float32, device="cuda")
     out = torch.empty(N, H, dtype=torch.bfloat16, device="cuda")
     x = x0.clone()
+    Wt = o.gemm_small_tile(W)
     if sp > 1:
-        o.gemm_small(X, W, P=P, splits=sp)
+        o.gemm_small(X, Wt, P=P, splits=sp)
         o.add_rmsnorm(x, w, out, 1e-6, yp=P, splits=sp)
     else:
         y = torch.empty(N, H, dtype=torch.bfloat16, device="cuda")
-        o.gemm_small(X, W, Y=y)
+        o.gemm_small(X, Wt, Y=y)
         o.add_rmsnorm(x, w, out, 1e-6, y=y)
     torch.cuda.synchronize()
     y_ref = (X.float() @ W.float().t()).to(torch.bfloat16).float()
@@ -100,10 +101,33 @@ def test_split_partials_feed_add_rmsnorm(N, H, K):
     assert e <= TOL
     if sp > 1:  # deterministic: a second run is bit-identical
         x2, out2 = x0.clone(), torch.empty_like(out)
-        o.gemm_small(X, W, P=P, splits=sp)
+        o.gemm_small(X, Wt, P=P, splits=sp)
         o.add_rmsnorm(x2, w, out2, 1e-6, yp=P, splits=sp)
         torch.cuda.synchronize()
         assert torch.equal(out, out2) and torch.equal(x, x2)
+
+
+def tile_reference(W):
+    """The tiled layout restated with tensor indexing: block (g, c) of 16 rows x
+    128 k, element 512 i + 8 l + e = W[16 g + l%16][128 c + 64 (i//2) +
+    16 (l//16) + 8 (i%2) + e]."""
+    M, K = W.shape
+    t = W.reshape(M // 16, 16, K // 128, 2, 4, 2, 8)   # g, r, c, j, q, hf, e
+    t = t.permute(0, 2, 3, 5, 4, 1, 6)                  # g, c, j, hf, q, r, e
+    return t.reshape(M, K)
+
+
+@pytest.mark.parametrize("M,K", [(64, 128), (48, 384), (12352, 2560)])
+def test_gemm_small_tile_layout(M, K):
+    """The tiling kernel is an exact permutation (bit-exact against the
+    indexing restatement) and round-trips every element."""
+    o = ops()
+    W = rand_bf16(M, K, seed=10)
+    Wt = o.gemm_small_tile(W)
+    torch.cuda.synchronize()
+    assert torch.equal(Wt, tile_reference(W))
+    assert torch.equal(torch.sort(Wt.view(-1).view(torch.int16))[0],
+                       torch.sort(W.view(-1).view(torch.int16))[0])
 
 
 def test_gemm_small_rejects_unsupported_shapes():
