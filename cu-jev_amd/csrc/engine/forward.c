@@ -346,7 +346,10 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
     a.rows = d + o_rows;
     a.cand = cand ? d + o_cand : NULL;
     a.ncand = cand ? d + o_ncand : NULL;
-    const cujev_chunks chunks = {d + o_ctok, d + o_clen, d + o_sc0, d + o_snc, nc, B};
+    int max_snc = 0;
+    for (int b = 0; b < B; b++)
+        max_snc = h[o_snc + b] > max_snc ? h[o_snc + b] : max_snc;
+    const cujev_chunks chunks = {d + o_ctok, d + o_clen, d + o_sc0, d + o_snc, nc, B, max_snc};
     a.chunks = chunks;
     return mode == CUJEV_FWD_EVAL ? run_eval(m, st, &a) : launch_all(m, st, &a);
 }

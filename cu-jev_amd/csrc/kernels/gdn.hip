@@ -719,6 +719,163 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
     }
 }
 
+/* ---------------------------------------------------------------------- */
+/* phase B for one-chunk segments with no state written back (eval branches) */
+/* ---------------------------------------------------------------------- */
+/* Every segment starts from the same S_in and nothing carries over between
+ * them, so a workgroup takes one v-head and spw consecutive segments (as many
+ * as keep about SB_WGS workgroups busy): S^T (bf16) goes to LDS once, then
+ * per segment wave w computes columns 32w..32w+31 of
+ *   V' = U - W S,  O = (Q e^G) S + QKm V'
+ * for the 16-row blocks that hold tokens (the same 16x16x32 steps and
+ * operand fragments as gdn_chunk_b_kernel), and the workgroup applies the
+ * gated RMSNorm of gdn_norm_gate_kernel to the segment's rows. */
+constexpr int SB_WGS = 512;
+
+__global__ __launch_bounds__(256) void gdn_short_b_kernel(
+    const bf16x8 *__restrict__ Wi, const bf16x8 *__restrict__ Qgi, const bf16x8 *__restrict__ QKi,
+    const bf16x8 *__restrict__ Ui, const int32_t *__restrict__ chunk_tok0,
+    const int32_t *__restrict__ chunk_len, const int32_t *__restrict__ seg_chunk0,
+    const int32_t *__restrict__ seg_nchunk, int nseg, int spw, const float *__restrict__ S_in,
+    int Hv,
+    const bf16 *__restrict__ z, int zs, const float *__restrict__ nw, float eps,
+    bf16 *__restrict__ y) {
+    __shared__ __attribute__((aligned(16))) bf16 sT[DV][DK + 8]; /* S^T [column][dk]       */
+    __shared__ __attribute__((aligned(16))) bf16 vT[DV][CH + 8]; /* V'^T [column][token]   */
+    __shared__ __attribute__((aligned(16))) bf16 ob[CH][DV + 8]; /* O (bf16) [token][column] */
+
+    const int hv = blockIdx.y, sg0 = blockIdx.x * spw;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q4 = lane >> 4, c16 = lane & 15;
+    const int col0 = 32 * wave;
+
+    /* S^T: thread reads S[dk0..dk0+7][dv4..dv4+3] (16-byte rows) and writes
+     * the 4 columns' 8-element runs */
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+        const int dv4 = 4 * (tid & 31), dk0 = 8 * (tid >> 5) + 64 * it;
+        float4 r[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            r[e] = S_in ? *(const float4 *)(S_in + ((size_t)hv * DK + dk0 + e) * DV + dv4)
+                        : float4{0.f, 0.f, 0.f, 0.f};
+        bf16x8 c[4];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            c[0][e] = f2bf(r[e].x);
+            c[1][e] = f2bf(r[e].y);
+            c[2][e] = f2bf(r[e].z);
+            c[3][e] = f2bf(r[e].w);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *(bf16x8 *)&sT[dv4 + j][dk0] = c[j];
+    }
+    /* V'^T rows past a segment's last 16-row block may be read by the QKm
+     * step (times an exact zero of the causal mask): keep them finite */
+    for (int i = tid; i < DV * (CH + 8) / 8; i += 256)
+        ((bf16x8 *)&vT[0][0])[i] = bf16x8{};
+    lds_barrier();
+
+    float wl[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        wl[e] = nw[8 * (tid & 15) + e];
+
+    for (int j = 0; j < spw; j++) {
+        const int seg = sg0 + j;
+        if (seg >= nseg)
+            break;
+        if (seg_nchunk[seg] <= 0)
+            continue;
+        const int ch = seg_chunk0[seg];
+        const int t0 = chunk_tok0[ch], L = chunk_len[ch];
+        const int nrb = (L + 15) >> 4, nks = (L + 31) >> 5;
+        const size_t cb = (size_t)ch * Hv + hv;
+
+        floatx4 O[4][2];
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            O[rb][0] = floatx4{};
+            O[rb][1] = floatx4{};
+            if (rb >= nrb)
+                continue;
+            bf16x8 w[4], qg[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                w[s] = Wi[cb * 1024 + rb * 256 + 64 * s + lane];
+                qg[s] = Qgi[cb * 1024 + rb * 256 + 64 * s + lane];
+            }
+            const bf16x8 u = Ui[cb * 1024 + (wave * 4 + rb) * 64 + lane];
+            floatx4 V[2] = {};
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int jb = 0; jb < 2; jb++) {
+                    const bf16x8 sb = *(const bf16x8 *)&sT[col0 + 16 * jb + c16][32 * s + 8 * q4];
+                    V[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[s], sb, V[jb], 0, 0, 0);
+                    O[rb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qg[s], sb, O[rb][jb], 0, 0, 0);
+                }
+#pragma unroll
+            for (int jb = 0; jb < 2; jb++) {
+                bf16x4 p;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    p[i] = f2bf(bf2f(u[4 * jb + i]) - V[jb][i]);
+                *(bf16x4 *)&vT[col0 + 16 * jb + c16][16 * rb + 4 * q4] = p;
+            }
+        }
+        /* the wave reads back only its own columns of V'^T: LDS order suffices */
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            if (rb >= nrb)
+                continue;
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                if (s >= nks)
+                    continue;
+                const bf16x8 qk = QKi[cb * 512 + rb * 128 + 64 * s + lane];
+#pragma unroll
+                for (int jb = 0; jb < 2; jb++) {
+                    const bf16x8 vb = *(const bf16x8 *)&vT[col0 + 16 * jb + c16][32 * s + 8 * q4];
+                    O[rb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qk, vb, O[rb][jb], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int jb = 0; jb < 2; jb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    ob[16 * rb + 4 * q4 + i][col0 + 16 * jb + c16] = f2bf(O[rb][jb][i]);
+        }
+        lds_barrier();
+        /* gated RMSNorm, 16 lanes per token row (as gdn_norm_gate_kernel) */
+        for (int r0 = 0; r0 < L; r0 += 16) {
+            const int t = r0 + (tid >> 4), sl = tid & 15;
+            if (t < L) { /* whole 16-lane groups */
+                const bf16x8 ov = *(const bf16x8 *)&ob[t][8 * sl];
+                const size_t n = (size_t)t0 + t;
+                const bf16 *zr = z + n * zs + hv * DV + 8 * sl;
+                float ss = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    ss += bf2f(ov[e]) * bf2f(ov[e]);
+#pragma unroll
+                for (int m = 1; m < 16; m <<= 1)
+                    ss += __shfl_xor(ss, m, 64);
+                const float inv = rsqrtf(ss * (1.f / DV) + eps);
+                bf16x8 res;
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    res[e] = f2bf(bf2f(f2bf(bf2f(ov[e]) * inv)) * wl[e] * silu_f(bf2f(zr[e])));
+                *(bf16x8 *)(y + (n * Hv + hv) * DV + 8 * sl) = res;
+            }
+        }
+        lds_barrier(); /* ob and vT are rewritten by the next segment */
+    }
+}
+
 /* y = bf16( w * bf16(o * rsqrt(mean o^2 + eps)) * silu(z) ): 16 lanes per
  * (token, v-head) row, 8 columns a lane. REF src/kernels/gdn.cu:193-216. */
 template <bool VEC>
@@ -804,6 +961,16 @@ extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t 
                        0, stream, (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, g, beta,
                        ck->chunk_tok0, ck->chunk_len, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->Qg,
                        (bf16 *)ws->QK, (bf16 *)ws->KgT, (bf16 *)ws->U, ws->Glast);
+    if (!S_out && ck->max_seg_chunks == 1) {
+        const int spw = max(1, CEIL_DIV(ck->num_segments * Hv, SB_WGS));
+        hipLaunchKernelGGL(gdn_short_b_kernel,
+                           dim3((unsigned)CEIL_DIV(ck->num_segments, spw), (unsigned)Hv),
+                           dim3(256), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
+                           (const bf16x8 *)ws->QK, (const bf16x8 *)ws->U, ck->chunk_tok0,
+                           ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk, ck->num_segments, spw,
+                           S_in, Hv, (const bf16 *)z, z_stride, norm_w, eps, (bf16 *)y);
+        return hipGetLastError();
+    }
     const int units = ck->num_segments * Hv;
     hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)(NCB * CEIL_DIV(units, 8) * 8)),
                        dim3(256), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,

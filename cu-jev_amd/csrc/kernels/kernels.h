@@ -89,6 +89,7 @@ typedef struct cujev_chunks {
     const int32_t *seg_nchunk; /* [num_segments] chunk count      */
     int num_chunks;
     int num_segments;
+    int max_seg_chunks; /* most chunks in one segment (host-side); 0 = not known */
 } cujev_chunks;
 
 /* Scratch of the chunked scan. Per (chunk, v-head), written by the parallel

@@ -2,10 +2,12 @@
 bench.py (timed with HIP events on the launch stream) and runnable on their
 own for profilers:
 
-    python -m cujev.kernel_bench attention|gdn|copy [iters]
+    python -m cujev.kernel_bench attention|gdn|gdn_branch|copy [iters]
 
 attention  config 3: Hq 16 / Hkv 4, D 256, state 8192 keys, 256 branches x 16
 gdn        config 2: Hk 16 / Hv 32, T = 2048 prefill (conv+gates, scan, norm)
+gdn_branch config 2 branches: 64 branches x 16 tokens continuing one state
+           (S and the conv tail read, nothing written back)
 copy       a plain device-to-device copy of 256 MiB (scale factor for the
            FETCH_SIZE / WRITE_SIZE counters)
 """
@@ -99,6 +101,46 @@ def gdn_case():
     return launch, {"bytes": nbytes}
 
 
+def gdn_branch_case(B=64, L=16):
+    import torch
+    from . import ops
+    ops.load()
+    Hk, Hv = 16, 32
+    N = B * L
+    C = (2 * Hk + Hv) * 128
+    Wd = C + Hv * 128 + 2 * Hv
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(3)
+    proj = torch.randn(N, Wd, device=dev, generator=g).to(torch.bfloat16)
+    conv_w = torch.randn(C, 4, device=dev, generator=g) * 0.5
+    conv_in = torch.randn(C, 3, device=dev, generator=g)
+    A_neg = -torch.rand(Hv, device=dev, generator=g) * 4
+    dt_bias = torch.zeros(Hv, device=dev)
+    norm_w = torch.ones(128, device=dev)
+    S_in = torch.randn(Hv, 128, 128, device=dev, generator=g) * 0.1
+    own_base = (torch.arange(N, device=dev, dtype=torch.int32) // L) * L
+    q = torch.empty(N, Hk, 128, dtype=torch.bfloat16, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty(N, Hv, 128, dtype=torch.bfloat16, device=dev)
+    gg = torch.empty(N, Hv, device=dev)
+    beta = torch.empty_like(gg)
+    y = torch.empty(N, Hv * 128, dtype=torch.bfloat16, device=dev)
+    tok0, clen, seg0, segn = (torch.as_tensor(a).to(dev) for a in ops.chunk_table([L] * B))
+    scratch = torch.empty(ops.gdn_scratch_bytes(len(tok0), Hv, N), dtype=torch.uint8, device=dev)
+
+    def launch():
+        ops.gdn_conv_prep(proj, conv_w, conv_in, None, N, own_base, A_neg, dt_bias, Hk, Hv, q, k,
+                          v, gg, beta)
+        ops.gdn_scan(q, k, v, gg, beta, tok0, clen, seg0, segn, S_in, None, proj[:, C:],
+                     proj.stride(0), norm_w, 1e-6, Hk, Hv, y, scratch,
+                     max_seg_chunks=(L + 63) // 64)
+
+    # compulsory bytes: pre-conv qkv, a/b, conv w, conv tail, S (once), z, bf16 out
+    nbytes = N * C * 2 + N * 2 * Hv * 2 + C * 4 * 4 + C * 3 * 4 + Hv * 128 * 128 * 4 \
+        + N * Hv * 128 * 2 + N * Hv * 128 * 2
+    return launch, {"bytes": nbytes}
+
+
 def copy_case(nbytes=256 << 20):
     import torch
     a = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
@@ -127,7 +169,8 @@ def time_launches(launch, iters=20, warmup=3):
     return e0.elapsed_time(e1) / iters * 1e3
 
 
-CASES = {"attention": attention_case, "gdn": gdn_case, "copy": copy_case}
+CASES = {"attention": attention_case, "gdn": gdn_case, "gdn_branch": gdn_branch_case,
+         "copy": copy_case}
 
 if __name__ == "__main__":
     name = sys.argv[1]

@@ -37,8 +37,8 @@ _SIGS = {
     "cujev_op_gemm_small": [_P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _P],
     "cujev_op_gemm_small_tile": [_P, _I, _I, _P, _P],
     "cujev_op_add_rmsnorm": [_P, _P, _P, _I, _P, _P, _I, _I, _F, _P, _I, _P],
-    "cujev_op_gdn_scan": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _F, _I,
-                          _I, _I, _P, _P, _P],
+    "cujev_op_gdn_scan": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _F,
+                          _I, _I, _I, _P, _P, _P],
 }
 
 
@@ -160,11 +160,14 @@ def gdn_scratch_bytes(num_chunks, Hv, N):
 
 
 def gdn_scan(q, k, v, g, beta, chunk_tok0, chunk_len, seg_chunk0, seg_nchunk, S_in, S_out, z,
-             z_stride, norm_w, eps, Hk, Hv, y, scratch):
+             z_stride, norm_w, eps, Hk, Hv, y, scratch, max_seg_chunks=0):
+    """max_seg_chunks: the largest seg_nchunk entry when the caller knows it
+    (0 = not given); 1 with S_out None takes the branch path."""
     _call("cujev_op_gdn_scan", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(chunk_tok0),
           _ptr(chunk_len), chunk_tok0.shape[0], _ptr(seg_chunk0), _ptr(seg_nchunk),
-          seg_chunk0.shape[0], _ptr(S_in), _ptr(S_out), _ptr(z), int(z_stride), _ptr(norm_w),
-          float(eps), Hk, Hv, q.shape[0], _ptr(y), _ptr(scratch), _stream())
+          seg_chunk0.shape[0], int(max_seg_chunks), _ptr(S_in), _ptr(S_out), _ptr(z),
+          int(z_stride), _ptr(norm_w), float(eps), Hk, Hv, q.shape[0], _ptr(y), _ptr(scratch),
+          _stream())
 
 
 _gemm_ws = None

@@ -129,11 +129,15 @@ size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv, int N);
  * chunks of 64 tokens from its start. S_in fp32 [Hv][128][128] (NULL = 0),
  * S_out (may be NULL) = final state of segment 0. y bf16 [N][Hv*128] is the
  * gated-RMSNorm output; z is read at z[n*z_stride + hv*128 + c].
+ * max_seg_chunks: the largest seg_nchunk entry as the caller knows it (0 =
+ * not given); 1 with S_out == NULL (branches continuing a state) selects a
+ * path that reads S once per v-head for a group of segments.
  * scratch: cujev_ops_gdn_scratch_bytes(num_chunks, Hv, N) bytes, 256-aligned. */
 int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const float *g,
                       const float *beta, const int32_t *chunk_tok0, const int32_t *chunk_len,
                       int num_chunks, const int32_t *seg_chunk0, const int32_t *seg_nchunk,
-                      int num_segments, const float *S_in, float *S_out, const void *z,
+                      int num_segments, int max_seg_chunks, const float *S_in, float *S_out,
+                      const void *z,
                       int z_stride, const float *norm_w, float eps, int Hk, int Hv, int N,
                       void *y, void *scratch, void *stream);
 

@@ -63,7 +63,9 @@ def oracle_segment(L, proj, tail, S0):
     return y.reshape(len(proj), -1), S, orc.gdn_conv_tail(x, tail)
 
 
-def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False):
+def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False, tell_max=True):
+    """tell_max: pass the chunk table's largest per-segment chunk count (lets
+    one-chunk branches take the branch path); False passes 0 (general path)."""
     dev = "cuda"
     N = proj.shape[0]
     pd = bf(proj).to(dev)
@@ -83,8 +85,9 @@ def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False):
     sin = t(S_in.astype(np.float32)) if S_in is not None else None
     sout = torch.zeros(L.Hv, DK, DV, dtype=torch.float32, device=dev) if write_state else None
     y = torch.empty(N, L.Hv * DV, dtype=torch.bfloat16, device=dev)
+    msc = int(np.max(segn)) if tell_max and len(segn) else 0
     o.gdn_scan(q, k, v, g, beta, t(tok0), t(clen), t(seg0), t(segn), sin, sout, pd[:, L.C:],
-               pd.stride(0), t(L.norm_w), L.eps, L.Hk, L.Hv, y, scratch)
+               pd.stride(0), t(L.norm_w), L.eps, L.Hk, L.Hv, y, scratch, max_seg_chunks=msc)
     torch.cuda.synchronize()
     res = {"y": y.float().cpu().numpy()}
     if write_state:
@@ -129,6 +132,29 @@ def test_gdn_branches_continue_from_state():
         e = rel_err(got["y"][start: start + Ls], y_ref)
         print(f"branch len {Ls}: {e:.3e}")
         assert e <= TOL
+        start += Ls
+
+
+@pytest.mark.parametrize("seg_lens", [[1, 2, 3, 5, 16, 17, 31, 32, 33, 47, 63, 64],
+                                      [20] * 4, [7] * 19])
+def test_gdn_one_chunk_branches(seg_lens):
+    """Branches of at most 64 tokens continuing a state (the eval): the path
+    that reads S once per v-head for a group of segments matches the oracle
+    and gives exactly the general path's output."""
+    o = ops()
+    L = Layer(9, 2, 4)
+    prefix = L.proj(100)
+    got_p = run_gpu(o, L, prefix, [100], write_state=True)
+    br = L.proj(sum(seg_lens))
+    got = run_gpu(o, L, br, seg_lens, conv_in=got_p["tail"], S_in=got_p["S"])
+    gen = run_gpu(o, L, br, seg_lens, conv_in=got_p["tail"], S_in=got_p["S"], tell_max=False)
+    np.testing.assert_array_equal(got["y"], gen["y"])
+    _, S0, tail0 = oracle_segment(L, prefix, None, None)
+    start = 0
+    for Ls in seg_lens:
+        y_ref, _, _ = oracle_segment(L, br[start: start + Ls], tail0, S0)
+        e = rel_err(got["y"][start: start + Ls], y_ref)
+        assert e <= TOL, (Ls, e)
         start += Ls
 
 
