@@ -187,6 +187,15 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
  * graph and every later one replays it. Graph nodes are kernels only (no
  * memset nodes). At most CUJEV_GRAPH_SLOTS shapes are kept (least recently
  * used goes first); a state's graphs are dropped with the state. */
+static int gdn_packing_enabled(void) {
+    static int cached = -1;
+    if (cached < 0) {
+        const char *e = getenv("CUJEV_GDN_PACK");
+        cached = !(e && *e == '0');
+    }
+    return cached;
+}
+
 static int graphs_enabled(void) {
     static int cached = -1;
     if (cached < 0) {
@@ -292,8 +301,31 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
         nc += (seg_len[b] + 63) / 64;
     if (nc > m->max_chunks)
         return cujev_fail(CUJEV_ERR_CAPACITY, "%d GDN chunks exceed %d", nc, m->max_chunks);
+    /* Eval branches that each fit a 64-token chunk: consecutive whole
+     * segments share a chunk (they all continue the stored state and write
+     * none back), so a scan chunk holds up to 64 tokens however short the
+     * branches are. npk = packed chunks, 0 when not packing. */
+    int npk = 0;
+    if (mode == CUJEV_FWD_EVAL && gdn_packing_enabled()) {
+        int fill = 64, end = -1;
+        for (int b = 0; b < B; b++) {
+            if (seg_len[b] > 64) {
+                npk = 0;
+                break;
+            }
+            if (seg_len[b] <= 0)
+                continue;
+            if (fill + seg_len[b] > 64 || seg_start[b] != end) {
+                npk++;
+                fill = 0;
+            }
+            fill += seg_len[b];
+            end = seg_start[b] + seg_len[b];
+        }
+    }
     int32_t *h = m->h_meta;
     size_t o = 0;
+    const size_t o_cst = o; o += 2 * (size_t)npk; /* uint64 segment-start masks, 8-byte aligned */
     const size_t o_tok = o; o += (size_t)N;
     const size_t o_pos = o; o += (size_t)N;
     const size_t o_base = o; o += (size_t)N;
@@ -323,6 +355,26 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
         }
         h[o_snc + b] = ci - h[o_sc0 + b];
     }
+    if (npk) { /* the chunk rows now describe packed chunks */
+        int pc = -1, end = -1;
+        uint64_t mask = 0;
+        for (int b = 0; b < B; b++) {
+            if (seg_len[b] <= 0)
+                continue;
+            if (pc < 0 || h[o_clen + pc] + seg_len[b] > 64 || seg_start[b] != end) {
+                if (pc >= 0)
+                    memcpy(h + o_cst + 2 * pc, &mask, 8);
+                pc++;
+                h[o_ctok + pc] = seg_start[b];
+                h[o_clen + pc] = 0;
+                mask = 0;
+            }
+            mask |= 1ull << h[o_clen + pc];
+            h[o_clen + pc] += seg_len[b];
+            end = seg_start[b] + seg_len[b];
+        }
+        memcpy(h + o_cst + 2 * pc, &mask, 8);
+    }
     if (cand) {
         memcpy(h + o_cand, cand, (size_t)B * maxc * 4);
         memcpy(h + o_ncand, ncand, (size_t)B * 4);
@@ -349,8 +401,13 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
     int max_snc = 0;
     for (int b = 0; b < B; b++)
         max_snc = h[o_snc + b] > max_snc ? h[o_snc + b] : max_snc;
-    const cujev_chunks chunks = {d + o_ctok, d + o_clen, d + o_sc0, d + o_snc, nc, B, max_snc};
+    const cujev_chunks chunks = {d + o_ctok, d + o_clen, d + o_sc0, d + o_snc, nc, B, max_snc,
+                                 NULL};
     a.chunks = chunks;
+    if (npk) {
+        a.nc = a.chunks.num_chunks = npk;
+        a.chunks.chunk_starts = (const uint64_t *)(d + o_cst);
+    }
     return mode == CUJEV_FWD_EVAL ? run_eval(m, st, &a) : launch_all(m, st, &a);
 }
 

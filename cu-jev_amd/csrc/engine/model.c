@@ -297,7 +297,7 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
     const size_t mix = N * (size_t)((m->Hq * m->D > m->V) ? m->Hq * m->D : m->V);
     const size_t br_kv = (size_t)m->Hkv * m->branch_stride * m->D * 2;
     m->max_chunks = m->max_tokens / 64 + (int)B + 1;
-    m->meta_ints = 3 * N + 3 * B + 2 * (size_t)m->max_chunks + B * (size_t)m->opts.max_candidates + B;
+    m->meta_ints = 3 * N + 3 * B + 4 * (size_t)m->max_chunks + B * (size_t)m->opts.max_candidates + B;
     m->gemm_ws_bytes = (size_t)64 << 20;
     struct {
         void **p;

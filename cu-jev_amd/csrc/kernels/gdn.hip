@@ -213,7 +213,12 @@ __global__ void gdn_conv_tail_kernel(const bf16 *__restrict__ proj, int ps,
  *      D tiles scaled by e^{G_last - G} are (k e^{G_last-G})^T, stored
  *      straight from registers after one cross-half exchange.
  *   5. W and U staged row-major in the freed q / v rows, then stored in
- *      fragment order. */
+ *      fragment order.
+ * A chunk may hold several whole segments (chunk_starts marks where each
+ * begins): G restarts at every segment start and A and QK^T are kept
+ * block-diagonal, so the segments do not see each other. This is valid for
+ * branches that all continue one state and write no final state: phase B then
+ * needs nothing per segment. */
 struct __attribute__((aligned(16))) ChunkA_Smem {
     bf16 K[CH][DK + 8];   /* k rows                     */
     bf16 Q[CH][DK + 8];   /* q rows, later W            */
@@ -221,6 +226,7 @@ struct __attribute__((aligned(16))) ChunkA_Smem {
     float AT[CH][CH + 4]; /* A, then T in place (rows 16-byte aligned) */
     bf16 QK[CH][CH + 8];  /* masked QK^T staging        */
     float G[CH], sK[CH], sKg[CH], sV[CH];
+    int Sid[CH]; /* segment of each token inside a packed chunk (1-based) */
 };
 static_assert(sizeof(ChunkA_Smem) <= 80 * 1024, "two phase-A workgroups per CU");
 
@@ -251,7 +257,8 @@ DEV float4 row_times(const float *P, const float *Qm) {
 __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
     const bf16 *__restrict__ qh, const bf16 *__restrict__ kh_, const bf16 *__restrict__ vh,
     const float *__restrict__ g, const float *__restrict__ beta,
-    const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len, int Hk, int Hv,
+    const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
+    const uint64_t *__restrict__ chunk_starts, int Hk, int Hv,
     bf16 *__restrict__ Wo, bf16 *__restrict__ Qgo, bf16 *__restrict__ QKo,
     bf16 *__restrict__ KgTo, bf16 *__restrict__ Uo, float *__restrict__ Glo) {
     __shared__ ChunkA_Smem sm;
@@ -279,13 +286,22 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
         if (wave == 0) {
             float gv = lane < L ? g[(size_t)(t0 + lane) * Hv + hv] : 0.f;
             const float bv = lane < L ? beta[(size_t)(t0 + lane) * Hv + hv] : 0.f;
+            /* segments packed into the chunk: st = first token of this
+             * lane's segment, en = its last (63 for the chunk's last one) */
+            const uint64_t starts = chunk_starts ? chunk_starts[ch] | 1ull : 1ull;
+            const uint64_t upto = lane == 63 ? ~0ull : (2ull << lane) - 1;
+            const int st = 63 - __builtin_clzll(starts & upto);
+            const uint64_t later = starts & ~upto;
+            const int en = later ? __builtin_ctzll(later) - 1 : 63;
+            /* cumulative sum restarted at each segment start */
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const float up = __shfl_up(gv, o, 64);
-                if (lane >= o)
+                if (lane - o >= st)
                     gv += up;
             }
-            const float gl = __shfl(gv, 63, 64);
+            const float gl = __shfl(gv, en, 64);
+            sm.Sid[lane] = __builtin_popcountll(starts & upto);
             sm.G[lane] = gv;
             sm.sK[lane] = bv * fast_exp(gv);
             sm.sKg[lane] = fast_exp(gl - gv);
@@ -319,22 +335,27 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
         }
         const int j = 32 * tj + col;
         const float Gj = sm.G[j];
+        const int Sj = sm.Sid[j];
         /* rows i = 32ti + 8m + 4h + 0..3: their G and beta four at a time,
          * read unconditionally (a read under the mask becomes a branch) */
         float Gi[16], Bi[16];
+        int Si[16];
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const float4 a = rd4(&sm.G[32 * ti + 8 * m + 4 * h]);
             const float4 b = rd4(&sm.sV[32 * ti + 8 * m + 4 * h]);
+            const int4 c = *(const int4 *)&sm.Sid[32 * ti + 8 * m + 4 * h];
             Gi[4 * m] = a.x, Gi[4 * m + 1] = a.y, Gi[4 * m + 2] = a.z, Gi[4 * m + 3] = a.w;
             Bi[4 * m] = b.x, Bi[4 * m + 1] = b.y, Bi[4 * m + 2] = b.z, Bi[4 * m + 3] = b.w;
+            Si[4 * m] = c.x, Si[4 * m + 1] = c.y, Si[4 * m + 2] = c.z, Si[4 * m + 3] = c.w;
         }
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int i = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
             const float dec = fast_exp(fminf(Gi[r] - Gj, 0.f));
-            sm.AT[i][j] = i > j ? Bi[r] * kk[r] * dec : 0.f;
-            sm.QK[i][j] = f2bf(i >= j ? qk[r] * dec : 0.f);
+            const bool same = Si[r] == Sj; /* tokens of one segment interact */
+            sm.AT[i][j] = i > j && same ? Bi[r] * kk[r] * dec : 0.f;
+            sm.QK[i][j] = f2bf(i >= j && same ? qk[r] * dec : 0.f);
         }
     }
     lds_barrier();
@@ -787,9 +808,10 @@ __global__ __launch_bounds__(256) void gdn_short_b_kernel(
         const int seg = sg0 + j;
         if (seg >= nseg)
             break;
-        if (seg_nchunk[seg] <= 0)
+        /* without a segment table every unit is one (packed) chunk */
+        if (seg_chunk0 && seg_nchunk[seg] <= 0)
             continue;
-        const int ch = seg_chunk0[seg];
+        const int ch = seg_chunk0 ? seg_chunk0[seg] : seg;
         const int t0 = chunk_tok0[ch], L = chunk_len[ch];
         const int nrb = (L + 15) >> 4, nks = (L + 31) >> 5;
         const size_t cb = (size_t)ch * Hv + hv;
@@ -959,18 +981,23 @@ extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t 
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(gdn_chunk_a_kernel, dim3((unsigned)ck->num_chunks, (unsigned)Hv), dim3(256),
                        0, stream, (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, g, beta,
-                       ck->chunk_tok0, ck->chunk_len, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->Qg,
-                       (bf16 *)ws->QK, (bf16 *)ws->KgT, (bf16 *)ws->U, ws->Glast);
-    if (!S_out && ck->max_seg_chunks == 1) {
-        const int spw = max(1, CEIL_DIV(ck->num_segments * Hv, SB_WGS));
-        hipLaunchKernelGGL(gdn_short_b_kernel,
-                           dim3((unsigned)CEIL_DIV(ck->num_segments, spw), (unsigned)Hv),
+                       ck->chunk_tok0, ck->chunk_len, ck->chunk_starts, Hk, Hv, (bf16 *)ws->W,
+                       (bf16 *)ws->Qg, (bf16 *)ws->QK, (bf16 *)ws->KgT, (bf16 *)ws->U, ws->Glast);
+    const bool packed = ck->chunk_starts != nullptr;
+    if (!S_out && (packed || ck->max_seg_chunks == 1)) {
+        /* packed: the units are the chunks, each scanned from S_in */
+        const int units = packed ? ck->num_chunks : ck->num_segments;
+        const int spw = max(1, CEIL_DIV(units * Hv, SB_WGS));
+        hipLaunchKernelGGL(gdn_short_b_kernel, dim3((unsigned)CEIL_DIV(units, spw), (unsigned)Hv),
                            dim3(256), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
                            (const bf16x8 *)ws->QK, (const bf16x8 *)ws->U, ck->chunk_tok0,
-                           ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk, ck->num_segments, spw,
-                           S_in, Hv, (const bf16 *)z, z_stride, norm_w, eps, (bf16 *)y);
+                           ck->chunk_len, packed ? nullptr : ck->seg_chunk0,
+                           packed ? nullptr : ck->seg_nchunk, units, spw, S_in, Hv,
+                           (const bf16 *)z, z_stride, norm_w, eps, (bf16 *)y);
         return hipGetLastError();
     }
+    if (packed)
+        return hipErrorInvalidValue; /* packed segments write no final state */
     const int units = ck->num_segments * Hv;
     hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)(NCB * CEIL_DIV(units, 8) * 8)),
                        dim3(256), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,

@@ -90,6 +90,11 @@ typedef struct cujev_chunks {
     int num_chunks;
     int num_segments;
     int max_seg_chunks; /* most chunks in one segment (host-side); 0 = not known */
+    /* [num_chunks] or NULL: bit t set where token t of the chunk starts a
+     * segment. Non-NULL packs whole segments (each <= 64 tokens) into chunks;
+     * only for branches that all continue S_in with no final state written.
+     * The segment arrays are then unused. */
+    const uint64_t *chunk_starts;
 } cujev_chunks;
 
 /* Scratch of the chunked scan. Per (chunk, v-head), written by the parallel

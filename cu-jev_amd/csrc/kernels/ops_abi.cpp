@@ -174,13 +174,16 @@ EXPORT int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const 
                              const float *beta, const int32_t *chunk_tok0,
                              const int32_t *chunk_len, int num_chunks, const int32_t *seg_chunk0,
                              const int32_t *seg_nchunk, int num_segments, int max_seg_chunks,
-                             const float *S_in, float *S_out, const void *z, int z_stride,
+                             const uint64_t *chunk_starts, const float *S_in, float *S_out,
+                             const void *z, int z_stride,
                              const float *norm_w, float eps, int Hk, int Hv, int N, void *y,
                              void *scratch, void *stream) {
     if (num_chunks < 0 || num_segments < 0 || N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk || !scratch)
         return fail(1, "gdn_scan: bad arguments");
-    cujev_chunks ck = {chunk_tok0, chunk_len,  seg_chunk0,    seg_nchunk,
-                       num_chunks, num_segments, max_seg_chunks};
+    if (chunk_starts && S_out)
+        return fail(1, "gdn_scan: packed segments write no final state");
+    cujev_chunks ck = {chunk_tok0, chunk_len,   seg_chunk0,     seg_nchunk,
+                       num_chunks, num_segments, max_seg_chunks, chunk_starts};
     cujev_gdn_scratch ws = cujev_gdn_scratch_carve(scratch, num_chunks, Hv);
     return launched(k_gdn_scan((const bf16_t *)q, (const bf16_t *)k, (const bf16_t *)v, g, beta,
                                &ck, S_in, S_out, (const bf16_t *)z, z_stride, norm_w, eps, Hk, Hv,

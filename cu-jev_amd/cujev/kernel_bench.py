@@ -2,12 +2,14 @@
 bench.py (timed with HIP events on the launch stream) and runnable on their
 own for profilers:
 
-    python -m cujev.kernel_bench attention|gdn|gdn_branch|copy [iters]
+    python -m cujev.kernel_bench attention|gdn|gdn_branch|gemm_*|blas_*|copy [iters]
 
 attention  config 3: Hq 16 / Hkv 4, D 256, state 8192 keys, 256 branches x 16
 gdn        config 2: Hk 16 / Hv 32, T = 2048 prefill (conv+gates, scan, norm)
 gdn_branch config 2 branches: 64 branches x 16 tokens continuing one state
            (S and the conv tail read, nothing written back)
+gemm_<p>    the few-token kernel on projection p (qkv, in, gate_up, down, o) at
+           N = 80 with cold weights; blas_<p> the same on hipBLASLt
 copy       a plain device-to-device copy of 256 MiB (scale factor for the
            FETCH_SIZE / WRITE_SIZE counters)
 """
@@ -125,20 +127,67 @@ def gdn_branch_case(B=64, L=16):
     gg = torch.empty(N, Hv, device=dev)
     beta = torch.empty_like(gg)
     y = torch.empty(N, Hv * 128, dtype=torch.bfloat16, device=dev)
-    tok0, clen, seg0, segn = (torch.as_tensor(a).to(dev) for a in ops.chunk_table([L] * B))
+    # the engine's eval table: whole branches packed into 64-token chunks
+    tok0, clen, starts = (torch.as_tensor(a).to(dev) for a in ops.packed_chunk_table([L] * B))
     scratch = torch.empty(ops.gdn_scratch_bytes(len(tok0), Hv, N), dtype=torch.uint8, device=dev)
 
     def launch():
         ops.gdn_conv_prep(proj, conv_w, conv_in, None, N, own_base, A_neg, dt_bias, Hk, Hv, q, k,
                           v, gg, beta)
-        ops.gdn_scan(q, k, v, gg, beta, tok0, clen, seg0, segn, S_in, None, proj[:, C:],
-                     proj.stride(0), norm_w, 1e-6, Hk, Hv, y, scratch,
-                     max_seg_chunks=(L + 63) // 64)
+        ops.gdn_scan(q, k, v, gg, beta, tok0, clen, None, None, S_in, None, proj[:, C:],
+                     proj.stride(0), norm_w, 1e-6, Hk, Hv, y, scratch, max_seg_chunks=1,
+                     chunk_starts=starts)
 
     # compulsory bytes: pre-conv qkv, a/b, conv w, conv tail, S (once), z, bf16 out
     nbytes = N * C * 2 + N * 2 * Hv * 2 + C * 4 * 4 + C * 3 * 4 + Hv * 128 * 128 * 4 \
         + N * Hv * 128 * 2 + N * Hv * 128 * 2
     return launch, {"bytes": nbytes}
+
+
+# The eval's projections at 4B shape: (rows M, inner K, gated gate|up pair)
+GEMM_SHAPES = {"qkv": (10240, 2560, False), "in": (12352, 2560, False),
+               "gate_up": (18432, 2560, True), "down": (2560, 9216, False),
+               "o": (2560, 4096, False)}
+
+
+def gemm_case(name, small=True, N=80):
+    """One projection of an 80-token eval with cold weights: every launch uses
+    the next of enough weight copies (> 1.2 GB in all) that none is still in
+    the 256 MB MALL, as in a request, where the other 31 layers evict a
+    layer's weights. small=True runs the few-token kernel on pre-tiled
+    weights (split-K partials where the engine uses them, the fused
+    silu(gate)*up for gate_up); small=False the hipBLASLt GEMM."""
+    import torch
+    from . import ops
+    ops.load()
+    M, K, gated = GEMM_SHAPES[name]
+    dev = "cuda"
+    ncopy = max(2, int(1.2e9 // (M * K * 2)))
+    g = torch.Generator(device=dev).manual_seed(5)
+    X = torch.randn(N, K, device=dev, generator=g).to(torch.bfloat16)
+    Ws = [(torch.randn(M, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+          for _ in range(ncopy)]
+    Y = torch.empty(N, M, dtype=torch.bfloat16, device=dev)
+    if small:
+        Ws = [ops.gemm_small_tile(W) for W in Ws]
+        sp = ops.gemm_small_splits(M, K)
+        P = torch.empty(max(sp, 1), N, M, dtype=torch.float32, device=dev)
+        A = torch.empty(N, M // 2, dtype=torch.bfloat16, device=dev)
+        if gated:
+            run = lambda W: ops.gemm_small(X, W, Y=A, gated=True)
+        elif M <= 4096 and sp > 1:  # residual projections: partials to the add
+            run = lambda W: ops.gemm_small(X, W, P=P, splits=sp)
+        else:
+            run = lambda W: ops.gemm_small(X, W, Y=Y)
+    else:
+        run = lambda W: ops.gemm(X, W, Y)
+    state = {"i": 0}
+
+    def launch():
+        run(Ws[state["i"] % ncopy])
+        state["i"] += 1
+
+    return launch, {"bytes": M * K * 2, "copies": ncopy}
 
 
 def copy_case(nbytes=256 << 20):
@@ -171,10 +220,14 @@ def time_launches(launch, iters=20, warmup=3):
 
 CASES = {"attention": attention_case, "gdn": gdn_case, "gdn_branch": gdn_branch_case,
          "copy": copy_case}
+for _g in GEMM_SHAPES:
+    CASES["gemm_" + _g] = lambda _g=_g: gemm_case(_g, small=True)
+    CASES["blas_" + _g] = lambda _g=_g: gemm_case(_g, small=False)
 
 if __name__ == "__main__":
     name = sys.argv[1]
     iters = int(sys.argv[2]) if len(sys.argv) > 2 else 20
     launch, info = CASES[name]()
     us = time_launches(launch, iters)
-    print(f"{name}: {us:.1f} us per launch {info}", flush=True)
+    tbs = f", {info['bytes'] / us / 1e6:.2f} TB/s" if "bytes" in info else ""
+    print(f"{name}: {us:.1f} us per launch{tbs} {info}", flush=True)

@@ -37,8 +37,8 @@ _SIGS = {
     "cujev_op_gemm_small": [_P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _P],
     "cujev_op_gemm_small_tile": [_P, _I, _I, _P, _P],
     "cujev_op_add_rmsnorm": [_P, _P, _P, _I, _P, _P, _I, _I, _F, _P, _I, _P],
-    "cujev_op_gdn_scan": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _F,
-                          _I, _I, _I, _P, _P, _P],
+    "cujev_op_gdn_scan": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P,
+                          _F, _I, _I, _I, _P, _P, _P],
 }
 
 
@@ -137,6 +137,30 @@ def gdn_conv_prep(proj, conv_w, conv_in, conv_out, seg0_len, own_base, A_neg_exp
           Hv, _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _stream())
 
 
+def packed_chunk_table(seg_lens, chunk=64):
+    """Host-side table of whole segments packed into chunks of at most `chunk`
+    tokens (consecutive segments while they fit), with the per-chunk bit mask
+    of segment starts. Every segment must fit one chunk. Returns chunk_tok0,
+    chunk_len (int32) and chunk_starts (uint64 bits in an int64 array)."""
+    import numpy as np
+    tok0, clen, starts = [], [], []
+    start = 0
+    for L in seg_lens:
+        if L > chunk:
+            raise ValueError("packed_chunk_table: segment longer than a chunk")
+        if L <= 0:
+            continue
+        if not tok0 or clen[-1] + L > chunk:
+            tok0.append(start)
+            clen.append(0)
+            starts.append(0)
+        starts[-1] |= 1 << clen[-1]
+        clen[-1] += L
+        start += L
+    as_i = lambda x: np.asarray(x, dtype=np.int32)
+    return as_i(tok0), as_i(clen), np.asarray(starts, dtype=np.uint64).view(np.int64)
+
+
 def chunk_table(seg_lens, chunk=64):
     """Host-side chunk table: every segment cut into `chunk`-token pieces."""
     import numpy as np
@@ -160,12 +184,15 @@ def gdn_scratch_bytes(num_chunks, Hv, N):
 
 
 def gdn_scan(q, k, v, g, beta, chunk_tok0, chunk_len, seg_chunk0, seg_nchunk, S_in, S_out, z,
-             z_stride, norm_w, eps, Hk, Hv, y, scratch, max_seg_chunks=0):
+             z_stride, norm_w, eps, Hk, Hv, y, scratch, max_seg_chunks=0, chunk_starts=None):
     """max_seg_chunks: the largest seg_nchunk entry when the caller knows it
-    (0 = not given); 1 with S_out None takes the branch path."""
+    (0 = not given); 1 with S_out None takes the branch path. chunk_starts
+    (int64 device tensor from packed_chunk_table, seg_chunk0 / seg_nchunk then
+    None) packs whole segments into chunks."""
+    nseg = seg_chunk0.shape[0] if seg_chunk0 is not None else 0
     _call("cujev_op_gdn_scan", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(chunk_tok0),
           _ptr(chunk_len), chunk_tok0.shape[0], _ptr(seg_chunk0), _ptr(seg_nchunk),
-          seg_chunk0.shape[0], int(max_seg_chunks), _ptr(S_in), _ptr(S_out), _ptr(z),
+          nseg, int(max_seg_chunks), _ptr(chunk_starts), _ptr(S_in), _ptr(S_out), _ptr(z),
           int(z_stride), _ptr(norm_w), float(eps), Hk, Hv, q.shape[0], _ptr(y), _ptr(scratch),
           _stream())
 

@@ -132,12 +132,16 @@ size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv, int N);
  * max_seg_chunks: the largest seg_nchunk entry as the caller knows it (0 =
  * not given); 1 with S_out == NULL (branches continuing a state) selects a
  * path that reads S once per v-head for a group of segments.
+ * chunk_starts (device uint64 [num_chunks], may be NULL): packs several whole
+ * segments of at most 64 tokens into one chunk; bit t is set where token t of
+ * the chunk starts a segment. Only with S_out == NULL: every segment continues
+ * S_in, and seg_chunk0 / seg_nchunk / num_segments are not read.
  * scratch: cujev_ops_gdn_scratch_bytes(num_chunks, Hv, N) bytes, 256-aligned. */
 int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const float *g,
                       const float *beta, const int32_t *chunk_tok0, const int32_t *chunk_len,
                       int num_chunks, const int32_t *seg_chunk0, const int32_t *seg_nchunk,
-                      int num_segments, int max_seg_chunks, const float *S_in, float *S_out,
-                      const void *z,
+                      int num_segments, int max_seg_chunks, const uint64_t *chunk_starts,
+                      const float *S_in, float *S_out, const void *z,
                       int z_stride, const float *norm_w, float eps, int Hk, int Hv, int N,
                       void *y, void *scratch, void *stream);
 

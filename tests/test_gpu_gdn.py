@@ -63,9 +63,12 @@ def oracle_segment(L, proj, tail, S0):
     return y.reshape(len(proj), -1), S, orc.gdn_conv_tail(x, tail)
 
 
-def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False, tell_max=True):
+def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False, tell_max=True,
+            pack=False):
     """tell_max: pass the chunk table's largest per-segment chunk count (lets
-    one-chunk branches take the branch path); False passes 0 (general path)."""
+    one-chunk branches take the branch path); False passes 0 (general path).
+    pack: whole segments packed into shared chunks (branches of <= 64 tokens
+    continuing S_in)."""
     dev = "cuda"
     N = proj.shape[0]
     pd = bf(proj).to(dev)
@@ -81,13 +84,21 @@ def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False, te
     o.gdn_conv_prep(pd, t(L.conv_w), cin, cout, seg_lens[0], t(own_base), t(L.A_neg),
                     t(L.dt_bias), L.Hk, L.Hv, q, k, v, g, beta)
     tok0, clen, seg0, segn = o.chunk_table(seg_lens)
+    starts = None
+    if pack:
+        tok0, clen, starts = o.packed_chunk_table(seg_lens)
     scratch = torch.empty(o.gdn_scratch_bytes(len(tok0), L.Hv, N), dtype=torch.uint8, device=dev)
     sin = t(S_in.astype(np.float32)) if S_in is not None else None
     sout = torch.zeros(L.Hv, DK, DV, dtype=torch.float32, device=dev) if write_state else None
     y = torch.empty(N, L.Hv * DV, dtype=torch.bfloat16, device=dev)
     msc = int(np.max(segn)) if tell_max and len(segn) else 0
-    o.gdn_scan(q, k, v, g, beta, t(tok0), t(clen), t(seg0), t(segn), sin, sout, pd[:, L.C:],
-               pd.stride(0), t(L.norm_w), L.eps, L.Hk, L.Hv, y, scratch, max_seg_chunks=msc)
+    if pack:
+        o.gdn_scan(q, k, v, g, beta, t(tok0), t(clen), None, None, sin, sout, pd[:, L.C:],
+                   pd.stride(0), t(L.norm_w), L.eps, L.Hk, L.Hv, y, scratch, max_seg_chunks=1,
+                   chunk_starts=t(starts))
+    else:
+        o.gdn_scan(q, k, v, g, beta, t(tok0), t(clen), t(seg0), t(segn), sin, sout, pd[:, L.C:],
+                   pd.stride(0), t(L.norm_w), L.eps, L.Hk, L.Hv, y, scratch, max_seg_chunks=msc)
     torch.cuda.synchronize()
     res = {"y": y.float().cpu().numpy()}
     if write_state:
@@ -149,6 +160,30 @@ def test_gdn_one_chunk_branches(seg_lens):
     got = run_gpu(o, L, br, seg_lens, conv_in=got_p["tail"], S_in=got_p["S"])
     gen = run_gpu(o, L, br, seg_lens, conv_in=got_p["tail"], S_in=got_p["S"], tell_max=False)
     np.testing.assert_array_equal(got["y"], gen["y"])
+    _, S0, tail0 = oracle_segment(L, prefix, None, None)
+    start = 0
+    for Ls in seg_lens:
+        y_ref, _, _ = oracle_segment(L, br[start: start + Ls], tail0, S0)
+        e = rel_err(got["y"][start: start + Ls], y_ref)
+        assert e <= TOL, (Ls, e)
+        start += Ls
+
+
+@pytest.mark.parametrize("seg_lens", [[1, 2, 3, 5, 16, 37, 64, 20, 20, 20, 63, 1],
+                                      [16] * 9, [64, 64, 1], [33, 31, 32, 32, 17]])
+def test_gdn_packed_branches(seg_lens):
+    """Branches of at most 64 tokens packed several to a chunk (block-diagonal
+    masks, G restarted per segment): every branch matches the oracle over
+    [prefix ++ branch] and stays close to the unpacked path."""
+    o = ops()
+    print(f"packed seg_lens={seg_lens}", flush=True)
+    L = Layer(11, 2, 4)
+    prefix = L.proj(90)
+    got_p = run_gpu(o, L, prefix, [90], write_state=True)
+    br = L.proj(sum(seg_lens))
+    got = run_gpu(o, L, br, seg_lens, conv_in=got_p["tail"], S_in=got_p["S"], pack=True)
+    ref = run_gpu(o, L, br, seg_lens, conv_in=got_p["tail"], S_in=got_p["S"])
+    assert rel_err(got["y"], ref["y"]) <= TOL
     _, S0, tail0 = oracle_segment(L, prefix, None, None)
     start = 0
     for Ls in seg_lens:
