@@ -146,9 +146,9 @@ def attention_roofline(iters=20):
     return dict(us=us, flop=info["flop"], tflops=info["flop"] / (us * 1e-6) / 1e12)
 
 
-def gdn_roofline(iters=20):
+def gdn_roofline(iters=20, case="gdn"):
     from cujev import kernel_bench
-    launch, info = kernel_bench.gdn_case()
+    launch, info = kernel_bench.CASES[case]()
     us = kernel_bench.time_launches(launch, iters)
     return dict(us=us, bytes=info["bytes"], gbs=info["bytes"] / (us * 1e-6) / 1e9)
 
@@ -285,13 +285,24 @@ def main():
                            "flop_per_launch": att["flop"]}
         gdn = gdn_roofline()
         log(f"gdn config 2 prefill: {gdn['us']:.1f} us, {gdn['gbs']:.1f} GB/s")
-        res["gdn_roofline"] = {"kernel": "gdn_conv_prep + conv_tail + chunk_a + chunk_b + "
-                                         "norm_gate, config 2 T=2048 prefill", "bound": "hbm",
+        res["gdn_roofline"] = {"kernel": "gdn layer call: conv_tail + chunk_a (conv and gates "
+                                         "inside) + chunk_b + norm_gate, config 2 T=2048 "
+                                         "prefill", "bound": "hbm",
                                "achieved": round(gdn["gbs"], 1), "peak": PEAK_HBM_GBS,
                                "unit": "GB/s", "frac": round(gdn["gbs"] / PEAK_HBM_GBS, 4),
                                "us_per_layer": round(gdn["us"], 2),
                                "compulsory_bytes": gdn["bytes"],
                                "traffic": kernel_bench.measured_traffic("gdn")}
+        gbr = gdn_roofline(case="gdn_branch")
+        log(f"gdn config 2 branches: {gbr['us']:.1f} us, {gbr['gbs']:.1f} GB/s")
+        res["gdn_branch_roofline"] = {"kernel": "gdn layer call: chunk_a (conv and gates inside, "
+                                                "packed chunks) + short_b (norm inside), config "
+                                                "2, 64 branches x 16 tokens", "bound": "hbm",
+                                      "achieved": round(gbr["gbs"], 1), "peak": PEAK_HBM_GBS,
+                                      "unit": "GB/s", "frac": round(gbr["gbs"] / PEAK_HBM_GBS, 4),
+                                      "us_per_layer": round(gbr["us"], 2),
+                                      "compulsory_bytes": gbr["bytes"],
+                                      "traffic": kernel_bench.measured_traffic("gdn_branch")}
     if not a.no_cpu_baseline:
         torch.cuda.empty_cache()
         base, parity = cpu_baseline(ckpt, e2e["first_req"], e2e["first_out"], e2e["first_full"])

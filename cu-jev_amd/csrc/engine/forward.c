@@ -139,16 +139,12 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
             K_TRY(proj_gemm(m, m->xb, ly->w_in, ly->wt_in, m->proj, N, m->w_gdn, H), "gemm in", l);
             const float *conv_in = mode == CUJEV_FWD_EVAL ? st->conv[l] : NULL;
             float *conv_out = mode == CUJEV_FWD_PREFILL ? st->conv[l] : NULL;
-            K_TRY(k_gdn_conv_prep(m->proj, m->w_gdn, ly->conv_w, conv_in, conv_out, N, a->base,
-                                  ly->A_neg_exp, ly->dt_bias, N, m->Hk, m->Hv, m->gq, m->gk, m->gv,
-                                  m->gg, m->gbeta, s),
-                  "gdn_conv_prep", l);
             const float *S_in = mode == CUJEV_FWD_EVAL ? st->S[l] : NULL;
             float *S_out = mode == CUJEV_FWD_PREFILL ? st->S[l] : NULL;
-            K_TRY(k_gdn_scan(m->gq, m->gk, m->gv, m->gg, m->gbeta, &a->chunks, S_in, S_out,
-                             m->proj + m->C, m->w_gdn, ly->g_norm, eps, m->Hk, m->Hv, m->mix_out,
-                             &gws, N, s),
-                  "gdn_scan", l);
+            K_TRY(k_gdn_layer(m->proj, m->w_gdn, ly->conv_w, conv_in, conv_out, N, a->base,
+                              ly->A_neg_exp, ly->dt_bias, &a->chunks, S_in, S_out, ly->g_norm,
+                              eps, m->Hk, m->Hv, m->mix_out, &gws, N, s),
+                  "gdn_layer", l);
             K_TRY(resid_gemm(m, m->mix_out, ly->w_out, ly->wt_out, N, H, m->V, &ry, &ryp, &rsp),
                   "gemm out", l);
         }

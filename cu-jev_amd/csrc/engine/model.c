@@ -312,11 +312,6 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
         {(void **)&m->mix_out, mix * 2},
         {(void **)&m->br_k, br_kv},
         {(void **)&m->br_vt, br_kv},
-        {(void **)&m->gq, N * (size_t)m->Hk * 128 * 2},
-        {(void **)&m->gk, N * (size_t)m->Hk * 128 * 2},
-        {(void **)&m->gv, N * (size_t)m->Hv * 128 * 2},
-        {(void **)&m->gg, N * (size_t)m->Hv * 4},
-        {(void **)&m->gbeta, N * (size_t)m->Hv * 4},
         {(void **)&m->gdn_scratch, cujev_gdn_scratch_bytes(m->max_chunks, m->Hv, m->max_tokens)},
         {(void **)&m->act, N * I * 2},
         {(void **)&m->hsel, B * H * 2},

@@ -85,8 +85,6 @@ struct cujev_model {
     bf16_t *q;       /* [N,Hq,256] prescaled */
     bf16_t *mix_out; /* [N, max(Hq*256, V)] */
     bf16_t *br_k, *br_vt;
-    bf16_t *gq, *gk, *gv; /* [N][Hk|Hv][128] */
-    float *gg, *gbeta;    /* [N][Hv] */
     void *gdn_scratch;
     bf16_t *act;  /* [N, I] */
     bf16_t *hsel; /* [B, H] */

@@ -254,9 +254,159 @@ DEV float4 row_times(const float *P, const float *Qm) {
     return acc;
 }
 
+/* The pre-conv inputs of the fused front end (gdn_conv_prep's arguments). */
+struct ConvSrc {
+    const bf16 *proj;
+    int ps;
+    const float *conv_w, *conv_in;
+    const int32_t *own_base;
+    const float *A_neg_exp, *dt_bias;
+    int N;
+};
+
+/* The three 128-channel slices a phase-A workgroup needs (q and k of its
+ * k-head, v of its v-head) through conv + SiLU (+ l2 norm and scale), with
+ * gdn_conv_prep_kernel's arithmetic step for step. Thread = (token block
+ * tid/16 of 4 tokens, channels 8(tid%16)..+7 of every slice). The 7
+ * pre-conv rows of each slice are loaded first; the conv weights and the
+ * state's tail (the same for all token blocks) go through LDS once:
+ * cw[slice][e][s] float4 and ct[slice][j][e][s] for channel 8s + e. */
+DEV int slice_c0(int sl, int Hk, int hk, int hv) {
+    return sl == 0 ? hk * DK : sl == 1 ? (Hk + hk) * DK : (2 * Hk + hv) * DK;
+}
+
+template <bool TAIL>
+DEV void conv_stage(const ConvSrc &cv, int Hk, int hk, int hv, int tid, float *cw, float *ct) {
+    for (int i = tid; i < 3 * DK; i += 256) {
+        const int sl = i / DK, c = i % DK, cg = slice_c0(sl, Hk, hk, hv) + c;
+        const int slot = (sl * 8 + (c & 7)) * 16 + (c >> 3);
+        *(float4 *)&cw[slot * 4] = *(const float4 *)(cv.conv_w + (size_t)cg * 4);
+        if constexpr (TAIL) {
+#pragma unroll
+            for (int j = 0; j < 3; j++)
+                ct[(sl * 3 + j) * 128 + (c & 7) * 16 + (c >> 3)] = cv.conv_in[(size_t)cg * 3 + j];
+        }
+    }
+}
+
+DEV void conv_rows(const ConvSrc &cv, int c0, int n0, bf16x8 (&x)[7]) {
+#pragma unroll
+    for (int i = 0; i < 7; i++) {
+        const int row = min(max(n0 - 3 + i, 0), cv.N - 1);
+        x[i] = ld8(cv.proj + (size_t)row * cv.ps + c0);
+    }
+}
+
+/* Sum over each row of 16 lanes with DPP moves (no LDS round trip). The
+ * quad steps leave identical sums in the 4 lanes of a quad, so the half-row
+ * and row mirrors read the same values as xor 4 and xor 8 would: the result
+ * equals the xor butterfly's bit for bit. */
+template <int CTRL> DEV float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                              0xf, 0xf, false));
+}
+DEV float sum16_dpp(float v) {
+    v += dpp<0xB1>(v);  /* quad_perm [1,0,3,2]: lane ^ 1 */
+    v += dpp<0x4E>(v);  /* quad_perm [2,3,0,1]: lane ^ 2 */
+    v += dpp<0x141>(v); /* row_half_mirror: the other quad of 8 */
+    v += dpp<0x140>(v); /* row_mirror: the other half of 16 */
+    return v;
+}
+
+template <bool TAIL>
+DEV void conv_slice(const bf16x8 (&x)[7], const int (&base)[4], const float *cw, const float *ct,
+                    int sl, bool norm, float scale, int t0, int L, int tid, bf16 (*dst)[DK + 8]) {
+    const int s = tid & 15, tb = tid >> 4;
+    float w[8][4];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float4 t = *(const float4 *)&cw[((sl * 8 + e) * 16 + s) * 4];
+        w[e][0] = t.x, w[e][1] = t.y, w[e][2] = t.z, w[e][3] = t.w;
+    }
+    float xf[7][8];
+#pragma unroll
+    for (int i = 0; i < 7; i++)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            xf[i][e] = bf2f(x[i][e]);
+    /* All 4 tokens in one segment (the usual case): rows before its start
+     * are replaced by the tail (or 0) once, and every token takes the plain
+     * 4-tap path. This is exactly the masked form below, whose single
+     * nonzero term is that same value. */
+    const int n0 = t0 + 4 * tb;
+    const bool one_seg = base[0] == base[3];
+    if (one_seg && n0 - 3 < base[0]) {
+#pragma unroll
+        for (int i = 0; i < 7; i++) {
+            const int k = n0 - 3 + i - base[0] + 3; /* tail slot of the row */
+            if (k < 3) {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    xf[i][e] = TAIL && k >= 0 ? ct[(sl * 3 + max(k, 0)) * 128 + e * 16 + s] : 0.f;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int tt = 4 * tb + j, local = t0 + tt - base[j];
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            y[e] = 0.f;
+        if (one_seg || local >= 3) { /* every tap inside the segment */
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    y[e] = fmaf(w[e][i], xf[j + i][e], y[e]);
+        } else { /* taps before the segment start: the state's tail or 0 */
+            float tail[3][8];
+#pragma unroll
+            for (int q = 0; q < 3; q++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    tail[q][e] = TAIL ? ct[(sl * 3 + q) * 128 + e * 16 + s] : 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tau = local - 3 + i;
+                const float mx = tau >= 0 ? 1.f : 0.f;
+                const float m0 = tau == -3 ? 1.f : 0.f, m1 = tau == -2 ? 1.f : 0.f,
+                            m2 = tau == -1 ? 1.f : 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float xi = mx * xf[j + i][e];
+                    if constexpr (TAIL)
+                        xi += m0 * tail[0][e] + m1 * tail[1][e] + m2 * tail[2][e];
+                    y[e] = fmaf(w[e][i], xi, y[e]);
+                }
+            }
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            y[e] = silu_f(y[e]);
+            ss += y[e] * y[e];
+        }
+        float inv = 1.f;
+        if (norm) {
+            ss = sum16_dpp(ss);
+            inv = rsqrtf(ss + 1e-6f) * scale;
+        }
+        bf16x8 out;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            out[e] = f2bf(tt < L ? y[e] * inv : 0.f);
+        *(bf16x8 *)&dst[tt][8 * s] = out;
+    }
+}
+
+/* SRC 0: q, k, v, g, beta read from gdn_conv_prep's outputs; 1: computed
+ * here from the pre-conv projection rows (zeros before a segment); 2: the
+ * same with the state's conv tail before each segment. */
+template <int SRC>
 __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
     const bf16 *__restrict__ qh, const bf16 *__restrict__ kh_, const bf16 *__restrict__ vh,
-    const float *__restrict__ g, const float *__restrict__ beta,
+    const float *__restrict__ g, const float *__restrict__ beta, ConvSrc cv,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
     const uint64_t *__restrict__ chunk_starts, int Hk, int Hv,
     bf16 *__restrict__ Wo, bf16 *__restrict__ Qgo, bf16 *__restrict__ QKo,
@@ -272,20 +422,58 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
 
     /* ---- 1. rows and gates ---- */
     {
-        bf16x8 kv[4], qv[4], vv[4];
+        float gv = 0.f, bv = 0.f;
+        if constexpr (SRC == 0) {
+            bf16x8 kv[4], qv[4], vv[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i = tid + 256 * j, t = i >> 4, c8 = (i & 15) * 8;
-            kv[j] = qv[j] = vv[j] = bf16x8{};
-            if (t < L) {
-                kv[j] = ld8(kh_ + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
-                qv[j] = ld8(qh + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
-                vv[j] = ld8(vh + ((size_t)(t0 + t) * Hv + hv) * DV + c8);
+            for (int j = 0; j < 4; j++) {
+                const int i = tid + 256 * j, t = i >> 4, c8 = (i & 15) * 8;
+                kv[j] = qv[j] = vv[j] = bf16x8{};
+                if (t < L) {
+                    kv[j] = ld8(kh_ + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
+                    qv[j] = ld8(qh + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
+                    vv[j] = ld8(vh + ((size_t)(t0 + t) * Hv + hv) * DV + c8);
+                }
             }
+            if (wave == 0 && lane < L) {
+                gv = g[(size_t)(t0 + lane) * Hv + hv];
+                bv = beta[(size_t)(t0 + lane) * Hv + hv];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = tid + 256 * j, t = i >> 4, c8 = (i & 15) * 8;
+                *(bf16x8 *)&sm.K[t][c8] = kv[j];
+                *(bf16x8 *)&sm.Q[t][c8] = qv[j];
+                *(bf16x8 *)&sm.V[t][c8] = vv[j];
+            }
+        } else {
+            constexpr bool TAIL = SRC == 2;
+            const int C = (2 * Hk + Hv) * DK;
+            if (wave == 0 && lane < L) {
+                const bf16 *ab = cv.proj + (size_t)(t0 + lane) * cv.ps + C + Hv * DV; /* b, a */
+                bv = sigmoid_f(bf2f(ab[hv]));
+                gv = cv.A_neg_exp[hv] * softplus_f(bf2f(ab[Hv + hv]) + cv.dt_bias[hv]);
+            }
+            /* all pre-conv rows in flight, then the weights and tail into
+             * LDS (the A/T area is free until step 2) */
+            const int n0 = t0 + 4 * (tid >> 4), s8 = 8 * (tid & 15);
+            bf16x8 xq[7], xk[7], xv[7];
+            conv_rows(cv, slice_c0(0, Hk, hk, hv) + s8, n0, xq);
+            conv_rows(cv, slice_c0(1, Hk, hk, hv) + s8, n0, xk);
+            conv_rows(cv, slice_c0(2, Hk, hk, hv) + s8, n0, xv);
+            int base[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                base[j] = cv.own_base[min(n0 + j, cv.N - 1)];
+            float *cw = &sm.AT[0][0], *ct = cw + 3 * 8 * 16 * 4;
+            conv_stage<TAIL>(cv, Hk, hk, hv, tid, cw, ct);
+            lds_barrier();
+            conv_slice<TAIL>(xq, base, cw, ct, 0, true, 0.08838834764831845f /* 128^-1/2 */, t0,
+                             L, tid, sm.Q);
+            conv_slice<TAIL>(xk, base, cw, ct, 1, true, 1.f, t0, L, tid, sm.K);
+            conv_slice<TAIL>(xv, base, cw, ct, 2, false, 1.f, t0, L, tid, sm.V);
         }
         if (wave == 0) {
-            float gv = lane < L ? g[(size_t)(t0 + lane) * Hv + hv] : 0.f;
-            const float bv = lane < L ? beta[(size_t)(t0 + lane) * Hv + hv] : 0.f;
             /* segments packed into the chunk: st = first token of this
              * lane's segment, en = its last (63 for the chunk's last one) */
             const uint64_t starts = chunk_starts ? chunk_starts[ch] | 1ull : 1ull;
@@ -307,13 +495,6 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
             sm.sKg[lane] = fast_exp(gl - gv);
             sm.sV[lane] = bv;
             Glo[cb * 64 + lane] = gl; /* one copy per lane of phase B's waves */
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i = tid + 256 * j, t = i >> 4, c8 = (i & 15) * 8;
-            *(bf16x8 *)&sm.K[t][c8] = kv[j];
-            *(bf16x8 *)&sm.Q[t][c8] = qv[j];
-            *(bf16x8 *)&sm.V[t][c8] = vv[j];
         }
     }
     lds_barrier();
@@ -970,19 +1151,11 @@ extern "C" hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const
     return hipGetLastError();
 }
 
-extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const float *g,
-                                 const float *beta, const cujev_chunks *ck, const float *S_in,
-                                 float *S_out, const bf16_t *z, int z_stride, const float *norm_w,
-                                 float eps, int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *ws,
-                                 int N, hipStream_t stream) {
-    if (ck->num_chunks <= 0 || N <= 0)
-        return hipSuccess;
-    if (Hk <= 0 || Hv % Hk != 0)
-        return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gdn_chunk_a_kernel, dim3((unsigned)ck->num_chunks, (unsigned)Hv), dim3(256),
-                       0, stream, (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, g, beta,
-                       ck->chunk_tok0, ck->chunk_len, ck->chunk_starts, Hk, Hv, (bf16 *)ws->W,
-                       (bf16 *)ws->Qg, (bf16 *)ws->QK, (bf16 *)ws->KgT, (bf16 *)ws->U, ws->Glast);
+/* Phase B and the gated norm after phase A (either front end). */
+static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *S_out,
+                              const bf16_t *z, int z_stride, const float *norm_w, float eps,
+                              int Hv, bf16_t *y, const cujev_gdn_scratch *ws, int N,
+                              hipStream_t stream) {
     const bool packed = ck->chunk_starts != nullptr;
     if (!S_out && (packed || ck->max_seg_chunks == 1)) {
         /* packed: the units are the chunks, each scanned from S_in */
@@ -1011,4 +1184,50 @@ extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t 
                        (const bf16 *)ws->O, (const bf16 *)z, z_stride, norm_w, eps, rows, Hv,
                        (bf16 *)y);
     return hipGetLastError();
+}
+
+extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const float *g,
+                                 const float *beta, const cujev_chunks *ck, const float *S_in,
+                                 float *S_out, const bf16_t *z, int z_stride, const float *norm_w,
+                                 float eps, int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *ws,
+                                 int N, hipStream_t stream) {
+    if (ck->num_chunks <= 0 || N <= 0)
+        return hipSuccess;
+    if (Hk <= 0 || Hv % Hk != 0 || (ck->chunk_starts && S_out))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gdn_chunk_a_kernel<0>, dim3((unsigned)ck->num_chunks, (unsigned)Hv),
+                       dim3(256), 0, stream, (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, g,
+                       beta, ConvSrc{}, ck->chunk_tok0, ck->chunk_len, ck->chunk_starts, Hk, Hv,
+                       (bf16 *)ws->W, (bf16 *)ws->Qg, (bf16 *)ws->QK, (bf16 *)ws->KgT,
+                       (bf16 *)ws->U, ws->Glast);
+    return gdn_phase_b(ck, S_in, S_out, z, z_stride, norm_w, eps, Hv, y, ws, N, stream);
+}
+
+extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const float *conv_w,
+                                  const float *conv_in, float *conv_out, int seg0_len,
+                                  const int32_t *own_base, const float *A_neg_exp,
+                                  const float *dt_bias, const cujev_chunks *ck, const float *S_in,
+                                  float *S_out, const float *norm_w, float eps, int Hk, int Hv,
+                                  bf16_t *y, const cujev_gdn_scratch *ws, int N,
+                                  hipStream_t stream) {
+    if (N <= 0)
+        return hipSuccess;
+    if (Hk <= 0 || Hv % Hk != 0 || (ck->chunk_starts && S_out) || proj_stride % 8 != 0 ||
+        ((uintptr_t)proj & 15) != 0)
+        return hipErrorInvalidValue;
+    const int C = (2 * Hk + Hv) * DK;
+    if (conv_out)
+        hipLaunchKernelGGL(gdn_conv_tail_kernel, dim3((unsigned)CEIL_DIV(C, 256)), dim3(256), 0,
+                           stream, (const bf16 *)proj, proj_stride, conv_in, conv_out, seg0_len, C);
+    if (ck->num_chunks <= 0)
+        return hipGetLastError();
+    const ConvSrc cv{(const bf16 *)proj, proj_stride, conv_w, conv_in, own_base,
+                     A_neg_exp,          dt_bias,     N};
+    hipLaunchKernelGGL(conv_in ? gdn_chunk_a_kernel<2> : gdn_chunk_a_kernel<1>,
+                       dim3((unsigned)ck->num_chunks, (unsigned)Hv), dim3(256), 0, stream,
+                       (const bf16 *)nullptr, (const bf16 *)nullptr, (const bf16 *)nullptr,
+                       (const float *)nullptr, (const float *)nullptr, cv, ck->chunk_tok0,
+                       ck->chunk_len, ck->chunk_starts, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->Qg,
+                       (bf16 *)ws->QK, (bf16 *)ws->KgT, (bf16 *)ws->U, ws->Glast);
+    return gdn_phase_b(ck, S_in, S_out, proj + C, proj_stride, norm_w, eps, Hv, y, ws, N, stream);
 }

@@ -155,6 +155,18 @@ hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const f
                       int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *scratch, int N,
                       hipStream_t stream);
 
+/* The whole GDN mixer after in_proj: k_gdn_conv_prep's conv + gates computed
+ * inside the scan's first phase (q, k, v never leave the chip), then
+ * k_gdn_scan's recurrence and gated norm with z read from proj at column
+ * C = (2Hk+Hv)*128. Same arguments and results as k_gdn_conv_prep followed by
+ * k_gdn_scan (bit for bit). proj rows must be 16-byte aligned. */
+hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const float *conv_w,
+                       const float *conv_in, float *conv_out, int seg0_len,
+                       const int32_t *own_base, const float *A_neg_exp, const float *dt_bias,
+                       const cujev_chunks *chunks, const float *S_in, float *S_out,
+                       const float *norm_w, float eps, int Hk, int Hv, bf16_t *y,
+                       const cujev_gdn_scratch *scratch, int N, hipStream_t stream);
+
 /* ---- per-layer glue --------------------------------------------------------
  * x[N,H] fp32 residual = E[tokens] (bf16 table).  REF elementwise.cu:3-11. */
 hipError_t k_embed(const int32_t *tokens, const bf16_t *E, float *x, int N, int H, hipStream_t s);

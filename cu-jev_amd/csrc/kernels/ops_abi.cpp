@@ -166,6 +166,31 @@ EXPORT int cujev_op_gdn_conv_prep(const void *proj, int proj_stride, const float
                     "gdn_conv_prep");
 }
 
+EXPORT int cujev_op_gdn_layer(const void *proj, int proj_stride, const float *conv_w,
+                              const float *conv_in, float *conv_out, int seg0_len,
+                              const int32_t *own_base, const float *A_neg_exp,
+                              const float *dt_bias, const int32_t *chunk_tok0,
+                              const int32_t *chunk_len, int num_chunks, const int32_t *seg_chunk0,
+                              const int32_t *seg_nchunk, int num_segments, int max_seg_chunks,
+                              const uint64_t *chunk_starts, const float *S_in, float *S_out,
+                              const float *norm_w, float eps, int Hk, int Hv, int N, void *y,
+                              void *scratch, void *stream) {
+    if (num_chunks < 0 || num_segments < 0 || N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk ||
+        !scratch || (conv_out && (seg0_len < 0 || seg0_len > N)))
+        return fail(1, "gdn_layer: bad arguments");
+    if (proj_stride % 8 || ((uintptr_t)proj & 15))
+        return fail(1, "gdn_layer: projection rows must be 16-byte aligned");
+    if (chunk_starts && S_out)
+        return fail(1, "gdn_layer: packed segments write no final state");
+    cujev_chunks ck = {chunk_tok0, chunk_len,   seg_chunk0,     seg_nchunk,
+                       num_chunks, num_segments, max_seg_chunks, chunk_starts};
+    cujev_gdn_scratch ws = cujev_gdn_scratch_carve(scratch, num_chunks, Hv);
+    return launched(k_gdn_layer((const bf16_t *)proj, proj_stride, conv_w, conv_in, conv_out,
+                                seg0_len, own_base, A_neg_exp, dt_bias, &ck, S_in, S_out, norm_w,
+                                eps, Hk, Hv, (bf16_t *)y, &ws, N, (hipStream_t)stream),
+                    "gdn_layer");
+}
+
 EXPORT size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv, int N) {
     return cujev_gdn_scratch_bytes(num_chunks, Hv, N);
 }

@@ -5,9 +5,11 @@ own for profilers:
     python -m cujev.kernel_bench attention|gdn|gdn_branch|gemm_*|blas_*|copy [iters]
 
 attention  config 3: Hq 16 / Hkv 4, D 256, state 8192 keys, 256 branches x 16
-gdn        config 2: Hk 16 / Hv 32, T = 2048 prefill (conv+gates, scan, norm)
+gdn        config 2: Hk 16 / Hv 32, T = 2048 prefill through the one-call GDN
+           layer (conv+gates inside the scan, norm)
 gdn_branch config 2 branches: 64 branches x 16 tokens continuing one state
-           (S and the conv tail read, nothing written back)
+           (S and the conv tail read, nothing written back), packed chunks
+gdn_split, gdn_branch_split: the same through conv_prep + scan (two calls)
 gemm_<p>    the few-token kernel on projection p (qkv, in, gate_up, down, o) at
            N = 80 with cold weights; blas_<p> the same on hipBLASLt
 copy       a plain device-to-device copy of 256 MiB (scale factor for the
@@ -26,14 +28,15 @@ import sys
 COPY_SCALE = {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0}
 MEASURED_KIB = {
     "attention": {"FETCH_SIZE": 115080.8, "WRITE_SIZE": 32930.9},
-    "gdn": {"FETCH_SIZE": 17519.0 + 36.5 + 16937.6 + 37053.2 + 16398.7,
-            "WRITE_SIZE": 33296.6 + 96.0 + 73984.0 + 18432.0 + 16384.0},
 }
 
 
 def measured_traffic(case):
-    """HBM bytes per launch of a case from the counter figures above."""
-    kib = MEASURED_KIB[case]
+    """HBM bytes per launch of a case from the counter figures above (None
+    while not measured for the kernels of this tree)."""
+    kib = MEASURED_KIB.get(case)
+    if kib is None:
+        return None
     return int(sum(kib[c] * COPY_SCALE[c] for c in kib) * 1024)
 
 
@@ -65,7 +68,7 @@ def attention_case():
     return launch, {"flop": flop}
 
 
-def gdn_case():
+def gdn_case(fused=True):
     import torch
     from . import ops
     ops.load()
@@ -92,6 +95,10 @@ def gdn_case():
     scratch = torch.empty(ops.gdn_scratch_bytes(len(tok0), Hv, T), dtype=torch.uint8, device=dev)
 
     def launch():
+        if fused:
+            ops.gdn_layer(proj, conv_w, None, conv_out, T, own_base, A_neg, dt_bias, tok0, clen,
+                          seg0, segn, None, S_out, norm_w, 1e-6, Hk, Hv, y, scratch)
+            return
         ops.gdn_conv_prep(proj, conv_w, None, conv_out, T, own_base, A_neg, dt_bias, Hk, Hv, q, k,
                           v, gg, beta)
         ops.gdn_scan(q, k, v, gg, beta, tok0, clen, seg0, segn, None, S_out, proj[:, C:],
@@ -103,7 +110,7 @@ def gdn_case():
     return launch, {"bytes": nbytes}
 
 
-def gdn_branch_case(B=64, L=16):
+def gdn_branch_case(B=64, L=16, fused=True):
     import torch
     from . import ops
     ops.load()
@@ -132,6 +139,11 @@ def gdn_branch_case(B=64, L=16):
     scratch = torch.empty(ops.gdn_scratch_bytes(len(tok0), Hv, N), dtype=torch.uint8, device=dev)
 
     def launch():
+        if fused:
+            ops.gdn_layer(proj, conv_w, conv_in, None, N, own_base, A_neg, dt_bias, tok0, clen,
+                          None, None, S_in, None, norm_w, 1e-6, Hk, Hv, y, scratch,
+                          max_seg_chunks=1, chunk_starts=starts)
+            return
         ops.gdn_conv_prep(proj, conv_w, conv_in, None, N, own_base, A_neg, dt_bias, Hk, Hv, q, k,
                           v, gg, beta)
         ops.gdn_scan(q, k, v, gg, beta, tok0, clen, None, None, S_in, None, proj[:, C:],
@@ -219,7 +231,8 @@ def time_launches(launch, iters=20, warmup=3):
 
 
 CASES = {"attention": attention_case, "gdn": gdn_case, "gdn_branch": gdn_branch_case,
-         "copy": copy_case}
+         "gdn_split": lambda: gdn_case(fused=False),
+         "gdn_branch_split": lambda: gdn_branch_case(fused=False), "copy": copy_case}
 for _g in GEMM_SHAPES:
     CASES["gemm_" + _g] = lambda _g=_g: gemm_case(_g, small=True)
     CASES["blas_" + _g] = lambda _g=_g: gemm_case(_g, small=False)

@@ -37,6 +37,8 @@ _SIGS = {
     "cujev_op_gemm_small": [_P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _P],
     "cujev_op_gemm_small_tile": [_P, _I, _I, _P, _P],
     "cujev_op_add_rmsnorm": [_P, _P, _P, _I, _P, _P, _I, _I, _F, _P, _I, _P],
+    "cujev_op_gdn_layer": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P,
+                           _P, _P, _F, _I, _I, _I, _P, _P, _P],
     "cujev_op_gdn_scan": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P,
                           _F, _I, _I, _I, _P, _P, _P],
 }
@@ -195,6 +197,20 @@ def gdn_scan(q, k, v, g, beta, chunk_tok0, chunk_len, seg_chunk0, seg_nchunk, S_
           nseg, int(max_seg_chunks), _ptr(chunk_starts), _ptr(S_in), _ptr(S_out), _ptr(z),
           int(z_stride), _ptr(norm_w), float(eps), Hk, Hv, q.shape[0], _ptr(y), _ptr(scratch),
           _stream())
+
+
+def gdn_layer(proj, conv_w, conv_in, conv_out, seg0_len, own_base, A_neg_exp, dt_bias,
+              chunk_tok0, chunk_len, seg_chunk0, seg_nchunk, S_in, S_out, norm_w, eps, Hk, Hv, y,
+              scratch, max_seg_chunks=0, chunk_starts=None):
+    """gdn_conv_prep + gdn_scan in one call (z from proj's columns after the
+    conv channels); q, k, v, g, beta stay on chip."""
+    N = proj.shape[0]
+    nseg = seg_chunk0.shape[0] if seg_chunk0 is not None else 0
+    _call("cujev_op_gdn_layer", _ptr(proj), proj.stride(0), _ptr(conv_w), _ptr(conv_in),
+          _ptr(conv_out), int(seg0_len), _ptr(own_base), _ptr(A_neg_exp), _ptr(dt_bias),
+          _ptr(chunk_tok0), _ptr(chunk_len), chunk_tok0.shape[0], _ptr(seg_chunk0),
+          _ptr(seg_nchunk), nseg, int(max_seg_chunks), _ptr(chunk_starts), _ptr(S_in),
+          _ptr(S_out), _ptr(norm_w), float(eps), Hk, Hv, N, _ptr(y), _ptr(scratch), _stream())
 
 
 _gemm_ws = None

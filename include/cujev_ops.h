@@ -145,6 +145,22 @@ int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const float *
                       int z_stride, const float *norm_w, float eps, int Hk, int Hv, int N,
                       void *y, void *scratch, void *stream);
 
+/* Replaces reference src/kernels/kernels.h:214-215 (k_gdn_conv), :221-223
+ * (k_gdn_prep), :228-230 (k_gdn_scan) and :233-234 (k_gdn_norm_gate): the
+ * GDN mixer from the in_proj rows to the gated-norm output in one call.
+ * Arguments as cujev_op_gdn_conv_prep followed by cujev_op_gdn_scan (z is
+ * read from proj at column C = (2Hk+Hv)*128); the result is bit-identical to
+ * that pair, but q, k, v, g and beta are never written out. proj rows must be
+ * 16-byte aligned (proj_stride % 8 == 0). */
+int cujev_op_gdn_layer(const void *proj, int proj_stride, const float *conv_w,
+                       const float *conv_in, float *conv_out, int seg0_len,
+                       const int32_t *own_base, const float *A_neg_exp, const float *dt_bias,
+                       const int32_t *chunk_tok0, const int32_t *chunk_len, int num_chunks,
+                       const int32_t *seg_chunk0, const int32_t *seg_nchunk, int num_segments,
+                       int max_seg_chunks, const uint64_t *chunk_starts, const float *S_in,
+                       float *S_out, const float *norm_w, float eps, int Hk, int Hv, int N,
+                       void *y, void *scratch, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

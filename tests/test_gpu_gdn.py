@@ -64,11 +64,12 @@ def oracle_segment(L, proj, tail, S0):
 
 
 def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False, tell_max=True,
-            pack=False):
+            pack=False, fused=False):
     """tell_max: pass the chunk table's largest per-segment chunk count (lets
     one-chunk branches take the branch path); False passes 0 (general path).
     pack: whole segments packed into shared chunks (branches of <= 64 tokens
-    continuing S_in)."""
+    continuing S_in). fused: the one-call layer entry (conv inside the scan)
+    instead of conv_prep + scan."""
     dev = "cuda"
     N = proj.shape[0]
     pd = bf(proj).to(dev)
@@ -92,7 +93,16 @@ def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False, te
     sout = torch.zeros(L.Hv, DK, DV, dtype=torch.float32, device=dev) if write_state else None
     y = torch.empty(N, L.Hv * DV, dtype=torch.bfloat16, device=dev)
     msc = int(np.max(segn)) if tell_max and len(segn) else 0
-    if pack:
+    if fused:  # conv + gates inside the scan's first phase
+        del q, k, v, g, beta
+        cout2 = torch.zeros(L.C, 3, dtype=torch.float32, device=dev) if write_state else None
+        o.gdn_layer(pd, t(L.conv_w), cin, cout2, seg_lens[0], t(own_base), t(L.A_neg),
+                    t(L.dt_bias), t(tok0), t(clen), None if pack else t(seg0),
+                    None if pack else t(segn), sin, sout, t(L.norm_w), L.eps, L.Hk, L.Hv, y,
+                    scratch, max_seg_chunks=1 if pack else msc,
+                    chunk_starts=t(starts) if pack else None)
+        cout = cout2
+    elif pack:
         o.gdn_scan(q, k, v, g, beta, t(tok0), t(clen), None, None, sin, sout, pd[:, L.C:],
                    pd.stride(0), t(L.norm_w), L.eps, L.Hk, L.Hv, y, scratch, max_seg_chunks=1,
                    chunk_starts=t(starts))
@@ -191,6 +201,31 @@ def test_gdn_packed_branches(seg_lens):
         e = rel_err(got["y"][start: start + Ls], y_ref)
         assert e <= TOL, (Ls, e)
         start += Ls
+
+
+@pytest.mark.parametrize("case", ["prefill", "branches", "one_chunk", "packed"])
+def test_gdn_layer_equals_conv_then_scan(case):
+    """The fused layer call (conv + gates computed inside phase A) gives the
+    output, final state and conv tail of conv_prep followed by the scan, bit
+    for bit, on every path: prefill with state written, multi-chunk branches,
+    one-chunk branches, packed branches."""
+    o = ops()
+    print(f"fused layer case={case}", flush=True)
+    L = Layer(13, 2, 4)
+    prefix = L.proj(137)
+    ref_p = run_gpu(o, L, prefix, [137], write_state=True)
+    got_p = run_gpu(o, L, prefix, [137], write_state=True, fused=True)
+    if case == "prefill":
+        for key in ("y", "S", "tail"):
+            np.testing.assert_array_equal(got_p[key], ref_p[key])
+        return
+    seg_lens = {"branches": [1, 3, 64, 65, 130, 7], "one_chunk": [1, 2, 16, 33, 64, 20],
+                "packed": [5, 16, 16, 43, 64, 1, 20, 20]}[case]
+    br = L.proj(sum(seg_lens))
+    kw = dict(conv_in=ref_p["tail"], S_in=ref_p["S"], pack=case == "packed")
+    ref = run_gpu(o, L, br, seg_lens, **kw)
+    got = run_gpu(o, L, br, seg_lens, fused=True, **kw)
+    np.testing.assert_array_equal(got["y"], ref["y"])
 
 
 def test_gdn_capacity_shape():
