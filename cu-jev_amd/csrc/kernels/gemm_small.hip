@@ -12,7 +12,7 @@
  *  - W comes pre-tiled (k_gemm_small_tile, once per weight): the 16 rows x
  *    128 k of one wave and chunk are one contiguous 4 KiB block laid out in
  *    the order the wave's four 16-byte loads consume it, so every load
- *    instruction reads 1 KiB of consecutive bytes. Streaming the plain
+ *    instruction reads 1 KiB of consecutive bytes; blocks are chunk-major. Streaming the plain
  *    [M][K] rows (16 rows x 64 bytes per instruction) runs at two thirds of
  *    that rate.
  *  - X (tiny, L2-resident) goes to an LDS ring by buffer DMA, the same three
@@ -99,11 +99,13 @@ __global__ __launch_bounds__(SG_THREADS, 2) void gemm_small_kernel(const bf16 *_
     const int wr0 = GATED ? blockIdx.x * 32 + 16 * (wave & 1) + (wave >> 1) * (M / 2)
                           : blockIdx.x * SG_BM + 16 * wave;
 
-    /* tiled W: block (row group wr0/16, chunk) of 2048 elements; load i of
-     * lane l is elements 512 i + 8 l .. +7 of the block */
-    const bf16 *wblk = W + ((size_t)(wr0 >> 4) * (K / SG_KC) + kb / SG_KC) * 2048 + lane * 8;
+    /* tiled W: block (chunk, row group wr0/16) of 2048 elements, chunk-major
+     * (G = M/16 row groups per chunk); load i of lane l is elements 512 i +
+     * 8 l .. +7 of the block */
+    const size_t G = (size_t)(M >> 4);
+    const bf16 *wblk = W + ((size_t)(kb / SG_KC) * G + (wr0 >> 4)) * 2048 + lane * 8;
     auto load_w = [&](int c, bf16x8 (&wf)[4]) {
-        const bf16 *p = wblk + (size_t)2048 * min(c, nch - 1);
+        const bf16 *p = wblk + (size_t)2048 * G * min(c, nch - 1);
 #pragma unroll
         for (int i = 0; i < 4; i++)
             wf[i] = ldg8(p + 512 * i);
@@ -235,8 +237,10 @@ __global__ __launch_bounds__(SG_THREADS, 2) void gemm_small_kernel(const bf16 *_
     }
 }
 
-/* W [M][K] -> the tiled layout the kernel streams: block b = (g, c), g = row
- * group of 16, c = 128-wide K chunk, at b = g (K/128) + c; element 512 i +
+/* W [M][K] -> the tiled layout the kernel streams: block b = (c, g), g = row
+ * group of 16, c = 128-wide K chunk, at b = c (M/16) + g (chunk-major: the
+ * workgroups, which move through K together, read one contiguous region at a
+ * time); element 512 i +
  * 8 l + e of the block is W[16 g + l%16][128 c + 64 (i/2) + 16 (l/16) +
  * 8 (i%2) + e] (the A operand of lane l = row l%16, k 16 (l/16) + 8 hf.., for
  * the two MFMAs of k step 64 j, i = 2 j + hf). One thread per 16 bytes. */
@@ -248,8 +252,8 @@ __global__ __launch_bounds__(256) void gemm_small_tile_kernel(const bf16 *__rest
         return;
     const int l = (int)(piece & 63), i = (int)((piece >> 6) & 3);
     const size_t b = piece >> 8;
-    const int nchunk = K / SG_KC;
-    const int g = (int)(b / nchunk), c = (int)(b % nchunk);
+    const int G = M / 16;
+    const int g = (int)(b % G), c = (int)(b / G);
     const int row = 16 * g + (l & 15);
     const int k = SG_KC * c + 64 * (i >> 1) + 16 * (l >> 4) + 8 * (i & 1);
     *(bf16x8 *)(Wt + piece * 8) = ldg8(W + (size_t)row * K + k);

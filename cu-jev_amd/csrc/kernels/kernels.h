@@ -205,7 +205,8 @@ int cujev_gemm_small_splits(int M, int K); /* suggested split count (<= MAX_SPLI
 hipError_t k_gemm_small(const bf16_t *X, int ldx, const bf16_t *W, int N, int M, int K, int gated,
                         int splits, bf16_t *Y, int ldy, float *P, hipStream_t stream);
 /* W [M, K] (M % 16 == 0, K % 128 == 0) -> Wt, the tiled copy k_gemm_small
- * streams: one contiguous 4 KiB block per 16 rows x 128 k. */
+ * streams: one contiguous 4 KiB block per 16 rows x 128 k, block number
+ * chunk * (M/16) + row group. */
 hipError_t k_gemm_small_tile(const bf16_t *W, int M, int K, bf16_t *Wt, hipStream_t stream);
 
 /* ---- projection GEMMs (hipBLASLt) ------------------------------------------

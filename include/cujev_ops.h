@@ -63,7 +63,8 @@ int cujev_op_gemm_small(const void *X, int ldx, const void *W, int N, int M, int
                         int splits, void *Y, int ldy, float *P, void *stream);
 /* The weight layout cujev_op_gemm_small reads: Wt (M*K bf16, distinct from W)
  * receives W [M][K] (M % 16 == 0, K % 128 == 0) as one contiguous 4 KiB
- * block per 16 rows x 128 k, in the order the kernel's loads consume it.
+ * block per 16 rows x 128 k, in the order the kernel's loads consume it;
+ * the block of row group g and 128-wide K chunk c is number c * (M/16) + g.
  * Run once per weight; no counterpart in the reference, whose cuBLAS calls
  * read the plain rows. */
 int cujev_op_gemm_small_tile(const void *W, int M, int K, void *Wt, void *stream);

@@ -108,12 +108,12 @@ def test_split_partials_feed_add_rmsnorm(N, H, K):
 
 
 def tile_reference(W):
-    """The tiled layout restated with tensor indexing: block (g, c) of 16 rows x
-    128 k, element 512 i + 8 l + e = W[16 g + l%16][128 c + 64 (i//2) +
-    16 (l//16) + 8 (i%2) + e]."""
+    """The tiled layout restated with tensor indexing: blocks of 16 rows x 128
+    k in chunk-major order (block c * M/16 + g), element 512 i + 8 l + e =
+    W[16 g + l%16][128 c + 64 (i//2) + 16 (l//16) + 8 (i%2) + e]."""
     M, K = W.shape
     t = W.reshape(M // 16, 16, K // 128, 2, 4, 2, 8)   # g, r, c, j, q, hf, e
-    t = t.permute(0, 2, 3, 5, 4, 1, 6)                  # g, c, j, hf, q, r, e
+    t = t.permute(2, 0, 3, 5, 4, 1, 6)                  # c, g, j, hf, q, r, e
     return t.reshape(M, K)
 
 
