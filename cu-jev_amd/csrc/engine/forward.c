@@ -183,13 +183,12 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
  * graph and every later one replays it. Graph nodes are kernels only (no
  * memset nodes). At most CUJEV_GRAPH_SLOTS shapes are kept (least recently
  * used goes first); a state's graphs are dropped with the state. */
-static int gdn_packing_enabled(void) {
-    static int cached = -1;
-    if (cached < 0) {
-        const char *e = getenv("CUJEV_GDN_PACK");
-        cached = !(e && *e == '0');
-    }
-    return cached;
+/* Pack eval branches into shared chunks when B * Hv exceeds this many
+ * (segment, head) units; CUJEV_GDN_PACK_MIN_UNITS overrides it (read on every
+ * forward; negative = never pack). */
+static int gdn_pack_min_units(void) {
+    const char *e = getenv("CUJEV_GDN_PACK_MIN_UNITS");
+    return e && *e ? atoi(e) : 512;
 }
 
 static int graphs_enabled(void) {
@@ -300,9 +299,13 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
     /* Eval branches that each fit a 64-token chunk: consecutive whole
      * segments share a chunk (they all continue the stored state and write
      * none back), so a scan chunk holds up to 64 tokens however short the
-     * branches are. npk = packed chunks, 0 when not packing. */
+     * branches are. Only when the branches already give the scan more
+     * (segment, head) units than about two workgroups per CU: below that,
+     * packing would only lengthen each workgroup's serial chain. npk =
+     * packed chunks, 0 when not packing. */
     int npk = 0;
-    if (mode == CUJEV_FWD_EVAL && gdn_packing_enabled()) {
+    const int pack_min = gdn_pack_min_units();
+    if (mode == CUJEV_FWD_EVAL && pack_min >= 0 && B * m->Hv > pack_min) {
         int fill = 64, end = -1;
         for (int b = 0; b < B; b++) {
             if (seg_len[b] > 64) {

@@ -101,7 +101,11 @@ def test_lengths_match_oracle(engine, oracle, plen, slen):
     check_probs(lg, ref, f"P={plen} L={slen}", ref64)
 
 
-def test_many_branches_packed(engine, oracle):
+@pytest.mark.parametrize("pack_min", ["0", "-1"])
+def test_many_branches_packed(engine, oracle, monkeypatch, pack_min):
+    """40 short branches, with their GDN chunks packed several branches to a
+    chunk (threshold 0) and one branch per chunk (packing off)."""
+    monkeypatch.setenv("CUJEV_GDN_PACK_MIN_UNITS", pack_min)
     cfg, W = oracle
     rng = np.random.default_rng(7)
     prefix = rand_ids(rng, 50)
