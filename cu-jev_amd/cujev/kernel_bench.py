@@ -28,6 +28,9 @@ import sys
 COPY_SCALE = {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0}
 MEASURED_KIB = {
     "attention": {"FETCH_SIZE": 115080.8, "WRITE_SIZE": 32930.9},
+    "gdn": {"FETCH_SIZE": 36.7 + 18148.3 + 37049.2 + 16398.7,
+            "WRITE_SIZE": 96.0 + 73984.0 + 18432.0 + 16384.0},
+    "gdn_branch": {"FETCH_SIZE": 9842.7 + 26690.0, "WRITE_SIZE": 36992.0 + 8192.0},
 }
 
 
