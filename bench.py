@@ -139,17 +139,24 @@ def run_e2e_in_child(ckpt, steps, warmup):
 # --------------------------------------------------------------------------
 # kernel rooflines (operator C ABI, HIP events on the launch stream)
 # --------------------------------------------------------------------------
-def attention_roofline(iters=20):
+# The first ~25 launches of a kernel in a fresh process run while the GPU's
+# clocks ramp up (the first attention launch takes over 1 ms, later ones
+# 484-490 us): the kernel cases warm up for ROOF_WARMUP launches and then time
+# ROOF_ITERS, the steady state.
+ROOF_WARMUP, ROOF_ITERS = 40, 50
+
+
+def attention_roofline(iters=ROOF_ITERS, warmup=ROOF_WARMUP):
     from cujev import kernel_bench
     launch, info = kernel_bench.attention_case()
-    us = kernel_bench.time_launches(launch, iters)
+    us = kernel_bench.time_launches(launch, iters, warmup)
     return dict(us=us, flop=info["flop"], tflops=info["flop"] / (us * 1e-6) / 1e12)
 
 
-def gdn_roofline(iters=20, case="gdn"):
+def gdn_roofline(iters=ROOF_ITERS, case="gdn", warmup=ROOF_WARMUP):
     from cujev import kernel_bench
     launch, info = kernel_bench.CASES[case]()
-    us = kernel_bench.time_launches(launch, iters)
+    us = kernel_bench.time_launches(launch, iters, warmup)
     return dict(us=us, bytes=info["bytes"], gbs=info["bytes"] / (us * 1e-6) / 1e9)
 
 
@@ -214,6 +221,45 @@ def cpu_baseline(ckpt, req, eng_out, eng_full):
     return base, parity
 
 
+def kernel_rooflines():
+    """The kernel roofline entries of the JSON line (attention, GDN prefill,
+    GDN branches), each timed in its steady state."""
+    res = {}
+    from cujev import kernel_bench
+    att = attention_roofline()
+    log(f"attention config 3: {att['us']:.1f} us, {att['tflops']:.1f} TFLOP/s")
+    res["roofline"] = {"kernel": "attention_kernel (ops library), config 3",
+                       "bound": "mfma", "achieved": round(att["tflops"], 2),
+                       "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                       "frac": round(att["tflops"] / PEAK_BF16_TFLOPS, 4),
+                       "traffic": kernel_bench.measured_traffic("attention"),
+                       "traffic_source": "rocprofv3 --pmc FETCH_SIZE x2 + WRITE_SIZE x1 "
+                                         "(copy-calibrated), bytes per launch",
+                       "us_per_launch": round(att["us"], 2),
+                       "flop_per_launch": att["flop"]}
+    gdn = gdn_roofline()
+    log(f"gdn config 2 prefill: {gdn['us']:.1f} us, {gdn['gbs']:.1f} GB/s")
+    res["gdn_roofline"] = {"kernel": "gdn layer call: conv_tail + chunk_a (conv and gates "
+                                     "inside) + chunk_b + norm_gate, config 2 T=2048 "
+                                     "prefill", "bound": "hbm",
+                           "achieved": round(gdn["gbs"], 1), "peak": PEAK_HBM_GBS,
+                           "unit": "GB/s", "frac": round(gdn["gbs"] / PEAK_HBM_GBS, 4),
+                           "us_per_layer": round(gdn["us"], 2),
+                           "compulsory_bytes": gdn["bytes"],
+                           "traffic": kernel_bench.measured_traffic("gdn")}
+    gbr = gdn_roofline(case="gdn_branch")
+    log(f"gdn config 2 branches: {gbr['us']:.1f} us, {gbr['gbs']:.1f} GB/s")
+    res["gdn_branch_roofline"] = {"kernel": "gdn layer call: chunk_a (conv and gates inside, "
+                                            "packed chunks) + short_b (norm inside), config "
+                                            "2, 64 branches x 16 tokens", "bound": "hbm",
+                                  "achieved": round(gbr["gbs"], 1), "peak": PEAK_HBM_GBS,
+                                  "unit": "GB/s", "frac": round(gbr["gbs"] / PEAK_HBM_GBS, 4),
+                                  "us_per_layer": round(gbr["us"], 2),
+                                  "compulsory_bytes": gbr["bytes"],
+                                  "traffic": kernel_bench.measured_traffic("gdn_branch")}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -222,6 +268,8 @@ def main():
     ap.add_argument("--ckpt", default=os.environ.get("CUJEV_BENCH_CKPT", "/tmp/cujev_synth_4b"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the kernel roofline entries (no request loop, no CPU baseline)")
     ap.add_argument("--e2e-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--full-out", help=argparse.SUPPRESS)
     a = ap.parse_args()
@@ -236,6 +284,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if a.kernels_only:
+        print(json.dumps(kernel_rooflines()), flush=True)
+        return
     from cujev import synthetic
     t0 = time.perf_counter()
     ckpt = synthetic.ensure_checkpoint(a.ckpt, "4b", seed=0, device="cuda")
@@ -271,38 +322,7 @@ def main():
                    "vocab": 248320, "weights_gib": round(e2e["info"]["weight_gib"], 2)},
     }
     if not a.no_kernels:
-        from cujev import kernel_bench
-        att = attention_roofline()
-        log(f"attention config 3: {att['us']:.1f} us, {att['tflops']:.1f} TFLOP/s")
-        res["roofline"] = {"kernel": "attention_kernel (ops library), config 3",
-                           "bound": "mfma", "achieved": round(att["tflops"], 2),
-                           "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                           "frac": round(att["tflops"] / PEAK_BF16_TFLOPS, 4),
-                           "traffic": kernel_bench.measured_traffic("attention"),
-                           "traffic_source": "rocprofv3 --pmc FETCH_SIZE x2 + WRITE_SIZE x1 "
-                                             "(copy-calibrated), bytes per launch",
-                           "us_per_launch": round(att["us"], 2),
-                           "flop_per_launch": att["flop"]}
-        gdn = gdn_roofline()
-        log(f"gdn config 2 prefill: {gdn['us']:.1f} us, {gdn['gbs']:.1f} GB/s")
-        res["gdn_roofline"] = {"kernel": "gdn layer call: conv_tail + chunk_a (conv and gates "
-                                         "inside) + chunk_b + norm_gate, config 2 T=2048 "
-                                         "prefill", "bound": "hbm",
-                               "achieved": round(gdn["gbs"], 1), "peak": PEAK_HBM_GBS,
-                               "unit": "GB/s", "frac": round(gdn["gbs"] / PEAK_HBM_GBS, 4),
-                               "us_per_layer": round(gdn["us"], 2),
-                               "compulsory_bytes": gdn["bytes"],
-                               "traffic": kernel_bench.measured_traffic("gdn")}
-        gbr = gdn_roofline(case="gdn_branch")
-        log(f"gdn config 2 branches: {gbr['us']:.1f} us, {gbr['gbs']:.1f} GB/s")
-        res["gdn_branch_roofline"] = {"kernel": "gdn layer call: chunk_a (conv and gates inside, "
-                                                "packed chunks) + short_b (norm inside), config "
-                                                "2, 64 branches x 16 tokens", "bound": "hbm",
-                                      "achieved": round(gbr["gbs"], 1), "peak": PEAK_HBM_GBS,
-                                      "unit": "GB/s", "frac": round(gbr["gbs"] / PEAK_HBM_GBS, 4),
-                                      "us_per_layer": round(gbr["us"], 2),
-                                      "compulsory_bytes": gbr["bytes"],
-                                      "traffic": kernel_bench.measured_traffic("gdn_branch")}
+        res.update(kernel_rooflines())
     if not a.no_cpu_baseline:
         torch.cuda.empty_cache()
         base, parity = cpu_baseline(ckpt, e2e["first_req"], e2e["first_out"], e2e["first_full"])

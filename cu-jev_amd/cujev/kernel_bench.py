@@ -2,7 +2,7 @@
 bench.py (timed with HIP events on the launch stream) and runnable on their
 own for profilers:
 
-    python -m cujev.kernel_bench attention|gdn|gdn_branch|gemm_*|blas_*|copy [iters]
+    python -m cujev.kernel_bench attention|gdn|gdn_branch|gemm_*|blas_*|copy [iters [warmup]]
 
 attention  config 3: Hq 16 / Hkv 4, D 256, state 8192 keys, 256 branches x 16
 gdn        config 2: Hk 16 / Hv 32, T = 2048 prefill through the one-call GDN
@@ -243,7 +243,8 @@ for _g in GEMM_SHAPES:
 if __name__ == "__main__":
     name = sys.argv[1]
     iters = int(sys.argv[2]) if len(sys.argv) > 2 else 20
+    warmup = int(sys.argv[3]) if len(sys.argv) > 3 else 3
     launch, info = CASES[name]()
-    us = time_launches(launch, iters)
+    us = time_launches(launch, iters, warmup)
     tbs = f", {info['bytes'] / us / 1e6:.2f} TB/s" if "bytes" in info else ""
     print(f"{name}: {us:.1f} us per launch{tbs} {info}", flush=True)
