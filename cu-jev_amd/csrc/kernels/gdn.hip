@@ -315,8 +315,8 @@ DEV float sum16_dpp(float v) {
 
 template <bool TAIL>
 DEV void conv_slice(const bf16x8 (&x)[7], const int (&base)[4], const float *cw, const float *ct,
-                    int sl, bool norm, float scale, int t0, int L, int tid, bf16 (*dst)[DK + 8]) {
-    const int s = tid & 15, tb = tid >> 4;
+                    int sl, bool norm, float scale, int t0, int L, int tb, int s,
+                    bf16 (*dst)[DK + 8]) {
     float w[8][4];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
@@ -454,24 +454,47 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
                 bv = sigmoid_f(bf2f(ab[hv]));
                 gv = cv.A_neg_exp[hv] * softplus_f(bf2f(ab[Hv + hv]) + cv.dt_bias[hv]);
             }
-            /* all pre-conv rows in flight, then the weights and tail into
-             * LDS (the A/T area is free until step 2) */
-            const int n0 = t0 + 4 * (tid >> 4), s8 = 8 * (tid & 15);
-            bf16x8 xq[7], xk[7], xv[7];
-            conv_rows(cv, slice_c0(0, Hk, hk, hv) + s8, n0, xq);
-            conv_rows(cv, slice_c0(1, Hk, hk, hv) + s8, n0, xk);
-            conv_rows(cv, slice_c0(2, Hk, hk, hv) + s8, n0, xv);
-            int base[4];
+            /* (slice, 4-token block) tasks over the 16-lane groups: only
+             * blocks holding tokens are computed, so a short chunk spreads
+             * its few tasks over all groups (64 tokens: one block, three
+             * slices per group). All pre-conv rows go in flight first, then
+             * the weights and tail into LDS (the A/T area is free until
+             * step 2). */
+            const int nblk = (L + 3) >> 2, ntask = 3 * nblk;
+            const int grp = tid >> 4, s16 = tid & 15;
+            bf16x8 xr[3][7];
+            int base[3][4];
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                base[j] = cv.own_base[min(n0 + j, cv.N - 1)];
+            for (int r = 0; r < 3; r++) {
+                const int t = grp + 16 * r;
+                if (t < ntask) {
+                    const int sl = t / nblk, n0 = t0 + 4 * (t - sl * nblk);
+                    conv_rows(cv, slice_c0(sl, Hk, hk, hv) + 8 * s16, n0, xr[r]);
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        base[r][j] = cv.own_base[min(n0 + j, cv.N - 1)];
+                }
+            }
             float *cw = &sm.AT[0][0], *ct = cw + 3 * 8 * 16 * 4;
             conv_stage<TAIL>(cv, Hk, hk, hv, tid, cw, ct);
+            /* rows of token blocks without tokens: zeros */
+            const int zrows = CH - 4 * nblk;
+            for (int i = tid; i < 3 * zrows * 16; i += 256) {
+                const int a = i / (zrows * 16), rem = i - a * zrows * 16;
+                bf16(*z)[DK + 8] = a == 0 ? sm.Q : a == 1 ? sm.K : sm.V;
+                *(bf16x8 *)&z[4 * nblk + (rem >> 4)][8 * (rem & 15)] = bf16x8{};
+            }
             lds_barrier();
-            conv_slice<TAIL>(xq, base, cw, ct, 0, true, 0.08838834764831845f /* 128^-1/2 */, t0,
-                             L, tid, sm.Q);
-            conv_slice<TAIL>(xk, base, cw, ct, 1, true, 1.f, t0, L, tid, sm.K);
-            conv_slice<TAIL>(xv, base, cw, ct, 2, false, 1.f, t0, L, tid, sm.V);
+#pragma unroll
+            for (int r = 0; r < 3; r++) {
+                const int t = grp + 16 * r;
+                if (t < ntask) {
+                    const int sl = t / nblk, tb = t - sl * nblk;
+                    conv_slice<TAIL>(xr[r], base[r], cw, ct, sl, sl < 2,
+                                     sl == 0 ? 0.08838834764831845f /* 128^-1/2 */ : 1.f, t0, L,
+                                     tb, s16, sl == 0 ? sm.Q : sl == 1 ? sm.K : sm.V);
+                }
+            }
         }
         if (wave == 0) {
             /* segments packed into the chunk: st = first token of this
