@@ -439,7 +439,10 @@ __global__ __launch_bounds__(256) void attention_kernel(
  * 256-wide row per step, lane l holding dims 4l..4l+3; RoPE pairs dim i with
  * i + rot/2, i.e. lane l with lane l ^ (rot/8). cos/sin come from a table
  * rope[pos][rot/2] of (cos, sin) pairs built once on the host. */
-constexpr int PREP_TOK = 16;
+/* Tokens per prep workgroup: each wave walks its tokens one after another
+ * (a 256-wide reduction and a RoPE exchange per token), so the per-token chain,
+ * not the data, sets the time; 4 tokens keep it short and the grid wide. */
+constexpr int PREP_TOK = 4;
 
 __global__ __launch_bounds__(320) void attn_prep_kernel(
     const bf16 *__restrict__ proj, int ps, const float *__restrict__ qw, const float *__restrict__ kw,
@@ -533,7 +536,8 @@ __global__ __launch_bounds__(320) void attn_prep_kernel(
         }
     }
 
-    /* V: [16 tokens][256] -> LDS [256][16] -> 256 vt rows of 16 columns */
+    /* V: [PREP_TOK tokens][256] -> LDS [256][PREP_TOK] -> 256 vt rows of
+     * PREP_TOK columns */
 #pragma unroll
     for (int k = 0; k < 2; k++) {
         const int idx = threadIdx.x + 320 * k;
@@ -545,14 +549,17 @@ __global__ __launch_bounds__(320) void attn_prep_kernel(
         }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < 256 * 2; idx += 320) {
-        const int d = idx >> 1, c = idx & 1;
-        bf16 *dst = vtc + ((size_t)kh * 256 + d) * cs + n0 + 8 * c;
-        if (8 * c + 8 <= nt) {
-            *(bf16x8 *)dst = *(const bf16x8 *)&vs[d][8 * c];
+    constexpr int VP = PREP_TOK < 8 ? PREP_TOK : 8; /* tokens per vt store */
+    constexpr int NPC = PREP_TOK / VP;
+    typedef __bf16 bf16xVP __attribute__((ext_vector_type(VP)));
+    for (int idx = threadIdx.x; idx < 256 * NPC; idx += 320) {
+        const int d = idx / NPC, c = idx % NPC;
+        bf16 *dst = vtc + ((size_t)kh * 256 + d) * cs + n0 + VP * c;
+        if (VP * c + VP <= nt) {
+            *(bf16xVP *)dst = *(const bf16xVP *)&vs[d][VP * c];
         } else {
-            for (int e = 0; e < 8 && 8 * c + e < nt; e++)
-                dst[e] = vs[d][8 * c + e];
+            for (int e = 0; e < VP && VP * c + e < nt; e++)
+                dst[e] = vs[d][VP * c + e];
         }
     }
 }
