@@ -130,7 +130,7 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
                   "attn_prep", l);
             K_TRY(k_attention(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l], st->kv_vt[l],
                               P, m->state_stride, kdst, vdst, kstride, a->base, N, m->Hq,
-                              m->Hkv, m->mix_out, s),
+                              m->Hkv, m->mix_out, m->attn_ws, m->attn_ws_bytes, s),
                   "attention", l);
             K_TRY(resid_gemm(m, m->mix_out, ly->w_o, ly->wt_o, N, H, m->Hq * m->D, &ry, &ryp,
                              &rsp),

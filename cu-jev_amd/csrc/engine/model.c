@@ -299,6 +299,10 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
     m->max_chunks = m->max_tokens / 64 + (int)B + 1;
     m->meta_ints = 3 * N + 3 * B + 4 * (size_t)m->max_chunks + B * (size_t)m->opts.max_candidates + B;
     m->gemm_ws_bytes = (size_t)64 << 20;
+    {
+        const int an = m->max_tokens < CUJEV_ATTN_SPLIT_MAX_N ? m->max_tokens : CUJEV_ATTN_SPLIT_MAX_N;
+        m->attn_ws_bytes = cujev_attention_ws_bytes(an, m->Hq, CUJEV_ATTN_MAX_SPLITS);
+    }
     struct {
         void **p;
         size_t bytes;
@@ -308,6 +312,7 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
         {(void **)&m->proj, N * (size_t)m->w_proj * 2},
         {(void **)&m->y, N * H * 2},
         {(void **)&m->ypart, (size_t)CUJEV_GEMM_SMALL_MAX_SPLITS * CUJEV_GEMM_SMALL_MAX_N * H * 4},
+        {&m->attn_ws, m->attn_ws_bytes},
         {(void **)&m->q, N * (size_t)m->Hq * m->D * 2},
         {(void **)&m->mix_out, mix * 2},
         {(void **)&m->br_k, br_kv},

@@ -82,6 +82,8 @@ struct cujev_model {
     bf16_t *proj;    /* [N, w_proj] */
     bf16_t *y;       /* [N,H] */
     float *ypart;    /* [CUJEV_GEMM_SMALL_MAX_SPLITS][CUJEV_GEMM_SMALL_MAX_N][H]: split-K partials of the few-token GEMMs */
+    void *attn_ws;   /* key-split partials of the attention for few-token evals */
+    size_t attn_ws_bytes;
     bf16_t *q;       /* [N,Hq,256] prescaled */
     bf16_t *mix_out; /* [N, max(Hq*256, V)] */
     bf16_t *br_k, *br_vt;

@@ -139,11 +139,22 @@ DEV void wait_lgkm(int n) { /* n is a constant once the loops are unrolled */
  * Per key tile i the loop overlaps, in each wave, the S^T MFMAs of tile i+1
  * with the softmax of tile i, then runs the PV MFMAs of tile i, while the
  * V^T of tile i+1 and the K of tile i+2 stream into the idle buffers. */
+/* Key-split partials (SPLIT): split s of a (token, q-head) row keeps the
+ * unnormalised o[256], l and the shift mu of its share of the key tiles. */
+struct AttnPart {
+    float *o;  /* [nsplit][N][Hq][256] */
+    float *l;  /* [nsplit][N][Hq]      */
+    float *mu; /* [nsplit][N][Hq]      */
+    int nsplit;
+};
+
+template <bool SPLIT>
 __global__ __launch_bounds__(256) void attention_kernel(
     const bf16 *__restrict__ q, const bf16 *__restrict__ gate, int gts, int ghs,
     const bf16 *__restrict__ pk, const bf16 *__restrict__ pvt, int P, int p_stride,
     const bf16 *__restrict__ ok, const bf16 *__restrict__ ovt, int o_stride,
-    const int32_t *__restrict__ own_base, int N, int Hq, int Hkv, int ntile, bf16 *__restrict__ out) {
+    const int32_t *__restrict__ own_base, int N, int Hq, int Hkv, int ntile, bf16 *__restrict__ out,
+    AttnPart part) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[LDS_BYTES];
 
     /* ---- XCD-aware work mapping ---- */
@@ -186,7 +197,19 @@ __global__ __launch_bounds__(256) void attention_kernel(
     const int own_hi = min(n0 + QW, N) - 1;
     const int nst = (P + BK - 1) / BK;
     const int own_t0 = own_lo / BK;
-    const int ntl = nst + own_hi / BK - own_t0 + 1;
+    const int ntl_all = nst + own_hi / BK - own_t0 + 1;
+    /* SPLIT: this workgroup's contiguous share [tb, tb + ntl) of the tiles */
+    const int split = SPLIT ? (int)blockIdx.y : 0;
+    const int tb = SPLIT ? split * ntl_all / part.nsplit : 0;
+    const int ntl = SPLIT ? (split + 1) * ntl_all / part.nsplit - tb : ntl_all;
+    if (SPLIT && ntl <= 0) { /* no tiles: an empty partial */
+        if (qvalid && h == 0) {
+            const size_t r = ((size_t)split * N + n) * Hq + head;
+            part.l[r] = 0.f;
+            part.mu[r] = 0.f;
+        }
+        return;
+    }
 
     uint32_t koff[2];
 #pragma unroll
@@ -206,6 +229,7 @@ __global__ __launch_bounds__(256) void attention_kernel(
     ow.vrow_bytes = o_stride * 2;
     ow.voff = vl * ow.vrow_bytes + vc;
     auto src_of = [&](int i) {
+        i += tb;
         TileSrc s = i < nst ? st : ow;
         s.kbase = i < nst ? i * BK : (own_t0 + i - nst) * BK;
         return s;
@@ -276,8 +300,9 @@ __global__ __launch_bounds__(256) void attention_kernel(
         unsigned char *const vdst = smem + V_OFF + (vbuf ^ 1) * V_BYTES;
 
         /* mask: key of accumulator slot r of block t is 32t + 16(r>>3) + 8h + (r&7) */
-        const bool own = i >= nst;
-        const int kbase = own ? (own_t0 + i - nst) * BK : i * BK;
+        const int gi = i + tb; /* index in the full tile list */
+        const bool own = gi >= nst;
+        const int kbase = own ? (own_t0 + gi - nst) * BK : gi * BK;
         if (own || kbase + BK > P) {
             const int lo = own ? base_n : 0, hi = own ? n : P - 1;
             const int k8 = kbase + 8 * h;
@@ -415,6 +440,22 @@ __global__ __launch_bounds__(256) void attention_kernel(
     if (!qvalid)
         return;
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    if constexpr (SPLIT) { /* the unnormalised partial; the merge gates it */
+        const size_t r = ((size_t)split * N + n) * Hq + head;
+        float *po = part.o + r * D;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int gq = 0; gq < 4; gq++)
+                *(float4 *)(po + 32 * dt + 8 * gq + 4 * h) =
+                    make_float4(o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2],
+                                o[dt][4 * gq + 3]);
+        if (h == 0) {
+            part.l[r] = l_tot;
+            part.mu[r] = mu_run;
+        }
+        return;
+    }
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const bf16 *g = gate + (size_t)n * gts + (size_t)head * ghs;
     bf16 *dst = out + ((size_t)n * Hq + head) * D;
@@ -431,6 +472,57 @@ __global__ __launch_bounds__(256) void attention_kernel(
             *(bf16x4 *)(dst + d0) = r;
         }
     }
+}
+
+/* Merge of the key-split partials: per (token, q-head) row, with mu the
+ * largest shift among the splits that saw keys, o = sum_s 2^(mu_s - mu) o_s
+ * and l likewise (the same p = 2^(s - mu) for every split, up to fp32 sum
+ * order); out = o / l * sigmoid(gate). One wave per row, 4 dims a lane. */
+__global__ __launch_bounds__(256) void attention_merge_kernel(AttnPart part,
+                                                              const bf16 *__restrict__ gate,
+                                                              int gts, int ghs, int N, int Hq,
+                                                              bf16 *__restrict__ out) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= N * Hq)
+        return;
+    const int n = row / Hq, head = row % Hq;
+    const size_t rs = (size_t)N * Hq;
+    /* every split's l, mu and o slice in flight before any arithmetic */
+    float ls[CUJEV_ATTN_MAX_SPLITS], ms[CUJEV_ATTN_MAX_SPLITS];
+    float4 os[CUJEV_ATTN_MAX_SPLITS];
+#pragma unroll
+    for (int sp = 0; sp < CUJEV_ATTN_MAX_SPLITS; sp++) {
+        const int spc = min(sp, part.nsplit - 1);
+        ls[sp] = part.l[spc * rs + row];
+        ms[sp] = part.mu[spc * rs + row];
+        os[sp] = *(const float4 *)(part.o + (spc * rs + row) * D + 4 * lane);
+    }
+    float mu = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < CUJEV_ATTN_MAX_SPLITS; sp++)
+        if (sp < part.nsplit && ls[sp] > 0.f)
+            mu = fmaxf(mu, ms[sp]);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float l = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < CUJEV_ATTN_MAX_SPLITS; sp++) {
+        /* a split without visible keys adds nothing (its o was not written) */
+        if (!(sp < part.nsplit && ls[sp] > 0.f))
+            continue;
+        const float w = fast_exp2(ms[sp] - mu);
+        const float4 v = os[sp];
+        acc.x = fmaf(w, v.x, acc.x), acc.y = fmaf(w, v.y, acc.y);
+        acc.z = fmaf(w, v.z, acc.z), acc.w = fmaf(w, v.w, acc.w);
+        l = fmaf(w, ls[sp], l);
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const bf16x4 gv = *(const bf16x4 *)(gate + (size_t)n * gts + (size_t)head * ghs + 4 * lane);
+    const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+    bf16x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        r[e] = f2bf(a[e] * inv * sigmoid_f(bf2f(gv[e])));
+    *(bf16x4 *)(out + (size_t)row * D + 4 * lane) = r;
 }
 
 /* ---- prep: norm + RoPE + scale for q, norm + RoPE for k, V transposed ----
@@ -585,11 +677,25 @@ extern "C" hipError_t k_attn_prep(const bf16_t *proj, int proj_stride, const flo
     return hipGetLastError();
 }
 
+extern "C" int cujev_attention_splits(int N, int Hkv, int P) {
+    const int wgs = CEIL_DIV(N, QW) * Hkv, nst = CEIL_DIV(P, BK);
+    if (N <= 0 || P <= 0 || N > CUJEV_ATTN_SPLIT_MAX_N || wgs >= 128)
+        return 1;
+    int s = 256 / wgs;
+    s = s > nst ? nst : s;
+    s = s > CUJEV_ATTN_MAX_SPLITS ? CUJEV_ATTN_MAX_SPLITS : s;
+    return s < 1 ? 1 : s;
+}
+
+extern "C" size_t cujev_attention_ws_bytes(int N, int Hq, int nsplit) {
+    return nsplit > 1 ? (size_t)nsplit * N * Hq * (D + 2) * sizeof(float) : 0;
+}
+
 extern "C" hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_tok_stride,
                                   int gate_head_stride, const bf16_t *pk, const bf16_t *pvt, int P,
                                   int p_stride, const bf16_t *ok, const bf16_t *ovt, int o_stride,
                                   const int32_t *own_base, int N, int Hq, int Hkv, bf16_t *out,
-                                  hipStream_t stream) {
+                                  void *ws, size_t ws_bytes, hipStream_t stream) {
     if (N <= 0)
         return hipSuccess;
     if (Hq != 4 * Hkv || P < 0 || p_stride % 64 != 0 || o_stride % 64 != 0)
@@ -602,9 +708,27 @@ extern "C" hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_
     } else {
         nblk = ntile * Hkv;
     }
-    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)nblk), dim3(256), 0, stream,
+    /* Few workgroups (an eval of a few branches: 4 kv-heads x 3 token tiles
+     * at 80 tokens): split the key tiles over blockIdx.y so that about 256
+     * workgroups run, when the workspace holds the partials. */
+    const int nsplit = cujev_attention_splits(N, Hkv, P);
+    if (nsplit > 1 && ws && ws_bytes >= cujev_attention_ws_bytes(N, Hq, nsplit)) {
+        const size_t rows = (size_t)nsplit * N * Hq;
+        AttnPart part{(float *)ws, (float *)ws + rows * D, (float *)ws + rows * (D + 1), nsplit};
+        hipLaunchKernelGGL(attention_kernel<true>, dim3((unsigned)nblk, (unsigned)nsplit),
+                           dim3(256), 0, stream, (const bf16 *)q, (const bf16 *)gate,
+                           gate_tok_stride, gate_head_stride, (const bf16 *)pk, (const bf16 *)pvt,
+                           P, p_stride, (const bf16 *)ok, (const bf16 *)ovt, o_stride, own_base, N,
+                           Hq, Hkv, ntile, (bf16 *)out, part);
+        hipLaunchKernelGGL(attention_merge_kernel, dim3((unsigned)CEIL_DIV(N * Hq, 4)), dim3(256),
+                           0, stream, part, (const bf16 *)gate, gate_tok_stride, gate_head_stride,
+                           N, Hq, (bf16 *)out);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(attention_kernel<false>, dim3((unsigned)nblk), dim3(256), 0, stream,
                        (const bf16 *)q, (const bf16 *)gate, gate_tok_stride, gate_head_stride,
                        (const bf16 *)pk, (const bf16 *)pvt, P, p_stride, (const bf16 *)ok,
-                       (const bf16 *)ovt, o_stride, own_base, N, Hq, Hkv, ntile, (bf16 *)out);
+                       (const bf16 *)ovt, o_stride, own_base, N, Hq, Hkv, ntile, (bf16 *)out,
+                       AttnPart{});
     return hipGetLastError();
 }

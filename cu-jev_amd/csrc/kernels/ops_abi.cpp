@@ -148,7 +148,27 @@ EXPORT int cujev_op_attention(const void *q, const void *gate, int gate_tok_stri
     return launched(k_attention((const bf16_t *)q, (const bf16_t *)gate, gate_tok_stride,
                                 gate_head_stride, (const bf16_t *)pk, (const bf16_t *)pvt, P,
                                 p_stride, (const bf16_t *)ok, (const bf16_t *)ovt, o_stride,
-                                own_base, N, Hq, Hkv, (bf16_t *)out, (hipStream_t)stream),
+                                own_base, N, Hq, Hkv, (bf16_t *)out, nullptr, 0,
+                                (hipStream_t)stream),
+                    "attention");
+}
+
+EXPORT size_t cujev_ops_attention_ws_bytes(int N, int Hq, int Hkv, int P) {
+    return cujev_attention_ws_bytes(N, Hq, cujev_attention_splits(N, Hkv, P));
+}
+
+EXPORT int cujev_op_attention_ws(const void *q, const void *gate, int gate_tok_stride,
+                                 int gate_head_stride, const void *pk, const void *pvt, int P,
+                                 int p_stride, const void *ok, const void *ovt, int o_stride,
+                                 const int32_t *own_base, int N, int Hq, int Hkv, void *out,
+                                 void *ws, size_t ws_bytes, void *stream) {
+    if (N < 0 || P < 0 || Hkv <= 0)
+        return fail(1, "attention: bad arguments");
+    return launched(k_attention((const bf16_t *)q, (const bf16_t *)gate, gate_tok_stride,
+                                gate_head_stride, (const bf16_t *)pk, (const bf16_t *)pvt, P,
+                                p_stride, (const bf16_t *)ok, (const bf16_t *)ovt, o_stride,
+                                own_base, N, Hq, Hkv, (bf16_t *)out, ws, ws_bytes,
+                                (hipStream_t)stream),
                     "attention");
 }
 

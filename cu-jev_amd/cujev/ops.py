@@ -32,6 +32,8 @@ _SIGS = {
     "cujev_op_rope_table": [_D, _I, _I, _P],
     "cujev_op_attn_prep": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _F, _F, _P, _P, _P, _I, _P],
     "cujev_op_attention": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P],
+    "cujev_op_attention_ws": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P,
+                              C.c_size_t, _P],
     "cujev_op_gdn_conv_prep": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P,
                                _P, _P],
     "cujev_op_gemm_small": [_P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _P],
@@ -64,6 +66,8 @@ def load():
     lib.cujev_ops_gdn_scratch_bytes.restype = C.c_size_t
     lib.cujev_ops_gemm_small_splits.argtypes = [_I, _I]
     lib.cujev_ops_gemm_small_splits.restype = _I
+    lib.cujev_ops_attention_ws_bytes.argtypes = [_I, _I, _I, _I]
+    lib.cujev_ops_attention_ws_bytes.restype = C.c_size_t
     lib.cujev_ops_blaslt_version.argtypes = []
     lib.cujev_ops_blaslt_version.restype = _I
     lib.cujev_op_gemm_tune.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, _I, _I, _I, _I,
@@ -80,7 +84,7 @@ def load():
 
 def exported_symbols():
     return ["cujev_ops_kv_stride", "cujev_ops_last_error", "cujev_ops_gdn_scratch_bytes",
-            "cujev_ops_gemm_small_splits",
+            "cujev_ops_gemm_small_splits", "cujev_ops_attention_ws_bytes",
             "cujev_ops_blaslt_version", "cujev_op_gemm_tune", *_SIGS]
 
 
@@ -123,9 +127,20 @@ def attn_prep(proj, q_norm_w, k_norm_w, pos, Hq, Hkv, rot, rope, eps, q_scale,
           _ptr(k_cache), _ptr(vt_cache), cache_stride, _stream())
 
 
+def attention_ws_bytes(N, Hq, Hkv, P) -> int:
+    return int(load().cujev_ops_attention_ws_bytes(int(N), int(Hq), int(Hkv), int(P)))
+
+
 def attention(q, gate, gate_tok_stride, gate_head_stride, pk, pvt, P, p_stride, ok, ovt,
-              o_stride, own_base, Hq, Hkv, out):
+              o_stride, own_base, Hq, Hkv, out, ws=None):
+    """ws: optional uint8 device workspace (attention_ws_bytes) that lets a
+    few-workgroup shape split its key tiles."""
     N = q.shape[0]
+    if ws is not None:
+        _call("cujev_op_attention_ws", _ptr(q), _ptr(gate), gate_tok_stride, gate_head_stride,
+              _ptr(pk), _ptr(pvt), int(P), p_stride, _ptr(ok), _ptr(ovt), o_stride,
+              _ptr(own_base), N, Hq, Hkv, _ptr(out), _ptr(ws), ws.numel(), _stream())
+        return
     _call("cujev_op_attention", _ptr(q), _ptr(gate), gate_tok_stride, gate_head_stride,
           _ptr(pk), _ptr(pvt), int(P), p_stride, _ptr(ok), _ptr(ovt), o_stride, _ptr(own_base),
           N, Hq, Hkv, _ptr(out), _stream())

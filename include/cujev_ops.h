@@ -106,6 +106,19 @@ int cujev_op_attention(const void *q, const void *gate, int gate_tok_stride, int
                        const void *pk, const void *pvt, int P, int p_stride, const void *ok,
                        const void *ovt, int o_stride, const int32_t *own_base, int N, int Hq,
                        int Hkv, void *out, void *stream);
+/* The same with a device workspace (no counterpart in the reference, whose
+ * kernel has one pass): with few workgroups (N <= 256 tokens giving under
+ * 128 of them) and P > 0 the key tiles are split over up to 16 workgroups
+ * per token tile and their softmax partials merged by a second kernel. The
+ * result equals one pass up to fp32 summation order. ws_bytes from
+ * cujev_ops_attention_ws_bytes (0 = no split for this shape; a smaller ws
+ * also runs one pass). */
+int cujev_op_attention_ws(const void *q, const void *gate, int gate_tok_stride,
+                          int gate_head_stride, const void *pk, const void *pvt, int P,
+                          int p_stride, const void *ok, const void *ovt, int o_stride,
+                          const int32_t *own_base, int N, int Hq, int Hkv, void *out, void *ws,
+                          size_t ws_bytes, void *stream);
+size_t cujev_ops_attention_ws_bytes(int N, int Hq, int Hkv, int P);
 
 /* Replaces reference src/kernels/kernels.h:214-215 (k_gdn_conv) and :221-223
  * (k_gdn_prep), fused. proj rows [q Hk*128 | k Hk*128 | v Hv*128 | z | b | a].

@@ -56,7 +56,9 @@ def make_case(seed, Hq, Hkv, P, seg_lens, stride_tokens=None):
     return q, gate, ks, vs, ko, vo, own_base
 
 
-def run_attention(o, q, gate, ks, vs, ko, vo, own_base, Hq, Hkv):
+def run_attention(o, q, gate, ks, vs, ko, vo, own_base, Hq, Hkv, split=False):
+    """split: pass a workspace so that few-workgroup shapes split their key
+    tiles over several workgroups and merge the partials."""
     dev = "cuda"
     N, P = q.shape[0], ks.shape[0]
     ps = o.kv_stride(max(P, 1))
@@ -76,7 +78,13 @@ def run_attention(o, q, gate, ks, vs, ko, vo, own_base, Hq, Hkv):
     qd = bf(q * orc.LOG2E / 16.0).to(dev)  # the prep kernel's prescaling
     out = torch.empty(N, Hq * D, dtype=torch.bfloat16, device=dev)
     ob = torch.as_tensor(own_base).to(dev)
-    o.attention(qd, qg[:, :, D:], Hq * 2 * D, 2 * D, pk, pvt, P, ps, ok, ovt, os_, ob, Hq, Hkv, out)
+    ws = None
+    if split:
+        nb = o.attention_ws_bytes(N, Hq, Hkv, P)
+        assert nb > 0, "shape does not split"
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    o.attention(qd, qg[:, :, D:], Hq * 2 * D, 2 * D, pk, pvt, P, ps, ok, ovt, os_, ob, Hq, Hkv, out,
+                ws=ws)
     torch.cuda.synchronize()
     return np32(out).reshape(N, Hq, D), np32(qd)
 
@@ -109,6 +117,26 @@ def test_attention_matches_oracle(seed, Hq, Hkv, P, seg_lens):
     err = rel_err(got, ref)
     print(f"rel err {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("seed,Hq,Hkv,P,seg_lens", [
+    (41, 16, 4, 530, [20, 20, 20, 20]),   # the 4B eval: 12 workgroups -> 9 key splits
+    (42, 8, 2, 100, [1, 17, 33]),          # 2 state tiles, own tiles in the last split
+    (43, 16, 4, 8192, [1]),                # one token, 16 splits of 8 tiles
+    (44, 4, 1, 70, [3, 64, 5]),            # state tile edge; a split of own tiles only
+])
+def test_attention_key_split_matches_oracle(seed, Hq, Hkv, P, seg_lens):
+    """Key tiles split over workgroups with the softmax partials merged: equal
+    to the oracle, and to the one-pass kernel up to fp32 summation order."""
+    o = ops()
+    print(f"key split seed={seed} P={P} seg_lens={seg_lens}", flush=True)
+    q, gate, ks, vs, ko, vo, ob = make_case(seed, Hq, Hkv, P, seg_lens)
+    got, qd = run_attention(o, q, gate, ks, vs, ko, vo, ob, Hq, Hkv, split=True)
+    one, _ = run_attention(o, q, gate, ks, vs, ko, vo, ob, Hq, Hkv)
+    ref = oracle_attention(qd, gate, ks, vs, ko, vo, ob)
+    e, e1 = rel_err(got, ref), rel_err(got, one)
+    print(f"vs oracle {e:.3e}  vs one pass {e1:.3e}")
+    assert e <= TOL and e1 <= 1e-2
 
 
 def test_attention_branch_isolation():
