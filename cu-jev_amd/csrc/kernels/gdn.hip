@@ -262,6 +262,8 @@ struct ConvSrc {
     const int32_t *own_base;
     const float *A_neg_exp, *dt_bias;
     int N;
+    float *conv_out; /* prefill: the last 3 pre-conv inputs of segment 0 */
+    int seg0_len;
 };
 
 /* The three 128-channel slices a phase-A workgroup needs (q and k of its
@@ -449,6 +451,22 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
         } else {
             constexpr bool TAIL = SRC == 2;
             const int C = (2 * Hk + Hv) * DK;
+            /* the state's new conv tail (gdn_conv_tail_kernel's values): the
+             * chunk-0 workgroups write their v slice, and the first v-head of
+             * each k-head also its q and k slices */
+            if (cv.conv_out && ch == 0 && tid < DK) {
+                const int nsl = hv % (Hv / Hk) == 0 ? 3 : 1;
+                for (int k = 0; k < nsl; k++) {
+                    const int cg = slice_c0(nsl == 3 ? k : 2, Hk, hk, hv) + tid;
+#pragma unroll
+                    for (int j = 0; j < 3; j++) {
+                        const int t = cv.seg0_len - 3 + j;
+                        cv.conv_out[(size_t)cg * 3 + j] =
+                            t >= 0 ? bf2f(cv.proj[(size_t)t * cv.ps + cg])
+                                   : (cv.conv_in ? cv.conv_in[(size_t)cg * 3 + t + 3] : 0.f);
+                    }
+                }
+            }
             if (wave == 0 && lane < L) {
                 const bf16 *ab = cv.proj + (size_t)(t0 + lane) * cv.ps + C + Hv * DV; /* b, a */
                 bv = sigmoid_f(bf2f(ab[hv]));
@@ -1239,13 +1257,16 @@ extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const flo
         ((uintptr_t)proj & 15) != 0)
         return hipErrorInvalidValue;
     const int C = (2 * Hk + Hv) * DK;
-    if (conv_out)
-        hipLaunchKernelGGL(gdn_conv_tail_kernel, dim3((unsigned)CEIL_DIV(C, 256)), dim3(256), 0,
-                           stream, (const bf16 *)proj, proj_stride, conv_in, conv_out, seg0_len, C);
-    if (ck->num_chunks <= 0)
+    if (ck->num_chunks <= 0) {
+        if (conv_out)
+            hipLaunchKernelGGL(gdn_conv_tail_kernel, dim3((unsigned)CEIL_DIV(C, 256)), dim3(256),
+                               0, stream, (const bf16 *)proj, proj_stride, conv_in, conv_out,
+                               seg0_len, C);
         return hipGetLastError();
+    }
+    /* phase A's chunk-0 workgroups also write the conv tail */
     const ConvSrc cv{(const bf16 *)proj, proj_stride, conv_w, conv_in, own_base,
-                     A_neg_exp,          dt_bias,     N};
+                     A_neg_exp,          dt_bias,     N,         conv_out, seg0_len};
     hipLaunchKernelGGL(conv_in ? gdn_chunk_a_kernel<2> : gdn_chunk_a_kernel<1>,
                        dim3((unsigned)ck->num_chunks, (unsigned)Hv), dim3(256), 0, stream,
                        (const bf16 *)nullptr, (const bf16 *)nullptr, (const bf16 *)nullptr,

@@ -168,7 +168,8 @@ hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const f
  * inside the scan's first phase (q, k, v never leave the chip), then
  * k_gdn_scan's recurrence and gated norm with z read from proj at column
  * C = (2Hk+Hv)*128. Same arguments and results as k_gdn_conv_prep followed by
- * k_gdn_scan (bit for bit). proj rows must be 16-byte aligned. */
+ * k_gdn_scan (bit for bit). proj rows must be 16-byte aligned; conv_out
+ * must not alias conv_in. */
 hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const float *conv_w,
                        const float *conv_in, float *conv_out, int seg0_len,
                        const int32_t *own_base, const float *A_neg_exp, const float *dt_bias,

@@ -165,7 +165,7 @@ int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const float *
  * Arguments as cujev_op_gdn_conv_prep followed by cujev_op_gdn_scan (z is
  * read from proj at column C = (2Hk+Hv)*128); the result is bit-identical to
  * that pair, but q, k, v, g and beta are never written out. proj rows must be
- * 16-byte aligned (proj_stride % 8 == 0). */
+ * 16-byte aligned (proj_stride % 8 == 0); conv_out must not alias conv_in. */
 int cujev_op_gdn_layer(const void *proj, int proj_stride, const float *conv_w,
                        const float *conv_in, float *conv_out, int seg0_len,
                        const int32_t *own_base, const float *A_neg_exp, const float *dt_bias,
