@@ -299,10 +299,7 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
     m->max_chunks = m->max_tokens / 64 + (int)B + 1;
     m->meta_ints = 3 * N + 3 * B + 4 * (size_t)m->max_chunks + B * (size_t)m->opts.max_candidates + B;
     m->gemm_ws_bytes = (size_t)64 << 20;
-    {
-        const int an = m->max_tokens < CUJEV_ATTN_SPLIT_MAX_N ? m->max_tokens : CUJEV_ATTN_SPLIT_MAX_N;
-        m->attn_ws_bytes = cujev_attention_ws_bytes(an, m->Hq, CUJEV_ATTN_MAX_SPLITS);
-    }
+    m->attn_ws_bytes = cujev_attention_ws_max(m->max_tokens, m->Hq, m->Hkv);
     struct {
         void **p;
         size_t bytes;

@@ -492,10 +492,12 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnPart part,
     float4 os[CUJEV_ATTN_MAX_SPLITS];
 #pragma unroll
     for (int sp = 0; sp < CUJEV_ATTN_MAX_SPLITS; sp++) {
-        const int spc = min(sp, part.nsplit - 1);
-        ls[sp] = part.l[spc * rs + row];
-        ms[sp] = part.mu[spc * rs + row];
-        os[sp] = *(const float4 *)(part.o + (spc * rs + row) * D + 4 * lane);
+        ls[sp] = 0.f, ms[sp] = 0.f, os[sp] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (sp < part.nsplit) { /* uniform */
+            ls[sp] = part.l[sp * rs + row];
+            ms[sp] = part.mu[sp * rs + row];
+            os[sp] = *(const float4 *)(part.o + (sp * rs + row) * D + 4 * lane);
+        }
     }
     float mu = -INFINITY;
 #pragma unroll
@@ -678,17 +680,29 @@ extern "C" hipError_t k_attn_prep(const bf16_t *proj, int proj_stride, const flo
 }
 
 extern "C" int cujev_attention_splits(int N, int Hkv, int P) {
-    const int wgs = CEIL_DIV(N, QW) * Hkv, nst = CEIL_DIV(P, BK);
-    if (N <= 0 || P <= 0 || N > CUJEV_ATTN_SPLIT_MAX_N || wgs >= 128)
+    const int wgs = CEIL_DIV(N, QW) * Hkv;
+    /* at most as many shares as a token tile has key tiles (state + own) */
+    const int ntl_max = CEIL_DIV(P, BK) + CEIL_DIV(N, BK) + 1;
+    if (N <= 0 || P < 0 || N > CUJEV_ATTN_SPLIT_MAX_N || wgs >= 128)
         return 1;
     int s = 256 / wgs;
-    s = s > nst ? nst : s;
+    s = s > ntl_max ? ntl_max : s;
     s = s > CUJEV_ATTN_MAX_SPLITS ? CUJEV_ATTN_MAX_SPLITS : s;
     return s < 1 ? 1 : s;
 }
 
 extern "C" size_t cujev_attention_ws_bytes(int N, int Hq, int nsplit) {
     return nsplit > 1 ? (size_t)nsplit * N * Hq * (D + 2) * sizeof(float) : 0;
+}
+
+extern "C" size_t cujev_attention_ws_max(int max_tokens, int Hq, int Hkv) {
+    size_t best = 0;
+    const int nmax = max_tokens < CUJEV_ATTN_SPLIT_MAX_N ? max_tokens : CUJEV_ATTN_SPLIT_MAX_N;
+    for (int n = 1; n <= nmax; n++) { /* P large: the most shares */
+        const size_t b = cujev_attention_ws_bytes(n, Hq, cujev_attention_splits(n, Hkv, 1 << 20));
+        best = b > best ? b : best;
+    }
+    return best;
 }
 
 extern "C" hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_tok_stride,

@@ -66,7 +66,7 @@ hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_tok_stride,
                        const int32_t *own_base, int N, int Hq, int Hkv, bf16_t *out,
                        void *ws, size_t ws_bytes, hipStream_t stream);
 /* With few workgroups (N <= CUJEV_ATTN_SPLIT_MAX_N tokens giving under 128
- * of them) and P > 0, k_attention splits the key tiles over
+ * of them), k_attention splits the key tiles over
  * cujev_attention_splits() workgroups per token tile and merges their
  * softmax partials in a second kernel, when `ws` holds
  * cujev_attention_ws_bytes() bytes; otherwise (ws NULL) one pass. */
@@ -74,6 +74,8 @@ hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_tok_stride,
 #define CUJEV_ATTN_MAX_SPLITS 16
 int cujev_attention_splits(int N, int Hkv, int P);
 size_t cujev_attention_ws_bytes(int N, int Hq, int nsplit);
+/* the largest workspace any N <= max_tokens can use */
+size_t cujev_attention_ws_max(int max_tokens, int Hq, int Hkv);
 
 /* ---- Gated DeltaNet -------------------------------------------------------
  * proj[N, proj_stride] bf16 is the fused row [q Hk*128 | k Hk*128 | v Hv*128 |

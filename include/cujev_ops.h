@@ -108,7 +108,7 @@ int cujev_op_attention(const void *q, const void *gate, int gate_tok_stride, int
                        int Hkv, void *out, void *stream);
 /* The same with a device workspace (no counterpart in the reference, whose
  * kernel has one pass): with few workgroups (N <= 256 tokens giving under
- * 128 of them) and P > 0 the key tiles are split over up to 16 workgroups
+ * 128 of them) the key tiles are split over up to 16 workgroups
  * per token tile and their softmax partials merged by a second kernel. The
  * result equals one pass up to fp32 summation order. ws_bytes from
  * cujev_ops_attention_ws_bytes (0 = no split for this shape; a smaller ws

@@ -124,6 +124,8 @@ def test_attention_matches_oracle(seed, Hq, Hkv, P, seg_lens):
     (42, 8, 2, 100, [1, 17, 33]),          # 2 state tiles, own tiles in the last split
     (43, 16, 4, 8192, [1]),                # one token, 16 splits of 8 tiles
     (44, 4, 1, 70, [3, 64, 5]),            # state tile edge; a split of own tiles only
+    (45, 16, 4, 0, [200]),                 # a prefill: causal, early rows see few tiles
+    (46, 8, 2, 0, [100, 120]),             # two prefill segments
 ])
 def test_attention_key_split_matches_oracle(seed, Hq, Hkv, P, seg_lens):
     """Key tiles split over workgroups with the softmax partials merged: equal
