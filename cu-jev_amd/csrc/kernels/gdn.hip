@@ -262,8 +262,16 @@ struct ConvSrc {
     const int32_t *own_base;
     const float *A_neg_exp, *dt_bias;
     int N;
-    float *conv_out; /* prefill: the last 3 pre-conv inputs of segment 0 */
-    int seg0_len;
+};
+
+/* The state's new conv tail (prefill): extra workgroups of the phase B grid
+ * copy it, beside the recurrence, which leaves half the CUs idle. */
+struct TailJob {
+    const bf16 *proj;
+    int ps;
+    const float *conv_in;
+    float *conv_out; /* NULL: no tail */
+    int seg0_len, C;
 };
 
 /* The three 128-channel slices a phase-A workgroup needs (q and k of its
@@ -451,22 +459,6 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
         } else {
             constexpr bool TAIL = SRC == 2;
             const int C = (2 * Hk + Hv) * DK;
-            /* the state's new conv tail (gdn_conv_tail_kernel's values): the
-             * chunk-0 workgroups write their v slice, and the first v-head of
-             * each k-head also its q and k slices */
-            if (cv.conv_out && ch == 0 && tid < DK) {
-                const int nsl = hv % (Hv / Hk) == 0 ? 3 : 1;
-                for (int k = 0; k < nsl; k++) {
-                    const int cg = slice_c0(nsl == 3 ? k : 2, Hk, hk, hv) + tid;
-#pragma unroll
-                    for (int j = 0; j < 3; j++) {
-                        const int t = cv.seg0_len - 3 + j;
-                        cv.conv_out[(size_t)cg * 3 + j] =
-                            t >= 0 ? bf2f(cv.proj[(size_t)t * cv.ps + cg])
-                                   : (cv.conv_in ? cv.conv_in[(size_t)cg * 3 + t + 3] : 0.f);
-                    }
-                }
-            }
             if (wave == 0 && lane < L) {
                 const bf16 *ab = cv.proj + (size_t)(t0 + lane) * cv.ps + C + Hv * DV; /* b, a */
                 bv = sigmoid_f(bf2f(ab[hv]));
@@ -807,12 +799,29 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
     const int32_t *__restrict__ seg_chunk0, const int32_t *__restrict__ seg_nchunk,
     const float *__restrict__ S_in, float *__restrict__ S_out, int Hv, int units,
-    bf16 *__restrict__ o) {
+    bf16 *__restrict__ o, TailJob tail) {
     __shared__ __attribute__((aligned(16))) bf16 sT[32][DK + 8];  /* S^T [column][dk]     */
     __shared__ __attribute__((aligned(16))) bf16 vT[32][CH + 8];  /* V'^T [column][token] */
     __shared__ __attribute__((aligned(16))) bf16 ost[4][16][40];  /* per-wave O tile      */
 
     const int bid = blockIdx.x;
+    const int nmain = NCB * ((units + 7) / 8) * 8;
+    if (bid >= nmain) { /* conv tail: 256 channels per workgroup */
+        const int c = (bid - nmain) * 256 + threadIdx.x;
+        if (c < tail.C) {
+            float tv[3];
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                const int t = tail.seg0_len - 3 + j;
+                tv[j] = t >= 0 ? bf2f(tail.proj[(size_t)t * tail.ps + c])
+                               : (tail.conv_in ? tail.conv_in[(size_t)c * 3 + t + 3] : 0.f);
+            }
+#pragma unroll
+            for (int j = 0; j < 3; j++)
+                tail.conv_out[(size_t)c * 3 + j] = tv[j];
+        }
+        return;
+    }
     const int u = (bid & 7) + 8 * ((bid >> 3) / NCB), cbk = (bid >> 3) % NCB;
     if (u >= units)
         return;
@@ -1196,12 +1205,16 @@ extern "C" hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const
 static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *S_out,
                               const bf16_t *z, int z_stride, const float *norm_w, float eps,
                               int Hv, bf16_t *y, const cujev_gdn_scratch *ws, int N,
-                              hipStream_t stream) {
+                              const TailJob &tail, hipStream_t stream) {
     const bool packed = ck->chunk_starts != nullptr;
     if (!S_out && (packed || ck->max_seg_chunks == 1)) {
         /* packed: the units are the chunks, each scanned from S_in */
         const int units = packed ? ck->num_chunks : ck->num_segments;
         const int spw = max(1, CEIL_DIV(units * Hv, SB_WGS));
+        if (tail.conv_out)
+            hipLaunchKernelGGL(gdn_conv_tail_kernel, dim3((unsigned)CEIL_DIV(tail.C, 256)),
+                               dim3(256), 0, stream, tail.proj, tail.ps, tail.conv_in,
+                               tail.conv_out, tail.seg0_len, tail.C);
         hipLaunchKernelGGL(gdn_short_b_kernel, dim3((unsigned)CEIL_DIV(units, spw), (unsigned)Hv),
                            dim3(256), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
                            (const bf16x8 *)ws->QK, (const bf16x8 *)ws->U, ck->chunk_tok0,
@@ -1213,11 +1226,12 @@ static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *
     if (packed)
         return hipErrorInvalidValue; /* packed segments write no final state */
     const int units = ck->num_segments * Hv;
-    hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)(NCB * CEIL_DIV(units, 8) * 8)),
+    const int ntail = tail.conv_out ? CEIL_DIV(tail.C, 256) : 0;
+    hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)(NCB * CEIL_DIV(units, 8) * 8 + ntail)),
                        dim3(256), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
                        (const bf16x8 *)ws->QK, (const bf16x8 *)ws->KgT, (const bf16x8 *)ws->U,
                        ws->Glast, ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk,
-                       S_in, S_out, Hv, units, (bf16 *)ws->O);
+                       S_in, S_out, Hv, units, (bf16 *)ws->O, tail);
     const int rows = N * Hv;
     const bool zvec = z_stride % 8 == 0 && ((uintptr_t)z & 15) == 0;
     hipLaunchKernelGGL(zvec ? gdn_norm_gate_kernel<true> : gdn_norm_gate_kernel<false>,
@@ -1241,7 +1255,8 @@ extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t 
                        beta, ConvSrc{}, ck->chunk_tok0, ck->chunk_len, ck->chunk_starts, Hk, Hv,
                        (bf16 *)ws->W, (bf16 *)ws->Qg, (bf16 *)ws->QK, (bf16 *)ws->KgT,
                        (bf16 *)ws->U, ws->Glast);
-    return gdn_phase_b(ck, S_in, S_out, z, z_stride, norm_w, eps, Hv, y, ws, N, stream);
+    return gdn_phase_b(ck, S_in, S_out, z, z_stride, norm_w, eps, Hv, y, ws, N, TailJob{},
+                       stream);
 }
 
 extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const float *conv_w,
@@ -1264,14 +1279,16 @@ extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const flo
                                seg0_len, C);
         return hipGetLastError();
     }
-    /* phase A's chunk-0 workgroups also write the conv tail */
     const ConvSrc cv{(const bf16 *)proj, proj_stride, conv_w, conv_in, own_base,
-                     A_neg_exp,          dt_bias,     N,         conv_out, seg0_len};
+                     A_neg_exp,          dt_bias,     N};
+    /* the conv tail rides along with phase B */
+    const TailJob tail{(const bf16 *)proj, proj_stride, conv_in, conv_out, seg0_len, C};
     hipLaunchKernelGGL(conv_in ? gdn_chunk_a_kernel<2> : gdn_chunk_a_kernel<1>,
                        dim3((unsigned)ck->num_chunks, (unsigned)Hv), dim3(256), 0, stream,
                        (const bf16 *)nullptr, (const bf16 *)nullptr, (const bf16 *)nullptr,
                        (const float *)nullptr, (const float *)nullptr, cv, ck->chunk_tok0,
                        ck->chunk_len, ck->chunk_starts, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->Qg,
                        (bf16 *)ws->QK, (bf16 *)ws->KgT, (bf16 *)ws->U, ws->Glast);
-    return gdn_phase_b(ck, S_in, S_out, proj + C, proj_stride, norm_w, eps, Hv, y, ws, N, stream);
+    return gdn_phase_b(ck, S_in, S_out, proj + C, proj_stride, norm_w, eps, Hv, y, ws, N, tail,
+                       stream);
 }
