@@ -977,14 +977,16 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
 /* Every segment starts from the same S_in and nothing carries over between
  * them, so a workgroup takes one v-head and spw consecutive segments (as many
  * as keep about SB_WGS workgroups busy): S^T (bf16) goes to LDS once, then
- * per segment wave w computes columns 32w..32w+31 of
+ * per segment wave w (of 8: short per-wave chains, since a few branches
+ * give few workgroups) computes columns 16w..16w+15 of
  *   V' = U - W S,  O = (Q e^G) S + QKm V'
  * for the 16-row blocks that hold tokens (the same 16x16x32 steps and
  * operand fragments as gdn_chunk_b_kernel), and the workgroup applies the
  * gated RMSNorm of gdn_norm_gate_kernel to the segment's rows. */
 constexpr int SB_WGS = 512;
+constexpr int SB_THREADS = 512; /* 8 waves, 16 state columns each */
 
-__global__ __launch_bounds__(256) void gdn_short_b_kernel(
+__global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
     const bf16x8 *__restrict__ Wi, const bf16x8 *__restrict__ Qgi, const bf16x8 *__restrict__ QKi,
     const bf16x8 *__restrict__ Ui, const int32_t *__restrict__ chunk_tok0,
     const int32_t *__restrict__ chunk_len, const int32_t *__restrict__ seg_chunk0,
@@ -1000,13 +1002,12 @@ __global__ __launch_bounds__(256) void gdn_short_b_kernel(
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q4 = lane >> 4, c16 = lane & 15;
-    const int col0 = 32 * wave;
+    const int col0 = 16 * wave; /* this wave's 16 state columns */
 
     /* S^T: thread reads S[dk0..dk0+7][dv4..dv4+3] (16-byte rows) and writes
      * the 4 columns' 8-element runs */
-#pragma unroll
-    for (int it = 0; it < 2; it++) {
-        const int dv4 = 4 * (tid & 31), dk0 = 8 * (tid >> 5) + 64 * it;
+    {
+        const int dv4 = 4 * (tid & 31), dk0 = 8 * (tid >> 5);
         float4 r[8];
 #pragma unroll
         for (int e = 0; e < 8; e++)
@@ -1026,7 +1027,7 @@ __global__ __launch_bounds__(256) void gdn_short_b_kernel(
     }
     /* V'^T rows past a segment's last 16-row block may be read by the QKm
      * step (times an exact zero of the causal mask): keep them finite */
-    for (int i = tid; i < DV * (CH + 8) / 8; i += 256)
+    for (int i = tid; i < DV * (CH + 8) / 8; i += SB_THREADS)
         ((bf16x8 *)&vT[0][0])[i] = bf16x8{};
     lds_barrier();
 
@@ -1047,11 +1048,10 @@ __global__ __launch_bounds__(256) void gdn_short_b_kernel(
         const int nrb = (L + 15) >> 4, nks = (L + 31) >> 5;
         const size_t cb = (size_t)ch * Hv + hv;
 
-        floatx4 O[4][2];
+        floatx4 O[4];
 #pragma unroll
         for (int rb = 0; rb < 4; rb++) {
-            O[rb][0] = floatx4{};
-            O[rb][1] = floatx4{};
+            O[rb] = floatx4{};
             if (rb >= nrb)
                 continue;
             bf16x8 w[4], qg[4];
@@ -1060,24 +1060,22 @@ __global__ __launch_bounds__(256) void gdn_short_b_kernel(
                 w[s] = Wi[cb * 1024 + rb * 256 + 64 * s + lane];
                 qg[s] = Qgi[cb * 1024 + rb * 256 + 64 * s + lane];
             }
-            const bf16x8 u = Ui[cb * 1024 + (wave * 4 + rb) * 64 + lane];
-            floatx4 V[2] = {};
+            /* U fragment of the 32-column block holding these 16 columns:
+             * values 0..3 its first 16 columns, 4..7 the second */
+            const bf16x8 u = Ui[cb * 1024 + ((wave >> 1) * 4 + rb) * 64 + lane];
+            const int jh = 4 * (wave & 1);
+            floatx4 V = {};
 #pragma unroll
-            for (int s = 0; s < 4; s++)
-#pragma unroll
-                for (int jb = 0; jb < 2; jb++) {
-                    const bf16x8 sb = *(const bf16x8 *)&sT[col0 + 16 * jb + c16][32 * s + 8 * q4];
-                    V[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[s], sb, V[jb], 0, 0, 0);
-                    O[rb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qg[s], sb, O[rb][jb], 0, 0, 0);
-                }
-#pragma unroll
-            for (int jb = 0; jb < 2; jb++) {
-                bf16x4 p;
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    p[i] = f2bf(bf2f(u[4 * jb + i]) - V[jb][i]);
-                *(bf16x4 *)&vT[col0 + 16 * jb + c16][16 * rb + 4 * q4] = p;
+            for (int s = 0; s < 4; s++) {
+                const bf16x8 sb = *(const bf16x8 *)&sT[col0 + c16][32 * s + 8 * q4];
+                V = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[s], sb, V, 0, 0, 0);
+                O[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qg[s], sb, O[rb], 0, 0, 0);
             }
+            bf16x4 p;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                p[i] = f2bf(bf2f(u[jh + i]) - V[i]);
+            *(bf16x4 *)&vT[col0 + c16][16 * rb + 4 * q4] = p;
         }
         /* the wave reads back only its own columns of V'^T: LDS order suffices */
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1090,21 +1088,16 @@ __global__ __launch_bounds__(256) void gdn_short_b_kernel(
                 if (s >= nks)
                     continue;
                 const bf16x8 qk = QKi[cb * 512 + rb * 128 + 64 * s + lane];
-#pragma unroll
-                for (int jb = 0; jb < 2; jb++) {
-                    const bf16x8 vb = *(const bf16x8 *)&vT[col0 + 16 * jb + c16][32 * s + 8 * q4];
-                    O[rb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qk, vb, O[rb][jb], 0, 0, 0);
-                }
+                const bf16x8 vb = *(const bf16x8 *)&vT[col0 + c16][32 * s + 8 * q4];
+                O[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qk, vb, O[rb], 0, 0, 0);
             }
 #pragma unroll
-            for (int jb = 0; jb < 2; jb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    ob[16 * rb + 4 * q4 + i][col0 + 16 * jb + c16] = f2bf(O[rb][jb][i]);
+            for (int i = 0; i < 4; i++)
+                ob[16 * rb + 4 * q4 + i][col0 + c16] = f2bf(O[rb][i]);
         }
         lds_barrier();
         /* gated RMSNorm, 16 lanes per token row (as gdn_norm_gate_kernel) */
-        for (int r0 = 0; r0 < L; r0 += 16) {
+        for (int r0 = 0; r0 < L; r0 += SB_THREADS / 16) {
             const int t = r0 + (tid >> 4), sl = tid & 15;
             if (t < L) { /* whole 16-lane groups */
                 const bf16x8 ov = *(const bf16x8 *)&ob[t][8 * sl];
@@ -1216,7 +1209,7 @@ static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *
                                dim3(256), 0, stream, tail.proj, tail.ps, tail.conv_in,
                                tail.conv_out, tail.seg0_len, tail.C);
         hipLaunchKernelGGL(gdn_short_b_kernel, dim3((unsigned)CEIL_DIV(units, spw), (unsigned)Hv),
-                           dim3(256), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
+                           dim3(SB_THREADS), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
                            (const bf16x8 *)ws->QK, (const bf16x8 *)ws->U, ck->chunk_tok0,
                            ck->chunk_len, packed ? nullptr : ck->seg_chunk0,
                            packed ? nullptr : ck->seg_nchunk, units, spw, S_in, Hv,
