@@ -639,8 +639,9 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
     }
     lds_barrier();
     /* 3c: T_10 = -T_11 (A_10 T_00) with 32x32 blocks; lane = (row 8w + l/8,
-     * columns 4(l%8)..+3) */
-    {
+     * columns 4(l%8)..+3). A chunk of at most 32 tokens has A_10 = 0 and so
+     * T_10 = 0, which the A/T array already holds; only padding rows read it. */
+    if (L > 32) {
         const int r = 32 + 8 * wave + (lane >> 3), c0 = 4 * (lane & 7);
         const float4 x = row_times<32>(&sm.AT[r][0], &sm.AT[0][c0]);
         lds_barrier();
