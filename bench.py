@@ -10,24 +10,30 @@ random-id state prefill + 4 question branches of 20 tokens, read out over
 (4 per request, the cujev-bench sense) and p50 ms/request are reported next
 to it.
 
-Also measured, each in its own timed loop with HIP events on the stream the
-kernel is launched on:
+Also measured:
+  config5        config 5 end to end: a random-init Qwen3.5-9B-shaped model
+                 (hidden 4096, intermediate 12288, untied LM head) at the
+                 engine's default capacity: 8192-token state, 256 branches x
+                 16 tokens, 8 labels each (no CPU leg at this size);
   roofline       the shared-prefix attention kernel at config 3 (Hq 16/Hkv 4,
                  state 8192, 256 branches x 16 tokens) against the bf16 dense
-                 MFMA peak;
-  gdn_roofline   the Gated DeltaNet layer at config 2 (T=2048 prefill) against
-                 the HBM peak, from its compulsory bytes.
-cpu_baseline: transformers' Qwen3_5ForCausalLM in fp32 on the host cores, on
-the same checkpoint file and the same first request (the HF-batched method
-of the reference's benchmarks/benefit.py:77-92); it is also the parity check
-of the request's decision probabilities.
+                 MFMA peak, HIP events on its launch stream;
+  gdn_roofline   the Gated DeltaNet layer at config 2 (T=2048 prefill; and
+                 the 64 x 16 branches) against the HBM peak, from its
+                 compulsory bytes.
+cpu_baseline: transformers' Qwen3_5ForCausalLM in fp32 on every host core
+this process may use, on the same checkpoint file and the first request (the
+HF-batched method of the reference's benchmarks/benefit.py:77-92): one
+full-size warm-up, then 5 timed requests, p50; configs 1-3 one layer at a
+time beside it. The same fp32 run is the parity reference of the request's
+decision probabilities.
 
-The request loop runs in a child process that imports only numpy and the
+The request loops run in a child process that imports only numpy and the
 ctypes binding, as the reference's Python layer does (python/cujev/_lib.py,
 systemone.py): a process that imported torch first would run the engine on
 torch's bundled HIP runtime and hipBLASLt instead of the system ROCm's.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-config5]
 """
 from __future__ import annotations
 
@@ -48,20 +54,33 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
-STATE_TOKENS = 530
-BRANCH_TOKENS = 20
-LABELS = [3, 2, 2, 4]      # labels per question (Starfighter-style)
+# the request of each end-to-end workload and the engine capacities it runs at
+WORKLOADS = {
+    "config4": dict(preset="4b", ckpt="/tmp/cujev_synth_4b", state=530, branch=20,
+                    labels=[3, 2, 2, 4],
+                    opts=dict(max_state_tokens=1024, max_branch_tokens=256, max_branches=16,
+                              max_candidates=256)),
+    "config5": dict(preset="9b", ckpt="/tmp/cujev_synth_9b", state=8192, branch=16,
+                    labels=[8] * 256,
+                    opts=dict(max_state_tokens=8192, max_branch_tokens=4096, max_branches=256,
+                              max_candidates=8)),
+}
+STATE_TOKENS, BRANCH_TOKENS = 530, 20
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def make_request(rng, vocab):
-    state = [int(x) for x in rng.integers(1000, 60000, size=STATE_TOKENS)]
+def make_request(rng, vocab, wl="config4"):
+    """(state ids, [(branch ids, candidate ids)]) of one request: ids in
+    [1000, 60000) as in the reference's tests/python/test_engine.py:56-58,
+    distinct single-token labels in [16, 1000)."""
+    w = WORKLOADS[wl]
+    state = [int(x) for x in rng.integers(1000, 60000, size=w["state"])]
     branches = []
-    for n in LABELS:
-        toks = [int(x) for x in rng.integers(1000, 60000, size=BRANCH_TOKENS)]
+    for n in w["labels"]:
+        toks = [int(x) for x in rng.integers(1000, 60000, size=w["branch"])]
         cands = [int(x) for x in rng.choice(np.arange(16, 1000), size=n, replace=False)]
         branches.append((toks, cands))
     return state, branches
@@ -70,12 +89,11 @@ def make_request(rng, vocab):
 # --------------------------------------------------------------------------
 # end to end
 # --------------------------------------------------------------------------
-def run_e2e(ckpt, steps, warmup, seed=0):
+def run_e2e(ckpt, steps, warmup, wl="config4", seed=0, full_logits=True):
     from cujev import Branch, Engine
-    eng = Engine(ckpt, max_state_tokens=1024, max_branch_tokens=256, max_branches=16,
-                 max_candidates=256)
+    eng = Engine(ckpt, **WORKLOADS[wl]["opts"])
     rng = np.random.default_rng(seed)
-    reqs = [make_request(rng, eng.vocab_size) for _ in range(warmup + steps)]
+    reqs = [make_request(rng, eng.vocab_size, wl) for _ in range(warmup + steps)]
     first_out = None
     wall, gpu = [], []
     for i, (state, brs) in enumerate(reqs):
@@ -98,40 +116,49 @@ def run_e2e(ckpt, steps, warmup, seed=0):
         t0 = time.perf_counter()
         eng.eval([Branch(t, c) for t, c in brs])
         ev_only.append((time.perf_counter() - t0) * 1e3)
-    # full-vocabulary logits of the first request, for the parity check
+    # full-vocabulary logits of the first request: the parity check (config
+    # 4) or the readout property (candidate logits == full logits)
     state, brs = reqs[0]
     eng.prefill(state)
-    first_full = eng.eval_full_logits([Branch(t, []) for t, _ in brs])
-    info = dict(name=eng.name, weight_gib=eng.weight_bytes / 2 ** 30)
+    first_full = eng.eval_full_logits([Branch(t, []) for t, _ in brs]) if full_logits else None
+    checks = {"finite": bool(all(np.all(np.isfinite(o)) for o in first_out))}
+    if first_full is not None:
+        checks["candidates_equal_full_logits_max_abs"] = float(max(
+            np.abs(np.asarray(o) - first_full[i, c]).max() for i, (o, (_, c)) in
+            enumerate(zip(first_out, brs))))
+    info = dict(name=eng.name, weight_gib=eng.weight_bytes / 2 ** 30,
+                workspace_gib=eng.workspace_bytes / 2 ** 30)
     eng.close()
     return dict(wall_ms=wall, gpu_ms=gpu, eval_only_ms=ev_only, first_req=reqs[0],
-                first_out=first_out, first_full=first_full, info=info)
+                first_out=first_out, first_full=first_full, info=info, checks=checks)
 
 
 def e2e_child(a):
     """--e2e-child: the request loop without torch in the process; prints one
     JSON line, the full-vocabulary logits go to a .npy file."""
     assert "torch" not in sys.modules
-    r = run_e2e(a.ckpt, a.steps, a.warmup)
-    np.save(a.full_out, np.asarray(r["first_full"], np.float32), allow_pickle=False)
+    r = run_e2e(a.ckpt, a.steps, a.warmup, wl=a.workload)
+    if r["first_full"] is not None and a.workload == "config4":
+        np.save(a.full_out, np.asarray(r["first_full"], np.float32), allow_pickle=False)
     r["first_full"] = None
     r["first_out"] = [np.asarray(o, np.float64).tolist() for o in r["first_out"]]
     r["torch_loaded"] = "torch" in sys.modules
     print(json.dumps(r), flush=True)
 
 
-def run_e2e_in_child(ckpt, steps, warmup):
+def run_e2e_in_child(ckpt, steps, warmup, wl="config4"):
     import subprocess
     import tempfile
     with tempfile.TemporaryDirectory() as d:
         full = os.path.join(d, "full.npy")
         cmd = [sys.executable, str(Path(__file__).resolve()), "--e2e-child", "--ckpt", ckpt,
-               "--steps", str(steps), "--warmup", str(warmup), "--full-out", full]
+               "--workload", wl, "--steps", str(steps), "--warmup", str(warmup),
+               "--full-out", full]
         p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=sys.stderr, text=True)
         if p.returncode != 0:
-            raise SystemExit(f"e2e child failed with status {p.returncode}")
+            raise SystemExit(f"e2e child ({wl}) failed with status {p.returncode}")
         r = json.loads(p.stdout.strip().splitlines()[-1])
-        r["first_full"] = np.load(full, allow_pickle=False)
+        r["first_full"] = np.load(full, allow_pickle=False) if os.path.exists(full) else None
     r["first_out"] = [np.asarray(o) for o in r["first_out"]]
     return r
 
@@ -169,55 +196,59 @@ def _softmax(x):
     return p / p.sum()
 
 
-def cpu_baseline(ckpt, req, eng_out, eng_full):
-    """transformers fp32 on the host cores: the timed baseline and the parity
-    reference. transformers' own bf16 run on the same request is reported next
-    to the engine's deviation: on a random-init 32-layer model the bf16 rounding
-    of GEMM inputs alone moves logits by a few tenths, for any bf16 engine."""
+def cpu_baseline(ckpt, req, eng_out, eng_full, reps=5):
+    """transformers fp32 on every host core this process may use: the timed
+    baseline (p50 of `reps` requests after a full-size warm-up) and the
+    parity reference; configs 1-3 timed one layer at a time beside it.
+    transformers' own bf16 run on the same request is reported next to the
+    engine's deviation: on a random-init 32-layer model the bf16 rounding of
+    GEMM inputs alone moves logits by a few tenths, for any bf16 engine."""
     try:
-        import torch
-        from transformers import AutoModelForCausalLM
+        from cujev import cpu_baseline as cb
+        import transformers  # noqa: F401
     except Exception as e:  # pragma: no cover
         return None, {"error": f"CPU baseline unavailable: {e}"}
-    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16")))
-    torch.set_num_threads(threads)
+    info = cb.cpu_info()
     state, brs = req
-    ids = torch.tensor([state + t for t, _ in brs])
     t0 = time.perf_counter()
-    model = AutoModelForCausalLM.from_pretrained(ckpt, dtype=torch.float32).eval()
-    log(f"transformers fp32 loaded on CPU in {time.perf_counter() - t0:.1f}s ({threads} threads)")
-    with torch.no_grad():
-        model(ids[:, :8], logits_to_keep=1)  # warm-up
-        t0 = time.perf_counter()
-        lg32 = model(ids, logits_to_keep=1).logits[:, -1, :].double().numpy()
-        dt = time.perf_counter() - t0
-    del model
-    model = AutoModelForCausalLM.from_pretrained(ckpt, dtype=torch.bfloat16).eval()
-    with torch.no_grad():
-        lg16 = model(ids, logits_to_keep=1).logits[:, -1, :].double().numpy()
-    del model
+    r = cb.request_baseline(ckpt, state, brs, reps=reps, log=log)
+    lg32, lg16 = r["fp32_logits"], r["bf16_logits"]
+    layers = cb.layer_baselines(log=log)
+    log(f"cpu baseline legs took {time.perf_counter() - t0:.0f} s")
 
     def dev(logits_labels, logits_full):
         dp = max(float(np.abs(_softmax(logits_labels[i]) - _softmax(lg32[i, c])).max())
                  for i, (_, c) in enumerate(brs))
         agree = all(int(np.argmax(logits_labels[i])) == int(np.argmax(lg32[i, c]))
                     for i, (_, c) in enumerate(brs))
-        dl = float(np.abs(np.asarray(logits_full) - lg32).max())
+        full = np.asarray(logits_full, np.float64)
+        dl = float(np.abs(full - lg32).max())
+        l1 = max(float(np.abs(_softmax(full[i]) - _softmax(lg32[i])).sum())
+                 for i in range(len(brs)))
         return {"max_abs_dprob_labels": round(dp, 5), "argmax_identical": agree,
-                "max_abs_dlogit_full_vocab": round(dl, 4)}
+                "max_abs_dlogit_full_vocab": round(dl, 4),
+                "max_L1_full_vocab_distribution": round(l1, 4)}
 
     eng = dev([np.asarray(o, np.float64) for o in eng_out], eng_full)
     hf16 = dev([lg16[i, c] for i, (_, c) in enumerate(brs)], lg16)
     margins = [round(float(np.sort(lg32[i, c])[-1] - np.sort(lg32[i, c])[-2]), 4)
                for i, (_, c) in enumerate(brs)]
-    base = {"value": round(1.0 / dt, 5), "unit": "requests/s", "cores": threads,
+    p50 = statistics.median(r["times_s"])
+    w = WORKLOADS["config4"]
+    base = {"value": round(1.0 / p50, 5), "unit": "requests/s", "cores": r["threads"],
             "kind": "reference",
-            "sample": (f"1 request (4 branches x [{STATE_TOKENS}+{BRANCH_TOKENS}] tokens, one "
-                       f"batch, logits_to_keep=1) through transformers Qwen3_5ForCausalLM fp32 "
-                       f"on {threads} host threads: {dt:.1f} s"),
-            "ms_per_request": round(dt * 1e3, 1)}
+            "sample": (f"{reps} requests after one full-size warm-up, p50: each request = "
+                       f"{len(brs)} rows of [{w['state']}+{w['branch']}] tokens in one batch, "
+                       f"logits_to_keep=1, through transformers Qwen3_5ForCausalLM fp32 on "
+                       f"{r['threads']} host threads ({info['cpu_model']})"),
+            "ms_per_request_p50": round(p50 * 1e3, 1),
+            "ms_per_request_all": [round(t * 1e3, 1) for t in r["times_s"]],
+            "cpu_model": info["cpu_model"],
+            "layers": layers}
     parity = {"reference": "transformers Qwen3_5ForCausalLM fp32 (CPU), same checkpoint and request",
-              "engine": eng, "transformers_bf16": hf16, "label_top2_logit_margins": margins}
+              "engine": eng, "transformers_bf16": hf16, "label_top2_logit_margins": margins,
+              "reference_repo_bar": "full-vocabulary L1 to fp32 < 0.05 "
+                                    "(tests/python/oracle_fp32.py:52)"}
     return base, parity
 
 
@@ -265,7 +296,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--ckpt", default=os.environ.get("CUJEV_BENCH_CKPT", "/tmp/cujev_synth_4b"))
+    ap.add_argument("--ckpt", default=os.environ.get("CUJEV_BENCH_CKPT",
+                                                     WORKLOADS["config4"]["ckpt"]))
+    ap.add_argument("--ckpt9b", default=os.environ.get("CUJEV_BENCH_CKPT9B",
+                                                       WORKLOADS["config5"]["ckpt"]))
+    ap.add_argument("--no-config5", action="store_true", help="skip the 9B capacity line")
+    ap.add_argument("--config5-steps", type=int, default=5)
+    ap.add_argument("--workload", default="config4", help=argparse.SUPPRESS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--kernels-only", action="store_true",
@@ -321,6 +358,9 @@ def main():
                    "model": e2e["info"]["name"], "layers": 32, "hidden": 2560,
                    "vocab": 248320, "weights_gib": round(e2e["info"]["weight_gib"], 2)},
     }
+    res["e2e_checks"] = e2e["checks"]
+    if not a.no_config5:
+        res["config5"] = config5_line(a)
     if not a.no_kernels:
         res.update(kernel_rooflines())
     if not a.no_cpu_baseline:
@@ -329,8 +369,37 @@ def main():
         res["cpu_baseline"] = base
         res["parity"] = parity
         if base:
-            log(f"cpu baseline: {base['ms_per_request']:.0f} ms/request; parity {parity}")
+            log(f"cpu baseline: {base['ms_per_request_p50']:.0f} ms/request p50; parity {parity}")
     print(json.dumps(res), flush=True)
+
+
+def config5_line(a):
+    """Config 5: the 9B-shaped model (untied LM head) at capacity, a fresh
+    8192-token state + 256 branches x 16 tokens with 8 labels each per
+    request, in the torch-free child. The checkpoint is written once on the
+    device (torch's generator) and reused; there is no CPU leg at this size."""
+    import torch
+    from cujev import synthetic
+    t0 = time.perf_counter()
+    ckpt = synthetic.ensure_checkpoint(a.ckpt9b, "9b", seed=0, device="cuda")
+    torch.cuda.empty_cache()
+    log(f"9B checkpoint ready at {ckpt} ({time.perf_counter() - t0:.1f}s)")
+    r = run_e2e_in_child(ckpt, a.config5_steps, 1, wl="config5")
+    wall = r["wall_ms"]
+    ms, p50 = statistics.mean(wall), statistics.median(wall)
+    nb = len(WORKLOADS["config5"]["labels"])
+    log(f"config 5: {ms:.1f} ms/request mean, p50 {p50:.1f} ms, checks {r['checks']}")
+    return {"workload": "Qwen3.5-9B-shaped hybrid (hidden 4096, intermediate 12288, 32 layers, "
+                        "8 full attention, untied LM head), fresh 8192-token state prefill + 256 "
+                        "branches x 16 tokens, 8 labels per branch",
+            "requests_per_s": round(1e3 / ms, 3), "branch_decisions_per_s": round(nb * 1e3 / ms, 1),
+            "ms_per_request_mean": round(ms, 2), "p50_ms_per_request": round(p50, 2),
+            "gpu_ms_per_request_p50": round(statistics.median(r["gpu_ms"]), 2),
+            "eval_only_ms_p50": round(statistics.median(r["eval_only_ms"]), 2),
+            "steps": a.config5_steps, "warmup": 1, "checks": r["checks"],
+            "weights_gib": round(r["info"]["weight_gib"], 2),
+            "workspace_gib": round(r["info"]["workspace_gib"], 2),
+            "cpu_baseline": None}
 
 
 if __name__ == "__main__":

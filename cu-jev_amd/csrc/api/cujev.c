@@ -40,9 +40,9 @@ static void load_gemm_table(cujev_model *m) {
     }
     const int n = cujev_gemm_load_table(m->gemm, path);
     if (n >= 0)
-        cujev_log(m->opts.verbose, "gemm table: %d tuned shapes from %s", n, path);
+        cujev_note(m->opts.verbose, "gemm table: %d tuned shapes from %s", n, path);
     else if (n == -2)
-        cujev_log(1, "gemm table %s was made with another hipBLASLt version; ignored", path);
+        cujev_note(1, "gemm table %s was made with another hipBLASLt version; ignored", path);
 }
 
 API void cujev_model_close(cujev_model *m) {
@@ -54,8 +54,8 @@ API void cujev_model_close(cujev_model *m) {
     cujev_gemm_destroy(m->gemm);
     if (m->h_meta)
         hipHostFree(m->h_meta);
-    cujev_arena_free(&m->work);
-    cujev_arena_free(&m->weights);
+    cujev_slab_release(&m->work);
+    cujev_slab_release(&m->weights);
     if (m->ev0)
         hipEventDestroy(m->ev0);
     if (m->ev1)
@@ -67,11 +67,11 @@ API void cujev_model_close(cujev_model *m) {
 
 API cujev_status cujev_model_open(const char *dir, const cujev_options *opts, cujev_model **out) {
     if (!dir || !out)
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "null argument");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "null argument");
     *out = NULL;
     cujev_model *m = (cujev_model *)calloc(1, sizeof *m);
     if (!m)
-        return cujev_fail(CUJEV_ERR_OOM, "model struct");
+        return cujev_raise(CUJEV_ERR_OOM, "model struct");
     if (opts)
         m->opts = *opts;
     else
@@ -79,7 +79,7 @@ API cujev_status cujev_model_open(const char *dir, const cujev_options *opts, cu
     if (m->opts.max_state_tokens <= 0 || m->opts.max_branch_tokens <= 0 ||
         m->opts.max_branches <= 0 || m->opts.max_candidates < 0) {
         free(m);
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "capacities must be positive");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "capacities must be positive");
     }
     /* config first: fails before any device call */
     cujev_status s = cujev_config_load(dir, &m->cfg);
@@ -114,22 +114,22 @@ API cujev_status cujev_model_open(const char *dir, const cujev_options *opts, cu
     if (e != hipSuccess) {
         const int dev = m->opts.device;
         free(m);
-        return cujev_fail(CUJEV_ERR_CUDA, "hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+        return cujev_raise(CUJEV_ERR_CUDA, "hipSetDevice(%d): %s", dev, hipGetErrorString(e));
     }
     if ((e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking)) != hipSuccess ||
         (e = hipEventCreate(&m->ev0)) != hipSuccess || (e = hipEventCreate(&m->ev1)) != hipSuccess) {
         cujev_model_close(m);
-        return cujev_fail(CUJEV_ERR_CUDA, "stream/event creation: %s", hipGetErrorString(e));
+        return cujev_raise(CUJEV_ERR_CUDA, "stream/event creation: %s", hipGetErrorString(e));
     }
     s = cujev_model_load_weights(m, dir);
     if (s == CUJEV_OK)
         s = cujev_model_alloc_workspace(m);
     if (s == CUJEV_OK && cujev_gemm_create(&m->gemm, m->gemm_ws, m->gemm_ws_bytes) != 0)
-        s = cujev_fail(CUJEV_ERR_CUDA, "hipblasLtCreate failed");
+        s = cujev_raise(CUJEV_ERR_CUDA, "hipblasLtCreate failed");
     if (s == CUJEV_OK)
         load_gemm_table(m);
     if (s == CUJEV_OK && (e = hipStreamSynchronize(m->stream)) != hipSuccess)
-        s = cujev_fail(CUJEV_ERR_CUDA, "%s", hipGetErrorString(e));
+        s = cujev_raise(CUJEV_ERR_CUDA, "%s", hipGetErrorString(e));
     if (s != CUJEV_OK) {
         cujev_model_close(m);
         return s;
@@ -140,7 +140,7 @@ API cujev_status cujev_model_open(const char *dir, const cujev_options *opts, cu
 
 API cujev_status cujev_model_info_get(const cujev_model *m, cujev_model_info *o) {
     if (!m || !o)
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "null argument");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "null argument");
     memset(o, 0, sizeof *o);
     snprintf(o->name, sizeof o->name, "%s", m->cfg.name);
     o->hidden_size = m->cfg.hidden_size;
@@ -150,8 +150,8 @@ API cujev_status cujev_model_info_get(const cujev_model *m, cujev_model_info *o)
     o->max_state_tokens = m->opts.max_state_tokens;
     o->max_branch_tokens = m->opts.max_branch_tokens;
     o->max_branches = m->opts.max_branches;
-    o->device_bytes_weights = m->weights.used;
-    o->device_bytes_workspace = m->work.used;
+    o->device_bytes_weights = cujev_slab_used(&m->weights);
+    o->device_bytes_workspace = cujev_slab_used(&m->work);
     return CUJEV_OK;
 }
 
@@ -162,7 +162,7 @@ API void cujev_state_destroy(cujev_state *st) {
         hipStreamSynchronize(st->model->stream);
         cujev_graphs_forget(st->model, st);
     }
-    cujev_arena_free(&st->mem);
+    cujev_slab_release(&st->mem);
     free(st->kv_k);
     free(st->kv_vt);
     free(st->S);
@@ -172,11 +172,11 @@ API void cujev_state_destroy(cujev_state *st) {
 
 API cujev_status cujev_state_create(cujev_model *m, cujev_state **out) {
     if (!m || !out)
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "null argument");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "null argument");
     *out = NULL;
     cujev_state *st = (cujev_state *)calloc(1, sizeof *st);
     if (!st)
-        return cujev_fail(CUJEV_ERR_OOM, "state struct");
+        return cujev_raise(CUJEV_ERR_OOM, "state struct");
     st->model = m;
     const int L = m->cfg.num_layers;
     st->kv_k = (bf16_t **)calloc((size_t)L, sizeof(bf16_t *));
@@ -185,35 +185,35 @@ API cujev_status cujev_state_create(cujev_model *m, cujev_state **out) {
     st->conv = (float **)calloc((size_t)L, sizeof(float *));
     if (!st->kv_k || !st->kv_vt || !st->S || !st->conv) {
         cujev_state_destroy(st);
-        return cujev_fail(CUJEV_ERR_OOM, "state tables");
+        return cujev_raise(CUJEV_ERR_OOM, "state tables");
     }
     const size_t kv_bytes = (size_t)m->Hkv * m->state_stride * m->D * 2;
     const size_t S_bytes = (size_t)m->Hv * 128 * 128 * 4;
     const size_t conv_bytes = (size_t)m->C * 3 * 4;
-    size_t total = 0;
-    for (int l = 0; l < L; l++)
-        total += m->cfg.layer_types[l] == CUJEV_LAYER_FULL
-                     ? 2 * cujev_align_up(kv_bytes, 256)
-                     : cujev_align_up(S_bytes, 256) + cujev_align_up(conv_bytes, 256);
-    cujev_status s = cujev_arena_init(&st->mem, total + 4096);
-    if (s != CUJEV_OK) {
-        cujev_state_destroy(st);
-        return s;
-    }
-    for (int l = 0; l < L; l++) {
-        if (m->cfg.layer_types[l] == CUJEV_LAYER_FULL) {
-            st->kv_k[l] = (bf16_t *)cujev_arena_alloc(&st->mem, kv_bytes);
-            st->kv_vt[l] = (bf16_t *)cujev_arena_alloc(&st->mem, kv_bytes);
-        } else {
-            st->S[l] = (float *)cujev_arena_alloc(&st->mem, S_bytes);
-            st->conv[l] = (float *)cujev_arena_alloc(&st->mem, conv_bytes);
+    /* pass 0 plans the slab, pass 1 carves it */
+    for (int pass = 0; pass < 2; pass++) {
+        for (int l = 0; l < L; l++) {
+            if (m->cfg.layer_types[l] == CUJEV_LAYER_FULL) {
+                st->kv_k[l] = (bf16_t *)cujev_slab_take(&st->mem, kv_bytes);
+                st->kv_vt[l] = (bf16_t *)cujev_slab_take(&st->mem, kv_bytes);
+            } else {
+                st->S[l] = (float *)cujev_slab_take(&st->mem, S_bytes);
+                st->conv[l] = (float *)cujev_slab_take(&st->mem, conv_bytes);
+            }
+        }
+        if (pass == 0) {
+            const cujev_status s = cujev_slab_commit(&st->mem, "state");
+            if (s != CUJEV_OK) {
+                cujev_state_destroy(st);
+                return s;
+            }
         }
     }
     /* finite everywhere: attention tiles read masked keys past the prefix */
-    hipError_t e = hipMemset(st->mem.base, 0, st->mem.used);
+    hipError_t e = hipMemset(st->mem.base, 0, cujev_slab_used(&st->mem));
     if (e != hipSuccess) {
         cujev_state_destroy(st);
-        return cujev_fail(CUJEV_ERR_CUDA, "hipMemset state: %s", hipGetErrorString(e));
+        return cujev_raise(CUJEV_ERR_CUDA, "hipMemset state: %s", hipGetErrorString(e));
     }
     *out = st;
     return CUJEV_OK;
@@ -223,30 +223,30 @@ API int cujev_state_num_tokens(const cujev_state *st) { return st ? st->num_toke
 
 API cujev_status cujev_state_prefill(cujev_model *m, cujev_state *st, const int32_t *tokens, int N) {
     if (!m || !st || !tokens || N <= 0)
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "bad prefill arguments");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "bad prefill arguments");
     if (st->model != m)
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "state belongs to another model");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "state belongs to another model");
     if (N > m->opts.max_state_tokens)
-        return cujev_fail(CUJEV_ERR_CAPACITY, "state of %d tokens exceeds max_state_tokens=%d", N,
+        return cujev_raise(CUJEV_ERR_CAPACITY, "state of %d tokens exceeds max_state_tokens=%d", N,
                           m->opts.max_state_tokens);
     for (int i = 0; i < N; i++)
         if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size)
-            return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "token id %d out of range", tokens[i]);
+            return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "token id %d out of range", tokens[i]);
     const int32_t ss = 0, sl = N;
     st->num_tokens = 0;
-    HIP_TRY(hipEventRecord(m->ev0, m->stream));
+    HIP_CHECK(hipEventRecord(m->ev0, m->stream));
     cujev_status s = cujev_forward(m, st, CUJEV_FWD_PREFILL, tokens, N, &ss, &sl, 1);
     if (s != CUJEV_OK) {
         hipStreamSynchronize(m->stream);
         return s;
     }
-    HIP_TRY(hipEventRecord(m->ev1, m->stream));
-    HIP_TRY(hipStreamSynchronize(m->stream));
-    HIP_TRY(hipGetLastError());
+    HIP_CHECK(hipEventRecord(m->ev1, m->stream));
+    HIP_CHECK(hipStreamSynchronize(m->stream));
+    HIP_CHECK(hipGetLastError());
     hipEventElapsedTime(&m->timing.prefill_ms, m->ev0, m->ev1);
     m->timing.prefill_tokens = N;
     st->num_tokens = N;
-    cujev_clear_error();
+    cujev_error_reset();
     return CUJEV_OK;
 }
 
@@ -256,29 +256,29 @@ static cujev_status pack_branches(cujev_model *m, const cujev_branch *br, int B,
     long long N = 0;
     for (int b = 0; b < B; b++) {
         if (br[b].num_tokens <= 0 || !br[b].tokens)
-            return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "branch %d has no tokens", b);
+            return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "branch %d has no tokens", b);
         if (br[b].num_candidates < 0 || (br[b].num_candidates > 0 && !br[b].candidates))
-            return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "branch %d: bad candidates", b);
+            return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "branch %d: bad candidates", b);
         if (br[b].num_candidates > m->opts.max_candidates)
-            return cujev_fail(CUJEV_ERR_CAPACITY, "branch %d: %d candidates > max_candidates=%d",
+            return cujev_raise(CUJEV_ERR_CAPACITY, "branch %d: %d candidates > max_candidates=%d",
                               b, br[b].num_candidates, m->opts.max_candidates);
         seg_start[b] = (int32_t)N;
         seg_len[b] = br[b].num_tokens;
         N += br[b].num_tokens;
     }
     if (N > m->opts.max_branch_tokens)
-        return cujev_fail(CUJEV_ERR_CAPACITY, "%lld branch tokens exceed max_branch_tokens=%d", N,
+        return cujev_raise(CUJEV_ERR_CAPACITY, "%lld branch tokens exceed max_branch_tokens=%d", N,
                           m->opts.max_branch_tokens);
     int32_t *t = (int32_t *)malloc((size_t)N * 4);
     if (!t)
-        return cujev_fail(CUJEV_ERR_OOM, "token staging");
+        return cujev_raise(CUJEV_ERR_OOM, "token staging");
     for (int b = 0; b < B; b++)
         memcpy(t + seg_start[b], br[b].tokens, (size_t)br[b].num_tokens * 4);
     for (long long i = 0; i < N; i++)
         if (t[i] < 0 || t[i] >= m->cfg.vocab_size) {
             const int32_t bad = t[i];
             free(t);
-            return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "token id %d out of range", bad);
+            return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "token id %d out of range", bad);
         }
     *tok = t;
     *N_out = (int)N;
@@ -288,25 +288,25 @@ static cujev_status pack_branches(cujev_model *m, const cujev_branch *br, int B,
 static cujev_status check_eval_args(cujev_model *m, cujev_state *st, const cujev_branch *br,
                                     int B) {
     if (!m || !st || !br || B <= 0)
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "bad eval arguments");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "bad eval arguments");
     if (st->model != m)
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "state belongs to another model");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "state belongs to another model");
     if (st->num_tokens == 0)
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "state has not been prefilled");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "state has not been prefilled");
     if (B > m->opts.max_branches)
-        return cujev_fail(CUJEV_ERR_CAPACITY, "%d branches > max_branches=%d", B,
+        return cujev_raise(CUJEV_ERR_CAPACITY, "%d branches > max_branches=%d", B,
                           m->opts.max_branches);
     return CUJEV_OK;
 }
 
 API cujev_status cujev_eval(cujev_model *m, cujev_state *st, const cujev_branch *br, int B,
                             float *logits_out, int ld) {
-    CUJEV_TRY(check_eval_args(m, st, br, B));
+    CJ_CHECK(check_eval_args(m, st, br, B));
     if (!logits_out)
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "logits_out is NULL");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "logits_out is NULL");
     int32_t *seg = (int32_t *)malloc((size_t)B * 2 * 4);
     if (!seg)
-        return cujev_fail(CUJEV_ERR_OOM, "segment table");
+        return cujev_raise(CUJEV_ERR_OOM, "segment table");
     int32_t *seg_start = seg, *seg_len = seg + B;
     int32_t *tok = NULL, *cand = NULL, *ncand = NULL;
     int N = 0, maxc = 0;
@@ -317,13 +317,13 @@ API cujev_status cujev_eval(cujev_model *m, cujev_state *st, const cujev_branch 
         if (br[b].num_candidates > maxc)
             maxc = br[b].num_candidates;
     if (ld < maxc) {
-        s = cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "ld=%d < max candidates=%d", ld, maxc);
+        s = cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "ld=%d < max candidates=%d", ld, maxc);
         goto out;
     }
     if (maxc > 0) {
         cand = (int32_t *)calloc((size_t)B * maxc + B, 4);
         if (!cand) {
-            s = cujev_fail(CUJEV_ERR_OOM, "candidate staging");
+            s = cujev_raise(CUJEV_ERR_OOM, "candidate staging");
             goto out;
         }
         ncand = cand + (size_t)B * maxc;
@@ -332,7 +332,7 @@ API cujev_status cujev_eval(cujev_model *m, cujev_state *st, const cujev_branch 
             for (int i = 0; i < br[b].num_candidates; i++) {
                 const int32_t id = br[b].candidates[i];
                 if (id < 0 || id >= m->cfg.vocab_size) {
-                    s = cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "candidate id %d out of range", id);
+                    s = cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "candidate id %d out of range", id);
                     goto out;
                 }
                 cand[(size_t)b * maxc + i] = id;
@@ -342,7 +342,7 @@ API cujev_status cujev_eval(cujev_model *m, cujev_state *st, const cujev_branch 
     {
         hipError_t e = hipEventRecord(m->ev0, m->stream);
         if (e != hipSuccess) {
-            s = cujev_fail(CUJEV_ERR_CUDA, "hipEventRecord: %s", hipGetErrorString(e));
+            s = cujev_raise(CUJEV_ERR_CUDA, "hipEventRecord: %s", hipGetErrorString(e));
             goto out;
         }
         int32_t *d_cand = NULL, *d_ncand = NULL;
@@ -354,19 +354,19 @@ API cujev_status cujev_eval(cujev_model *m, cujev_state *st, const cujev_branch 
             e = hipMemcpy2DAsync(logits_out, (size_t)ld * 4, m->d_logits, (size_t)maxc * 4,
                                  (size_t)maxc * 4, (size_t)B, hipMemcpyDeviceToHost, m->stream);
             if (e != hipSuccess) {
-                s = cujev_fail(CUJEV_ERR_CUDA, "readout: %s", hipGetErrorString(e));
+                s = cujev_raise(CUJEV_ERR_CUDA, "readout: %s", hipGetErrorString(e));
                 goto sync_out;
             }
         }
         if ((e = hipEventRecord(m->ev1, m->stream)) != hipSuccess ||
             (e = hipStreamSynchronize(m->stream)) != hipSuccess) {
-            s = cujev_fail(CUJEV_ERR_CUDA, "eval: %s", hipGetErrorString(e));
+            s = cujev_raise(CUJEV_ERR_CUDA, "eval: %s", hipGetErrorString(e));
             goto out;
         }
         hipEventElapsedTime(&m->timing.eval_ms, m->ev0, m->ev1);
         m->timing.eval_tokens = N;
         m->timing.eval_branches = B;
-        cujev_clear_error();
+        cujev_error_reset();
         goto out;
     }
 sync_out:
@@ -380,12 +380,12 @@ out:
 
 API cujev_status cujev_eval_full_logits(cujev_model *m, cujev_state *st, const cujev_branch *br,
                                         int B, float *logits_out) {
-    CUJEV_TRY(check_eval_args(m, st, br, B));
+    CJ_CHECK(check_eval_args(m, st, br, B));
     if (!logits_out)
-        return cujev_fail(CUJEV_ERR_INVALID_ARGUMENT, "logits_out is NULL");
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "logits_out is NULL");
     int32_t *seg = (int32_t *)malloc((size_t)B * 2 * 4);
     if (!seg)
-        return cujev_fail(CUJEV_ERR_OOM, "segment table");
+        return cujev_raise(CUJEV_ERR_OOM, "segment table");
     int32_t *tok = NULL;
     int N = 0;
     const int V = m->cfg.vocab_size, H = m->cfg.hidden_size;
@@ -406,12 +406,12 @@ API cujev_status cujev_eval_full_logits(cujev_model *m, cujev_state *st, const c
         if (s == CUJEV_OK && e == hipSuccess)
             e = e2;
         if (s == CUJEV_OK && e != hipSuccess)
-            s = cujev_fail(CUJEV_ERR_CUDA, "full logits: %s", hipGetErrorString(e));
+            s = cujev_raise(CUJEV_ERR_CUDA, "full logits: %s", hipGetErrorString(e));
         if (s == CUJEV_OK) {
             hipEventElapsedTime(&m->timing.eval_ms, m->ev0, m->ev1);
             m->timing.eval_tokens = N;
             m->timing.eval_branches = B;
-            cujev_clear_error();
+            cujev_error_reset();
         }
     }
     free(tok);

@@ -6,7 +6,7 @@
  * per kv-head, conv 4) are enforced here, before any device call. */
 #include "core/config.h"
 #include "core/json.h"
-#include "core/util.h"
+#include "core/devmem.h"
 
 static int geti(const js_node *o, const char *k, int dflt) {
     const js_node *v = js_get(o, k);
@@ -25,7 +25,7 @@ cujev_status cujev_config_parse(const char *text, size_t len, const char *what, 
     char err[256];
     js_doc *doc = js_parse(text, len, err, sizeof err);
     if (!doc)
-        return cujev_fail(CUJEV_ERR_FORMAT, "%s: invalid JSON (%s)", what, err);
+        return cujev_raise(CUJEV_ERR_FORMAT, "%s: invalid JSON (%s)", what, err);
     const js_node *root = js_root(doc);
     const js_node *t = js_get(root, "text_config");
     if (!js_is(t, JS_OBJ))
@@ -35,7 +35,7 @@ cujev_status cujev_config_parse(const char *text, size_t len, const char *what, 
 
     const js_node *mt = js_get(t, "model_type");
     if (!js_is(mt, JS_STR) || strncmp(mt->str, "qwen3_5", 7) != 0) {
-        st = cujev_fail(CUJEV_ERR_UNSUPPORTED, "model_type %s is not qwen3_5",
+        st = cujev_raise(CUJEV_ERR_UNSUPPORTED, "model_type %s is not qwen3_5",
                         js_is(mt, JS_STR) ? mt->str : "(missing)");
         goto done;
     }
@@ -62,13 +62,13 @@ cujev_status cujev_config_parse(const char *text, size_t len, const char *what, 
     {
         const js_node *lt = js_get(t, "layer_types");
         if (!js_is(lt, JS_ARR) || lt->count != c->num_layers || c->num_layers > CUJEV_MAX_LAYERS) {
-            st = cujev_fail(CUJEV_ERR_FORMAT, "%s: layer_types missing or wrong length", what);
+            st = cujev_raise(CUJEV_ERR_FORMAT, "%s: layer_types missing or wrong length", what);
             goto done;
         }
         int i = 0;
         for (const js_node *e = lt->child; e; e = e->next, i++) {
             if (!js_is(e, JS_STR)) {
-                st = cujev_fail(CUJEV_ERR_FORMAT, "%s: layer_types[%d] is not a string", what, i);
+                st = cujev_raise(CUJEV_ERR_FORMAT, "%s: layer_types[%d] is not a string", what, i);
                 goto done;
             }
             if (strcmp(e->str, "full_attention") == 0) {
@@ -78,7 +78,7 @@ cujev_status cujev_config_parse(const char *text, size_t len, const char *what, 
                 c->layer_types[i] = CUJEV_LAYER_LINEAR;
                 c->num_linear_layers++;
             } else {
-                st = cujev_fail(CUJEV_ERR_UNSUPPORTED, "layer type %s", e->str);
+                st = cujev_raise(CUJEV_ERR_UNSUPPORTED, "layer type %s", e->str);
                 goto done;
             }
         }
@@ -86,32 +86,32 @@ cujev_status cujev_config_parse(const char *text, size_t len, const char *what, 
     if (c->hidden_size <= 0 || c->num_layers <= 0 || c->vocab_size <= 0 || c->num_heads <= 0 ||
         c->num_kv_heads <= 0 || c->lin_num_v_heads <= 0 || c->lin_num_k_heads <= 0 ||
         c->intermediate_size <= 0) {
-        st = cujev_fail(CUJEV_ERR_FORMAT, "%s: missing required fields", what);
+        st = cujev_raise(CUJEV_ERR_FORMAT, "%s: missing required fields", what);
         goto done;
     }
     if (c->lin_num_v_heads % c->lin_num_k_heads != 0 || c->num_heads % c->num_kv_heads != 0) {
-        st = cujev_fail(CUJEV_ERR_UNSUPPORTED, "head counts must divide");
+        st = cujev_raise(CUJEV_ERR_UNSUPPORTED, "head counts must divide");
         goto done;
     }
     if (c->lin_k_dim != 128 || c->lin_v_dim != 128 || c->head_dim != 256 || c->rotary_dim != 64) {
-        st = cujev_fail(CUJEV_ERR_UNSUPPORTED,
+        st = cujev_raise(CUJEV_ERR_UNSUPPORTED,
                         "kernels are specialised for k=v=128, head_dim=256, rotary=64 "
                         "(got %d/%d/%d/%d)",
                         c->lin_k_dim, c->lin_v_dim, c->head_dim, c->rotary_dim);
         goto done;
     }
     if (c->num_heads / c->num_kv_heads != 4) {
-        st = cujev_fail(CUJEV_ERR_UNSUPPORTED,
+        st = cujev_raise(CUJEV_ERR_UNSUPPORTED,
                         "attention kernel needs 4 q-heads per kv-head (got %d)",
                         c->num_heads / c->num_kv_heads);
         goto done;
     }
     if (c->lin_conv_kernel != 4) {
-        st = cujev_fail(CUJEV_ERR_UNSUPPORTED, "conv kernel %d (need 4)", c->lin_conv_kernel);
+        st = cujev_raise(CUJEV_ERR_UNSUPPORTED, "conv kernel %d (need 4)", c->lin_conv_kernel);
         goto done;
     }
     if (c->hidden_size % 8 || c->intermediate_size % 4 || c->hidden_size > 16384) {
-        st = cujev_fail(CUJEV_ERR_UNSUPPORTED, "hidden %d / intermediate %d not supported",
+        st = cujev_raise(CUJEV_ERR_UNSUPPORTED, "hidden %d / intermediate %d not supported",
                         c->hidden_size, c->intermediate_size);
         goto done;
     }
@@ -137,24 +137,24 @@ cujev_status cujev_config_load(const char *dir, cujev_config *c) {
     snprintf(path, sizeof path, "%s/config.json", dir);
     FILE *f = fopen(path, "rb");
     if (!f)
-        return cujev_fail(CUJEV_ERR_IO, "cannot read %s", path);
+        return cujev_raise(CUJEV_ERR_IO, "cannot read %s", path);
     fseek(f, 0, SEEK_END);
     long n = ftell(f);
     fseek(f, 0, SEEK_SET);
     if (n < 0) {
         fclose(f);
-        return cujev_fail(CUJEV_ERR_IO, "cannot read %s", path);
+        return cujev_raise(CUJEV_ERR_IO, "cannot read %s", path);
     }
     char *buf = (char *)malloc((size_t)n + 1);
     if (!buf) {
         fclose(f);
-        return cujev_fail(CUJEV_ERR_OOM, "config buffer");
+        return cujev_raise(CUJEV_ERR_OOM, "config buffer");
     }
     size_t got = fread(buf, 1, (size_t)n, f);
     fclose(f);
     if (got != (size_t)n) {
         free(buf);
-        return cujev_fail(CUJEV_ERR_IO, "short read of %s", path);
+        return cujev_raise(CUJEV_ERR_IO, "short read of %s", path);
     }
     buf[n] = 0;
     cujev_status s = cujev_config_parse(buf, (size_t)n, path, c);

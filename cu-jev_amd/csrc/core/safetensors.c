@@ -1,6 +1,6 @@
 #include "core/safetensors.h"
 #include "core/json.h"
-#include "core/util.h"
+#include "core/devmem.h"
 #include <dirent.h>
 #include <fcntl.h>
 #include <sys/mman.h>
@@ -25,8 +25,12 @@ static void st_file_close(st_file *f) {
     free(f);
 }
 
-static int cmp_tensor(const void *a, const void *b) {
-    return strcmp(((const st_tensor *)a)->name, ((const st_tensor *)b)->name);
+/* FNV-1a over the name bytes. */
+static uint32_t name_hash(const char *s) {
+    uint32_t h = 2166136261u;
+    for (; *s; s++)
+        h = (h ^ (uint8_t)*s) * 16777619u;
+    return h;
 }
 
 static st_dtype parse_dtype(const char *s) {
@@ -46,37 +50,37 @@ static size_t dtype_size(st_dtype d) { return d == ST_F32 ? 4 : 2; }
 static cujev_status open_file(st_bundle *b, const char *path, int *cap) {
     st_file *f = (st_file *)calloc(1, sizeof *f);
     if (!f)
-        return cujev_fail(CUJEV_ERR_OOM, "st_file");
+        return cujev_raise(CUJEV_ERR_OOM, "st_file");
     f->fd = open(path, O_RDONLY);
     cujev_status s = CUJEV_OK;
     int appended = 0;
     if (f->fd < 0) {
-        s = cujev_fail(CUJEV_ERR_IO, "open %s failed", path);
+        s = cujev_raise(CUJEV_ERR_IO, "open %s failed", path);
         goto fail;
     }
     struct stat stt;
     if (fstat(f->fd, &stt) != 0 || stt.st_size < 8) {
-        s = cujev_fail(CUJEV_ERR_FORMAT, "%s: too small", path);
+        s = cujev_raise(CUJEV_ERR_FORMAT, "%s: too small", path);
         goto fail;
     }
     f->size = (size_t)stt.st_size;
     f->map = mmap(NULL, f->size, PROT_READ, MAP_PRIVATE, f->fd, 0);
     if (f->map == MAP_FAILED) {
         f->map = NULL;
-        s = cujev_fail(CUJEV_ERR_IO, "mmap %s failed", path);
+        s = cujev_raise(CUJEV_ERR_IO, "mmap %s failed", path);
         goto fail;
     }
     uint64_t hlen;
     memcpy(&hlen, f->map, 8);
     if (hlen > f->size - 8) {
-        s = cujev_fail(CUJEV_ERR_FORMAT, "%s: bad header length", path);
+        s = cujev_raise(CUJEV_ERR_FORMAT, "%s: bad header length", path);
         goto fail;
     }
     {
         char err[256];
         f->header = js_parse((const char *)f->map + 8, (size_t)hlen, err, sizeof err);
         if (!f->header || !js_is(js_root(f->header), JS_OBJ)) {
-            s = cujev_fail(CUJEV_ERR_FORMAT, "%s: header is not a JSON object", path);
+            s = cujev_raise(CUJEV_ERR_FORMAT, "%s: header is not a JSON object", path);
             goto fail;
         }
     }
@@ -90,7 +94,7 @@ static cujev_status open_file(st_bundle *b, const char *path, int *cap) {
                           *off = js_get(e, "data_offsets");
             if (!js_is(dt, JS_STR) || !js_is(sh, JS_ARR) || !js_is(off, JS_ARR) ||
                 off->count != 2 || sh->count > 8) {
-                s = cujev_fail(CUJEV_ERR_FORMAT, "%s: malformed entry %s", path, e->key);
+                s = cujev_raise(CUJEV_ERR_FORMAT, "%s: malformed entry %s", path, e->key);
                 goto fail;
             }
             st_tensor t;
@@ -102,22 +106,23 @@ static cujev_status open_file(st_bundle *b, const char *path, int *cap) {
             int i = 0;
             for (const js_node *d = sh->child; d; d = d->next, i++) {
                 if (!js_is(d, JS_NUM) || d->num < 0) {
-                    s = cujev_fail(CUJEV_ERR_FORMAT, "%s: bad shape of %s", path, e->key);
+                    s = cujev_raise(CUJEV_ERR_FORMAT, "%s: bad shape of %s", path, e->key);
                     goto fail;
                 }
                 t.shape[i] = (int64_t)d->num;
                 numel *= (size_t)t.shape[i];
             }
+            t.numel = numel;
             const js_node *o0 = js_at(off, 0), *o1 = js_at(off, 1);
             if (!js_is(o0, JS_NUM) || !js_is(o1, JS_NUM) || o0->num < 0 || o1->num < o0->num ||
                 (size_t)o1->num > data_size) {
-                s = cujev_fail(CUJEV_ERR_FORMAT, "%s: tensor %s offsets out of range", path, e->key);
+                s = cujev_raise(CUJEV_ERR_FORMAT, "%s: tensor %s offsets out of range", path, e->key);
                 goto fail;
             }
             t.data = base + (size_t)o0->num;
             t.nbytes = (size_t)o1->num - (size_t)o0->num;
             if (t.dtype != ST_OTHER && t.nbytes != numel * dtype_size(t.dtype)) {
-                s = cujev_fail(CUJEV_ERR_FORMAT, "%s: tensor %s size does not match its shape",
+                s = cujev_raise(CUJEV_ERR_FORMAT, "%s: tensor %s size does not match its shape",
                                path, e->key);
                 goto fail;
             }
@@ -125,7 +130,7 @@ static cujev_status open_file(st_bundle *b, const char *path, int *cap) {
                 int nc = *cap ? *cap * 2 : 256;
                 st_tensor *nt = (st_tensor *)realloc(b->tensors, (size_t)nc * sizeof(st_tensor));
                 if (!nt) {
-                    s = cujev_fail(CUJEV_ERR_OOM, "tensor table");
+                    s = cujev_raise(CUJEV_ERR_OOM, "tensor table");
                     goto fail;
                 }
                 b->tensors = nt;
@@ -138,7 +143,7 @@ static cujev_status open_file(st_bundle *b, const char *path, int *cap) {
     {
         st_file **nf = (st_file **)realloc(b->files, (size_t)(b->num_files + 1) * sizeof(st_file *));
         if (!nf) {
-            s = cujev_fail(CUJEV_ERR_OOM, "file table");
+            s = cujev_raise(CUJEV_ERR_OOM, "file table");
             goto fail;
         }
         b->files = nf;
@@ -155,7 +160,7 @@ cujev_status st_bundle_open(const char *dir, st_bundle *b) {
     memset(b, 0, sizeof *b);
     DIR *d = opendir(dir);
     if (!d)
-        return cujev_fail(CUJEV_ERR_IO, "cannot open directory %s", dir);
+        return cujev_raise(CUJEV_ERR_IO, "cannot open directory %s", dir);
     int cap = 0, nfound = 0;
     cujev_status s = CUJEV_OK;
     struct dirent *de;
@@ -171,40 +176,49 @@ cujev_status st_bundle_open(const char *dir, st_bundle *b) {
     }
     closedir(d);
     if (s == CUJEV_OK && nfound == 0)
-        s = cujev_fail(CUJEV_ERR_IO, "no *.safetensors in %s", dir);
+        s = cujev_raise(CUJEV_ERR_IO, "no *.safetensors in %s", dir);
     if (s != CUJEV_OK) {
-        st_bundle_close(b);
+        st_bundle_release(b);
         return s;
     }
-    qsort(b->tensors, (size_t)b->num_tensors, sizeof(st_tensor), cmp_tensor);
-    for (int i = 1; i < b->num_tensors; i++)
-        if (strcmp(b->tensors[i - 1].name, b->tensors[i].name) == 0) {
-            s = cujev_fail(CUJEV_ERR_FORMAT, "tensor %s appears twice", b->tensors[i].name);
-            st_bundle_close(b);
-            return s;
-        }
+    /* index: linear probing in a table at most half full */
+    uint32_t nslots = 16;
+    while (nslots < 2u * (uint32_t)b->num_tensors)
+        nslots <<= 1;
+    b->slots = (int32_t *)malloc(nslots * sizeof(int32_t));
+    if (!b->slots) {
+        st_bundle_release(b);
+        return cujev_raise(CUJEV_ERR_OOM, "tensor index");
+    }
+    memset(b->slots, 0xff, nslots * sizeof(int32_t));
+    b->slot_mask = nslots - 1;
+    for (int i = 0; i < b->num_tensors; i++) {
+        uint32_t k = name_hash(b->tensors[i].name) & b->slot_mask;
+        for (; b->slots[k] >= 0; k = (k + 1) & b->slot_mask)
+            if (strcmp(b->tensors[b->slots[k]].name, b->tensors[i].name) == 0) {
+                s = cujev_raise(CUJEV_ERR_FORMAT, "tensor %s appears twice", b->tensors[i].name);
+                st_bundle_release(b);
+                return s;
+            }
+        b->slots[k] = i;
+    }
     return CUJEV_OK;
 }
 
-void st_bundle_close(st_bundle *b) {
+void st_bundle_release(st_bundle *b) {
     for (int i = 0; i < b->num_files; i++)
         st_file_close(b->files[i]);
     free(b->files);
     free(b->tensors);
+    free(b->slots);
     memset(b, 0, sizeof *b);
 }
 
-const st_tensor *st_bundle_find(const st_bundle *b, const char *name) {
-    st_tensor key;
-    memset(&key, 0, sizeof key);
-    key.name = name;
-    return (const st_tensor *)bsearch(&key, b->tensors, (size_t)b->num_tensors, sizeof(st_tensor),
-                                      cmp_tensor);
-}
-
-size_t st_numel(const st_tensor *t) {
-    size_t n = 1;
-    for (int i = 0; i < t->ndim; i++)
-        n *= (size_t)t->shape[i];
-    return n;
+const st_tensor *st_lookup(const st_bundle *b, const char *name) {
+    if (!b->slots)
+        return NULL;
+    for (uint32_t k = name_hash(name) & b->slot_mask; b->slots[k] >= 0; k = (k + 1) & b->slot_mask)
+        if (strcmp(b->tensors[b->slots[k]].name, name) == 0)
+            return &b->tensors[b->slots[k]];
+    return NULL;
 }

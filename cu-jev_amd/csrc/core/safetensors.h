@@ -20,6 +20,7 @@ typedef struct st_tensor {
     st_dtype dtype;
     int ndim;
     int64_t shape[8];
+    size_t numel;     /* product of shape */
     const void *data; /* inside the mmap */
     size_t nbytes;
 } st_tensor;
@@ -29,14 +30,18 @@ typedef struct st_file st_file;
 typedef struct st_bundle {
     st_file **files;
     int num_files;
-    st_tensor *tensors; /* sorted by name */
+    st_tensor *tensors; /* in file order */
     int num_tensors;
+    int32_t *slots;     /* open-addressing index: tensor number or -1 */
+    uint32_t slot_mask; /* slot count - 1 (a power of two, >= 2 x tensors) */
 } st_bundle;
 
+/* Maps every *.safetensors of `dir` and indexes their tensors by name; a name
+ * that appears twice is a FORMAT error. */
 cujev_status st_bundle_open(const char *dir, st_bundle *out);
-void st_bundle_close(st_bundle *b);
-const st_tensor *st_bundle_find(const st_bundle *b, const char *name);
-size_t st_numel(const st_tensor *t);
+void st_bundle_release(st_bundle *b);
+/* The tensor called `name`, or NULL. */
+const st_tensor *st_lookup(const st_bundle *b, const char *name);
 
 #ifdef __cplusplus
 }

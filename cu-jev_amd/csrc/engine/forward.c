@@ -27,7 +27,7 @@ static int debug_sync_enabled(void) {
 
 static cujev_status check(cujev_model *m, hipError_t launch, const char *what, int layer) {
     if (launch != hipSuccess)
-        return cujev_fail(launch == hipErrorInvalidValue ? CUJEV_ERR_UNSUPPORTED : CUJEV_ERR_CUDA,
+        return cujev_raise(launch == hipErrorInvalidValue ? CUJEV_ERR_UNSUPPORTED : CUJEV_ERR_CUDA,
                           "%s (layer %d): %s", what, layer, hipGetErrorString(launch));
     if (!debug_sync_enabled())
         return CUJEV_OK;
@@ -35,11 +35,11 @@ static cujev_status check(cujev_model *m, hipError_t launch, const char *what, i
     if (e == hipSuccess)
         e = hipGetLastError();
     if (e != hipSuccess)
-        return cujev_fail(CUJEV_ERR_CUDA, "%s (layer %d): %s", what, layer, hipGetErrorString(e));
+        return cujev_raise(CUJEV_ERR_CUDA, "%s (layer %d): %s", what, layer, hipGetErrorString(e));
     return CUJEV_OK;
 }
 
-#define K_TRY(call, what, layer) CUJEV_TRY(check(m, (call), (what), (layer)))
+#define K_TRY(call, what, layer) CJ_CHECK(check(m, (call), (what), (layer)))
 
 /* Everything the launch sequence needs besides the model and the state. */
 typedef struct {
@@ -216,10 +216,13 @@ static cujev_status run_eval(cujev_model *m, cujev_state *st, const fwd_launch *
         return launch_all(m, st, a);
     cujev_graph_slot *g = NULL, *victim = &m->graphs[0];
     const int has_cand = a->cand != NULL;
+    /* a packed and an unpacked table can have the same chunk count, but
+     * their metadata sits at other offsets of the uploaded block */
+    const int packed = a->chunks.chunk_starts != NULL;
     for (int i = 0; i < CUJEV_GRAPH_SLOTS; i++) {
         cujev_graph_slot *x = &m->graphs[i];
         if (x->st == st && x->P == a->P && x->N == a->N && x->B == a->B && x->nc == a->nc &&
-            x->maxc == a->maxc && x->has_cand == has_cand) {
+            x->maxc == a->maxc && x->has_cand == has_cand && x->packed == packed) {
             g = x;
             break;
         }
@@ -238,12 +241,13 @@ static cujev_status run_eval(cujev_model *m, cujev_state *st, const fwd_launch *
         g->nc = a->nc;
         g->maxc = a->maxc;
         g->has_cand = has_cand;
+        g->packed = packed;
     }
     g->stamp = ++m->graph_clock;
     if (g->exec) {
         hipError_t e = hipGraphLaunch(g->exec, m->stream);
         return e == hipSuccess ? CUJEV_OK
-                               : cujev_fail(CUJEV_ERR_CUDA, "hipGraphLaunch: %s",
+                               : cujev_raise(CUJEV_ERR_CUDA, "hipGraphLaunch: %s",
                                             hipGetErrorString(e));
     }
     if (g->seen == 0 || g->seen < 0) {
@@ -271,7 +275,7 @@ static cujev_status run_eval(cujev_model *m, cujev_state *st, const fwd_launch *
     if (graph)
         hipGraphDestroy(graph);
     if (e != hipSuccess) { /* not capturable here: this shape stays eager */
-        cujev_log(1, "eval graph capture failed (%s); shape N=%d B=%d runs eagerly",
+        cujev_note(1, "eval graph capture failed (%s); shape N=%d B=%d runs eagerly",
                   hipGetErrorString(e), a->N, a->B);
         (void)hipGetLastError();
         g->seen = -1;
@@ -280,7 +284,7 @@ static cujev_status run_eval(cujev_model *m, cujev_state *st, const fwd_launch *
     g->exec = exec;
     e = hipGraphLaunch(exec, m->stream);
     return e == hipSuccess ? CUJEV_OK
-                           : cujev_fail(CUJEV_ERR_CUDA, "hipGraphLaunch: %s", hipGetErrorString(e));
+                           : cujev_raise(CUJEV_ERR_CUDA, "hipGraphLaunch: %s", hipGetErrorString(e));
 }
 
 cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
@@ -295,7 +299,7 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
     for (int b = 0; b < B; b++)
         nc += (seg_len[b] + 63) / 64;
     if (nc > m->max_chunks)
-        return cujev_fail(CUJEV_ERR_CAPACITY, "%d GDN chunks exceed %d", nc, m->max_chunks);
+        return cujev_raise(CUJEV_ERR_CAPACITY, "%d GDN chunks exceed %d", nc, m->max_chunks);
     /* Eval branches that each fit a 64-token chunk: consecutive whole
      * segments share a chunk (they all continue the stored state and write
      * none back), so a scan chunk holds up to 64 tokens however short the
@@ -336,7 +340,7 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
     const size_t o_cand = o; o += cand ? (size_t)B * maxc : 0;
     const size_t o_ncand = o; o += cand ? (size_t)B : 0;
     if (o > m->meta_ints)
-        return cujev_fail(CUJEV_ERR_CAPACITY, "per-call metadata exceeds its buffer");
+        return cujev_raise(CUJEV_ERR_CAPACITY, "per-call metadata exceeds its buffer");
     memcpy(h + o_tok, tokens, (size_t)N * 4);
     int ci = 0;
     for (int b = 0; b < B; b++) {
@@ -378,7 +382,7 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
         memcpy(h + o_cand, cand, (size_t)B * maxc * 4);
         memcpy(h + o_ncand, ncand, (size_t)B * 4);
     }
-    HIP_TRY(hipMemcpyAsync(m->d_meta, h, o * 4, hipMemcpyHostToDevice, m->stream));
+    HIP_CHECK(hipMemcpyAsync(m->d_meta, h, o * 4, hipMemcpyHostToDevice, m->stream));
     const int32_t *d = m->d_meta;
     if (d_cand) {
         *d_cand = cand ? m->d_meta + o_cand : NULL;

@@ -3,9 +3,10 @@
  * Behaviour of REF src/engine/model.c:161-247 (which tensors, the "model." or
  * "model.language_model." prefix, tied embeddings, row-fused q|k|v, qkv|z|b|a
  * and gate|up, +1 on the zero-centred norms, A_neg_exp = -exp(A_log)) and
- * :249-313 (one workspace arena for the largest call). Matrices are uploaded
+ * :249-313 (one workspace for the largest call). Matrices are uploaded
  * as bf16 (F16/F32 converted with round-to-nearest-even), vectors as fp32.
- * Sizes are computed by a dry run of the same walk, so the arena is exact. */
+ * The weight and workspace slabs are sized by a planning pass of the same
+ * code that carves them (core/devmem.h), so their sizes are exact. */
 #include "engine/model.h"
 #include "core/safetensors.h"
 #include <math.h>
@@ -59,42 +60,41 @@ static float elem_f32(const st_tensor *t, size_t i) {
     }
 }
 
+/* One walk over the checkpoint's tensors. The walk runs twice: while the
+ * weight slab is planning it only sizes the uploads, then it uploads. Names
+ * are resolved inside a scope: the checkpoint's text-model prefix
+ * ("model." or "model.language_model."), plus "layers.<l>." inside a layer. */
 typedef struct loader {
     cujev_model *m;
     const st_bundle *b;
     const char *prefix;
-    int dry;      /* size only */
-    size_t bytes; /* dry-run total */
-    uint16_t *conv; /* conversion buffer */
+    char scope[128];    /* prefix + current layer's "layers.<l>." */
+    uint16_t *conv;     /* host staging for F16/F32 -> bf16 conversion */
     size_t conv_cap;
 } loader;
 
-static const st_tensor *find(loader *L, const char *fmt, int layer) {
-    char name[256], full[320];
-    snprintf(name, sizeof name, fmt, layer);
-    snprintf(full, sizeof full, "%s%s", L->prefix, name);
-    return st_bundle_find(L->b, full);
+static void scope_top(loader *L) { snprintf(L->scope, sizeof L->scope, "%s", L->prefix); }
+static void scope_layer(loader *L, int layer) {
+    snprintf(L->scope, sizeof L->scope, "%slayers.%d.", L->prefix, layer);
 }
 
-static cujev_status want(loader *L, const char *fmt, int layer, const st_tensor **out) {
-    *out = find(L, fmt, layer);
-    if (!*out) {
-        char name[256];
-        snprintf(name, sizeof name, fmt, layer);
-        return cujev_fail(CUJEV_ERR_FORMAT, "missing tensor %s%s", L->prefix, name);
-    }
-    if ((*out)->dtype == ST_OTHER)
-        return cujev_fail(CUJEV_ERR_UNSUPPORTED, "tensor %s: unsupported dtype", (*out)->name);
+/* The tensor `leaf` of the current scope; FORMAT if absent, UNSUPPORTED if
+ * its dtype is none of BF16 / F16 / F32. */
+static cujev_status need(loader *L, const char *leaf, const st_tensor **out) {
+    char full[256];
+    snprintf(full, sizeof full, "%s%s", L->scope, leaf);
+    const st_tensor *t = st_lookup(L->b, full);
+    *out = t;
+    if (!t)
+        return cujev_raise(CUJEV_ERR_FORMAT, "checkpoint has no tensor %s", full);
+    if (t->dtype == ST_OTHER)
+        return cujev_raise(CUJEV_ERR_UNSUPPORTED, "tensor %s: dtype is not BF16/F16/F32", full);
     return CUJEV_OK;
 }
 
-static void *take(loader *L, size_t bytes) {
-    if (L->dry) {
-        L->bytes += cujev_align_up(bytes, 256);
-        return NULL;
-    }
-    return cujev_arena_alloc(&L->m->weights, bytes);
-}
+static int planning(const loader *L) { return cujev_slab_planning(&L->m->weights); }
+
+static void *take(loader *L, size_t bytes) { return cujev_slab_take(&L->m->weights, bytes); }
 
 /* Row-concatenation of 2-D tensors [rows_i, K] -> one bf16 [sum rows, K]. */
 static cujev_status upload_fused(loader *L, const st_tensor **parts, int nparts, int K,
@@ -102,34 +102,34 @@ static cujev_status upload_fused(loader *L, const st_tensor **parts, int nparts,
     size_t rows = 0;
     for (int i = 0; i < nparts; i++) {
         if (parts[i]->ndim != 2 || parts[i]->shape[1] != K)
-            return cujev_fail(CUJEV_ERR_FORMAT, "tensor %s: expected [*, %d]", parts[i]->name, K);
+            return cujev_raise(CUJEV_ERR_FORMAT, "tensor %s: expected [*, %d]", parts[i]->name, K);
         rows += (size_t)parts[i]->shape[0];
     }
     bf16_t *d = (bf16_t *)take(L, rows * (size_t)K * 2);
-    if (L->dry)
+    if (planning(L))
         return CUJEV_OK;
     if (!d)
-        return cujev_fail(CUJEV_ERR_OOM, "weight arena exhausted");
+        return cujev_raise(CUJEV_ERR_OOM, "weight slab exhausted");
     size_t off = 0;
     for (int i = 0; i < nparts; i++) {
         const st_tensor *t = parts[i];
-        const size_t n = st_numel(t);
+        const size_t n = t->numel;
         if (t->dtype == ST_BF16) {
-            HIP_TRY(hipMemcpy(d + off, t->data, n * 2, hipMemcpyHostToDevice));
+            HIP_CHECK(hipMemcpy(d + off, t->data, n * 2, hipMemcpyHostToDevice));
         } else {
             const size_t step = (size_t)1 << 24;
             if (L->conv_cap < step) {
                 free(L->conv);
                 L->conv = (uint16_t *)malloc(step * 2);
                 if (!L->conv)
-                    return cujev_fail(CUJEV_ERR_OOM, "host conversion buffer");
+                    return cujev_raise(CUJEV_ERR_OOM, "host conversion buffer");
                 L->conv_cap = step;
             }
             for (size_t s = 0; s < n; s += step) {
                 const size_t c = n - s < step ? n - s : step;
                 for (size_t j = 0; j < c; j++)
                     L->conv[j] = f32_to_bf16_bits(elem_f32(t, s + j));
-                HIP_TRY(hipMemcpy(d + off + s, L->conv, c * 2, hipMemcpyHostToDevice));
+                HIP_CHECK(hipMemcpy(d + off + s, L->conv, c * 2, hipMemcpyHostToDevice));
             }
         }
         off += n;
@@ -147,29 +147,29 @@ static cujev_status upload_tiled(loader *L, const bf16_t *w, int M, int K, bf16_
     if (cujev_gemm_small_splits(M, K) <= 0)
         return CUJEV_OK;
     bf16_t *d = (bf16_t *)take(L, (size_t)M * K * 2);
-    if (L->dry)
+    if (planning(L))
         return CUJEV_OK;
     if (!d)
-        return cujev_fail(CUJEV_ERR_OOM, "weight arena exhausted");
-    HIP_TRY(k_gemm_small_tile(w, M, K, d, L->m->stream));
+        return cujev_raise(CUJEV_ERR_OOM, "weight slab exhausted");
+    HIP_CHECK(k_gemm_small_tile(w, M, K, d, L->m->stream));
     *out = d;
     return CUJEV_OK;
 }
 
 static cujev_status upload_f32(loader *L, const st_tensor *t, float add, int negexp, size_t expect,
                                float **out) {
-    const size_t n = st_numel(t);
+    const size_t n = t->numel;
     if (expect && n != expect)
-        return cujev_fail(CUJEV_ERR_FORMAT, "tensor %s: %zu elements, expected %zu", t->name, n,
+        return cujev_raise(CUJEV_ERR_FORMAT, "tensor %s: %zu elements, expected %zu", t->name, n,
                           expect);
     float *d = (float *)take(L, n * 4);
-    if (L->dry)
+    if (planning(L))
         return CUJEV_OK;
     if (!d)
-        return cujev_fail(CUJEV_ERR_OOM, "weight arena exhausted");
+        return cujev_raise(CUJEV_ERR_OOM, "weight slab exhausted");
     float *h = (float *)malloc(n * 4);
     if (!h)
-        return cujev_fail(CUJEV_ERR_OOM, "host vector");
+        return cujev_raise(CUJEV_ERR_OOM, "host vector");
     for (size_t i = 0; i < n; i++) {
         const float v = elem_f32(t, i);
         h[i] = negexp ? -expf(v) : v + add;
@@ -177,7 +177,7 @@ static cujev_status upload_f32(loader *L, const st_tensor *t, float add, int neg
     hipError_t e = hipMemcpy(d, h, n * 4, hipMemcpyHostToDevice);
     free(h);
     if (e != hipSuccess)
-        return cujev_fail(CUJEV_ERR_CUDA, "hipMemcpy: %s", hipGetErrorString(e));
+        return cujev_raise(CUJEV_ERR_CUDA, "hipMemcpy: %s", hipGetErrorString(e));
     *out = d;
     return CUJEV_OK;
 }
@@ -187,105 +187,104 @@ static cujev_status walk(loader *L) {
     const cujev_config *c = &m->cfg;
     const int H = c->hidden_size;
     const st_tensor *t, *parts[4];
-    CUJEV_TRY(want(L, "embed_tokens.weight", 0, &t));
+    scope_top(L);
+    CJ_CHECK(need(L, "embed_tokens.weight", &t));
     if (t->ndim != 2 || t->shape[0] != c->vocab_size || t->shape[1] != H)
-        return cujev_fail(CUJEV_ERR_FORMAT, "embed_tokens shape mismatch");
-    CUJEV_TRY(upload_fused(L, &t, 1, H, &m->embed));
+        return cujev_raise(CUJEV_ERR_FORMAT, "embed_tokens shape mismatch");
+    CJ_CHECK(upload_fused(L, &t, 1, H, &m->embed));
     m->lm_head = m->embed;
     if (!c->tie_word_embeddings) {
-        const st_tensor *lm = st_bundle_find(L->b, "lm_head.weight");
+        const st_tensor *lm = st_lookup(L->b, "lm_head.weight"); /* outside the prefix */
         if (!lm)
-            return cujev_fail(CUJEV_ERR_FORMAT,
+            return cujev_raise(CUJEV_ERR_FORMAT,
                               "tie_word_embeddings is false but lm_head.weight is missing");
         if (lm->ndim != 2 || lm->shape[0] != c->vocab_size)
-            return cujev_fail(CUJEV_ERR_FORMAT, "lm_head shape mismatch");
-        CUJEV_TRY(upload_fused(L, &lm, 1, H, &m->lm_head));
+            return cujev_raise(CUJEV_ERR_FORMAT, "lm_head shape mismatch");
+        CJ_CHECK(upload_fused(L, &lm, 1, H, &m->lm_head));
     }
-    CUJEV_TRY(want(L, "norm.weight", 0, &t));
-    CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)H, &m->final_norm));
+    CJ_CHECK(need(L, "norm.weight", &t));
+    CJ_CHECK(upload_f32(L, t, 1.f, 0, (size_t)H, &m->final_norm));
     for (int l = 0; l < c->num_layers; l++) {
         cujev_layer *ly = &m->layers[l];
         ly->type = c->layer_types[l];
-        CUJEV_TRY(want(L, "layers.%d.input_layernorm.weight", l, &t));
-        CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)H, &ly->in_norm));
-        CUJEV_TRY(want(L, "layers.%d.post_attention_layernorm.weight", l, &t));
-        CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)H, &ly->post_norm));
+        scope_layer(L, l);
+        CJ_CHECK(need(L, "input_layernorm.weight", &t));
+        CJ_CHECK(upload_f32(L, t, 1.f, 0, (size_t)H, &ly->in_norm));
+        CJ_CHECK(need(L, "post_attention_layernorm.weight", &t));
+        CJ_CHECK(upload_f32(L, t, 1.f, 0, (size_t)H, &ly->post_norm));
         if (ly->type == CUJEV_LAYER_FULL) {
-            CUJEV_TRY(want(L, "layers.%d.self_attn.q_proj.weight", l, &parts[0]));
-            CUJEV_TRY(want(L, "layers.%d.self_attn.k_proj.weight", l, &parts[1]));
-            CUJEV_TRY(want(L, "layers.%d.self_attn.v_proj.weight", l, &parts[2]));
+            CJ_CHECK(need(L, "self_attn.q_proj.weight", &parts[0]));
+            CJ_CHECK(need(L, "self_attn.k_proj.weight", &parts[1]));
+            CJ_CHECK(need(L, "self_attn.v_proj.weight", &parts[2]));
             if (parts[0]->shape[0] != (int64_t)m->Hq * 2 * m->D ||
                 parts[1]->shape[0] != (int64_t)m->Hkv * m->D ||
                 parts[2]->shape[0] != (int64_t)m->Hkv * m->D)
-                return cujev_fail(CUJEV_ERR_FORMAT, "layer %d: attention projection shapes", l);
-            CUJEV_TRY(upload_fused(L, parts, 3, H, &ly->w_qkv));
-            CUJEV_TRY(upload_tiled(L, ly->w_qkv, m->w_attn, H, &ly->wt_qkv));
-            CUJEV_TRY(want(L, "layers.%d.self_attn.o_proj.weight", l, &t));
-            CUJEV_TRY(upload_fused(L, &t, 1, m->Hq * m->D, &ly->w_o));
-            CUJEV_TRY(upload_tiled(L, ly->w_o, H, m->Hq * m->D, &ly->wt_o));
-            CUJEV_TRY(want(L, "layers.%d.self_attn.q_norm.weight", l, &t));
-            CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)m->D, &ly->q_norm));
-            CUJEV_TRY(want(L, "layers.%d.self_attn.k_norm.weight", l, &t));
-            CUJEV_TRY(upload_f32(L, t, 1.f, 0, (size_t)m->D, &ly->k_norm));
+                return cujev_raise(CUJEV_ERR_FORMAT, "layer %d: attention projection shapes", l);
+            CJ_CHECK(upload_fused(L, parts, 3, H, &ly->w_qkv));
+            CJ_CHECK(upload_tiled(L, ly->w_qkv, m->w_attn, H, &ly->wt_qkv));
+            CJ_CHECK(need(L, "self_attn.o_proj.weight", &t));
+            CJ_CHECK(upload_fused(L, &t, 1, m->Hq * m->D, &ly->w_o));
+            CJ_CHECK(upload_tiled(L, ly->w_o, H, m->Hq * m->D, &ly->wt_o));
+            CJ_CHECK(need(L, "self_attn.q_norm.weight", &t));
+            CJ_CHECK(upload_f32(L, t, 1.f, 0, (size_t)m->D, &ly->q_norm));
+            CJ_CHECK(need(L, "self_attn.k_norm.weight", &t));
+            CJ_CHECK(upload_f32(L, t, 1.f, 0, (size_t)m->D, &ly->k_norm));
         } else {
-            CUJEV_TRY(want(L, "layers.%d.linear_attn.in_proj_qkv.weight", l, &parts[0]));
-            CUJEV_TRY(want(L, "layers.%d.linear_attn.in_proj_z.weight", l, &parts[1]));
-            CUJEV_TRY(want(L, "layers.%d.linear_attn.in_proj_b.weight", l, &parts[2]));
-            CUJEV_TRY(want(L, "layers.%d.linear_attn.in_proj_a.weight", l, &parts[3]));
+            CJ_CHECK(need(L, "linear_attn.in_proj_qkv.weight", &parts[0]));
+            CJ_CHECK(need(L, "linear_attn.in_proj_z.weight", &parts[1]));
+            CJ_CHECK(need(L, "linear_attn.in_proj_b.weight", &parts[2]));
+            CJ_CHECK(need(L, "linear_attn.in_proj_a.weight", &parts[3]));
             if (parts[0]->shape[0] != m->C || parts[1]->shape[0] != m->V ||
                 parts[2]->shape[0] != m->Hv || parts[3]->shape[0] != m->Hv)
-                return cujev_fail(CUJEV_ERR_FORMAT, "layer %d: GDN projection shapes", l);
-            CUJEV_TRY(upload_fused(L, parts, 4, H, &ly->w_in));
-            CUJEV_TRY(upload_tiled(L, ly->w_in, m->w_gdn, H, &ly->wt_in));
-            CUJEV_TRY(want(L, "layers.%d.linear_attn.out_proj.weight", l, &t));
-            CUJEV_TRY(upload_fused(L, &t, 1, m->V, &ly->w_out));
-            CUJEV_TRY(upload_tiled(L, ly->w_out, H, m->V, &ly->wt_out));
-            CUJEV_TRY(want(L, "layers.%d.linear_attn.conv1d.weight", l, &t));
-            CUJEV_TRY(upload_f32(L, t, 0.f, 0, (size_t)m->C * 4, &ly->conv_w));
-            CUJEV_TRY(want(L, "layers.%d.linear_attn.A_log", l, &t));
-            CUJEV_TRY(upload_f32(L, t, 0.f, 1, (size_t)m->Hv, &ly->A_neg_exp));
-            CUJEV_TRY(want(L, "layers.%d.linear_attn.dt_bias", l, &t));
-            CUJEV_TRY(upload_f32(L, t, 0.f, 0, (size_t)m->Hv, &ly->dt_bias));
-            CUJEV_TRY(want(L, "layers.%d.linear_attn.norm.weight", l, &t));
-            CUJEV_TRY(upload_f32(L, t, 0.f, 0, 128, &ly->g_norm));
+                return cujev_raise(CUJEV_ERR_FORMAT, "layer %d: GDN projection shapes", l);
+            CJ_CHECK(upload_fused(L, parts, 4, H, &ly->w_in));
+            CJ_CHECK(upload_tiled(L, ly->w_in, m->w_gdn, H, &ly->wt_in));
+            CJ_CHECK(need(L, "linear_attn.out_proj.weight", &t));
+            CJ_CHECK(upload_fused(L, &t, 1, m->V, &ly->w_out));
+            CJ_CHECK(upload_tiled(L, ly->w_out, H, m->V, &ly->wt_out));
+            CJ_CHECK(need(L, "linear_attn.conv1d.weight", &t));
+            CJ_CHECK(upload_f32(L, t, 0.f, 0, (size_t)m->C * 4, &ly->conv_w));
+            CJ_CHECK(need(L, "linear_attn.A_log", &t));
+            CJ_CHECK(upload_f32(L, t, 0.f, 1, (size_t)m->Hv, &ly->A_neg_exp));
+            CJ_CHECK(need(L, "linear_attn.dt_bias", &t));
+            CJ_CHECK(upload_f32(L, t, 0.f, 0, (size_t)m->Hv, &ly->dt_bias));
+            CJ_CHECK(need(L, "linear_attn.norm.weight", &t));
+            CJ_CHECK(upload_f32(L, t, 0.f, 0, 128, &ly->g_norm));
         }
-        CUJEV_TRY(want(L, "layers.%d.mlp.gate_proj.weight", l, &parts[0]));
-        CUJEV_TRY(want(L, "layers.%d.mlp.up_proj.weight", l, &parts[1]));
+        CJ_CHECK(need(L, "mlp.gate_proj.weight", &parts[0]));
+        CJ_CHECK(need(L, "mlp.up_proj.weight", &parts[1]));
         if (parts[0]->shape[0] != c->intermediate_size || parts[1]->shape[0] != c->intermediate_size)
-            return cujev_fail(CUJEV_ERR_FORMAT, "layer %d: MLP shapes", l);
-        CUJEV_TRY(upload_fused(L, parts, 2, H, &ly->w_gate_up));
-        CUJEV_TRY(upload_tiled(L, ly->w_gate_up, 2 * c->intermediate_size, H, &ly->wt_gate_up));
-        CUJEV_TRY(want(L, "layers.%d.mlp.down_proj.weight", l, &t));
-        CUJEV_TRY(upload_fused(L, &t, 1, c->intermediate_size, &ly->w_down));
-        CUJEV_TRY(upload_tiled(L, ly->w_down, H, c->intermediate_size, &ly->wt_down));
+            return cujev_raise(CUJEV_ERR_FORMAT, "layer %d: MLP shapes", l);
+        CJ_CHECK(upload_fused(L, parts, 2, H, &ly->w_gate_up));
+        CJ_CHECK(upload_tiled(L, ly->w_gate_up, 2 * c->intermediate_size, H, &ly->wt_gate_up));
+        CJ_CHECK(need(L, "mlp.down_proj.weight", &t));
+        CJ_CHECK(upload_fused(L, &t, 1, c->intermediate_size, &ly->w_down));
+        CJ_CHECK(upload_tiled(L, ly->w_down, H, c->intermediate_size, &ly->wt_down));
     }
     return CUJEV_OK;
 }
 
 cujev_status cujev_model_load_weights(cujev_model *m, const char *dir) {
     st_bundle b;
-    CUJEV_TRY(st_bundle_open(dir, &b));
+    CJ_CHECK(st_bundle_open(dir, &b));
     loader L;
     memset(&L, 0, sizeof L);
     L.m = m;
     L.b = &b;
-    L.prefix = st_bundle_find(&b, "model.language_model.embed_tokens.weight") ? "model.language_model."
-                                                                               : "model.";
-    L.dry = 1;
-    cujev_status s = walk(&L);
+    L.prefix = st_lookup(&b, "model.language_model.embed_tokens.weight") ? "model.language_model."
+                                                                          : "model.";
+    cujev_status s = walk(&L); /* planning pass: sizes only */
     if (s == CUJEV_OK) {
-        cujev_log(m->opts.verbose, "weights: %.2f GiB in %d tensors, %d shards",
-                  L.bytes / 1073741824.0, b.num_tensors, b.num_files);
-        s = cujev_arena_init(&m->weights, L.bytes + 4096);
+        cujev_note(m->opts.verbose, "weights: %.2f GiB from %d tensors in %d shard(s)",
+                   m->weights.planned / 1073741824.0, b.num_tensors, b.num_files);
+        s = cujev_slab_commit(&m->weights, "weights");
     }
-    if (s == CUJEV_OK) {
-        L.dry = 0;
-        s = walk(&L);
-    }
+    if (s == CUJEV_OK)
+        s = walk(&L); /* upload pass */
     if (s == CUJEV_OK && hipStreamSynchronize(m->stream) != hipSuccess) /* the tiling kernels */
-        s = cujev_fail(CUJEV_ERR_CUDA, "weight tiling failed");
+        s = cujev_raise(CUJEV_ERR_CUDA, "weight tiling failed");
     free(L.conv);
-    st_bundle_close(&b);
+    st_bundle_release(&b);
     return s;
 }
 
@@ -324,32 +323,31 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
         {(void **)&m->rope, (size_t)m->rope_positions * c->rotary_dim * 4},
     };
     const int np = (int)(sizeof parts / sizeof parts[0]);
-    size_t total = 0;
-    for (int i = 0; i < np; i++)
-        total += cujev_align_up(parts[i].bytes, 256);
-    CUJEV_TRY(cujev_arena_init(&m->work, total + 4096));
+    for (int i = 0; i < np; i++) /* planning pass */
+        cujev_slab_take(&m->work, parts[i].bytes);
+    CJ_CHECK(cujev_slab_commit(&m->work, "workspace"));
     for (int i = 0; i < np; i++) {
-        *parts[i].p = cujev_arena_alloc(&m->work, parts[i].bytes);
+        *parts[i].p = cujev_slab_take(&m->work, parts[i].bytes);
         if (!*parts[i].p)
-            return cujev_fail(CUJEV_ERR_OOM, "workspace arena undersized");
+            return cujev_raise(CUJEV_ERR_OOM, "workspace slab undersized");
     }
     /* Branch K/V scratch must hold finite values everywhere: 64-key tiles read
      * past the valid keys (masked to p = 0, and 0 * NaN would be NaN). */
-    HIP_TRY(hipMemset(m->br_k, 0, br_kv));
-    HIP_TRY(hipMemset(m->br_vt, 0, br_kv));
-    HIP_TRY(hipHostMalloc((void **)&m->h_meta, m->meta_ints * 4, hipHostMallocDefault));
+    HIP_CHECK(hipMemset(m->br_k, 0, br_kv));
+    HIP_CHECK(hipMemset(m->br_vt, 0, br_kv));
+    HIP_CHECK(hipHostMalloc((void **)&m->h_meta, m->meta_ints * 4, hipHostMallocDefault));
     {
         const size_t rb = (size_t)m->rope_positions * c->rotary_dim * 4;
         float *h = (float *)malloc(rb);
         if (!h)
-            return cujev_fail(CUJEV_ERR_OOM, "RoPE table");
+            return cujev_raise(CUJEV_ERR_OOM, "RoPE table");
         cujev_rope_table_host(c->rope_theta, c->rotary_dim, m->rope_positions, h);
         hipError_t e = hipMemcpy(m->rope, h, rb, hipMemcpyHostToDevice);
         free(h);
         if (e != hipSuccess)
-            return cujev_fail(CUJEV_ERR_CUDA, "RoPE table upload: %s", hipGetErrorString(e));
+            return cujev_raise(CUJEV_ERR_CUDA, "RoPE table upload: %s", hipGetErrorString(e));
     }
-    cujev_log(m->opts.verbose, "workspace: %.2f GiB for %zu tokens, %zu branches",
-              m->work.used / 1073741824.0, N, B);
+    cujev_note(m->opts.verbose, "workspace: %.2f GiB for %zu tokens, %zu branches",
+              cujev_slab_used(&m->work) / 1073741824.0, N, B);
     return CUJEV_OK;
 }

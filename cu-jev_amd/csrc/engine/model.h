@@ -9,7 +9,7 @@
 #define CUJEV_MODEL_H
 
 #include "core/config.h"
-#include "core/util.h"
+#include "core/devmem.h"
 #include "cujev.h"
 #include "kernels/kernels.h"
 #include <hip/hip_runtime_api.h>
@@ -48,6 +48,7 @@ typedef struct cujev_layer {
 typedef struct cujev_graph_slot {
     const struct cujev_state *st;
     int P, N, B, nc, maxc, has_cand;
+    int packed; /* GDN chunk table packed (its metadata offsets differ) */
     int seen; /* eager runs so far; -1: capture failed, this key stays eager */
     hipGraphExec_t exec;
     unsigned long long stamp;
@@ -56,8 +57,8 @@ typedef struct cujev_graph_slot {
 struct cujev_model {
     cujev_config cfg;
     cujev_options opts;
-    cujev_arena weights;
-    cujev_arena work;
+    cujev_slab weights; /* bf16 matrices (plain and tiled), fp32 vectors */
+    cujev_slab work;    /* per-call buffers sized for the largest call */
     cujev_gemm *gemm;
     hipStream_t stream;
     hipEvent_t ev0, ev1;
@@ -105,7 +106,7 @@ struct cujev_model {
 
 struct cujev_state {
     cujev_model *model;
-    cujev_arena mem;
+    cujev_slab mem; /* K / V^T caches, S, conv tails */
     int num_tokens;
     bf16_t **kv_k, **kv_vt; /* per layer, NULL for GDN layers */
     float **S;              /* per layer, NULL for full layers */

@@ -6,7 +6,8 @@ own for profilers:
 
 attention  config 3: Hq 16 / Hkv 4, D 256, state 8192 keys, 256 branches x 16
 gdn        config 2: Hk 16 / Hv 32, T = 2048 prefill through the one-call GDN
-           layer (conv+gates inside the scan, norm)
+           layer (conv+gates inside the scan, norm); config 2's gates:
+           A_neg_exp = -1, dt_bias = 0, so g = -softplus(a), a ~ N(0, 1)
 gdn_branch config 2 branches: 64 branches x 16 tokens continuing one state
            (S and the conv tail read, nothing written back), packed chunks
 gdn_split, gdn_branch_split: the same through conv_prep + scan (two calls)
@@ -82,7 +83,7 @@ def gdn_case(fused=True):
     g = torch.Generator(device=dev).manual_seed(2)
     proj = torch.randn(T, Wd, device=dev, generator=g).to(torch.bfloat16)
     conv_w = torch.randn(C, 4, device=dev, generator=g) * 0.5
-    A_neg = -torch.rand(Hv, device=dev, generator=g) * 4
+    A_neg = -torch.ones(Hv, device=dev)  # config 2: g = -softplus(a)
     dt_bias = torch.zeros(Hv, device=dev)
     norm_w = torch.ones(128, device=dev)
     own_base = torch.zeros(T, dtype=torch.int32, device=dev)
@@ -126,7 +127,7 @@ def gdn_branch_case(B=64, L=16, fused=True):
     proj = torch.randn(N, Wd, device=dev, generator=g).to(torch.bfloat16)
     conv_w = torch.randn(C, 4, device=dev, generator=g) * 0.5
     conv_in = torch.randn(C, 3, device=dev, generator=g)
-    A_neg = -torch.rand(Hv, device=dev, generator=g) * 4
+    A_neg = -torch.ones(Hv, device=dev)  # config 2: g = -softplus(a)
     dt_bias = torch.zeros(Hv, device=dev)
     norm_w = torch.ones(128, device=dev)
     S_in = torch.randn(Hv, 128, 128, device=dev, generator=g) * 0.1

@@ -108,6 +108,8 @@ def write_checkpoint(path, cfg, *, seed=0, std=0.02, norm_std=0.0, device="cpu",
 
     path = Path(path)
     path.mkdir(parents=True, exist_ok=True)
+    if generator == "blocks":
+        return _write_blocks(path, cfg, seed=seed, std=std, norm_std=norm_std)
     if generator == "numpy":
         rng = np.random.default_rng(seed)
 
@@ -153,6 +155,69 @@ def write_checkpoint(path, cfg, *, seed=0, std=0.02, norm_std=0.0, device="cpu",
             t = t.to(torch.bfloat16)
         tensors[name] = t.cpu().contiguous()
     save_file(tensors, str(path / "model.safetensors"), metadata={"format": "pt"})
+    with open(path / "config.json", "w") as f:
+        json.dump(cfg, f, indent=1)
+    return str(path)
+
+
+BLOCK_ROWS_ELEMS = 1 << 22  # elements per independently seeded block
+
+
+def _write_blocks(path, cfg, *, seed, std, norm_std):
+    """generator="blocks": the numpy draws of generator="numpy" made parallel.
+    Tensor i (in tensor_shapes order) is cut into row blocks of about 4M
+    elements; block j is drawn from PCG64 seeded with the entropy list
+    [seed, i, j], so the bits do not depend on the thread count or the host,
+    and the blocks are drawn on a thread pool (numpy releases the GIL while
+    filling). Matrices ~ N(0, std) in float32, then rounded to bf16; 1-D
+    parameters as in write_checkpoint (A_log = log U(0, 16) through scalar
+    libm, dt_bias 1, norms 0 / 1 (+ N(0, norm_std)))."""
+    import math
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    import torch
+    from safetensors.torch import save_file
+
+    shapes = tensor_shapes(cfg)
+    jobs = []
+    out = {}
+    for i, (name, shape) in enumerate(shapes):
+        if len(shape) >= 2:
+            rows = shape[0]
+            per_row = int(np.prod(shape[1:]))
+            step = max(1, BLOCK_ROWS_ELEMS // per_row)
+            t = torch.empty(shape, dtype=torch.bfloat16)
+            out[name] = t
+            for j, r0 in enumerate(range(0, rows, step)):
+                jobs.append((t, i, j, r0, min(rows, r0 + step)))
+            continue
+        rng = np.random.default_rng([seed, i, 0])
+        leaf = name.rsplit(".", 1)[0] if name.endswith(".weight") else name
+        if name.endswith("A_log"):
+            u = np.maximum(rng.random(shape, dtype=np.float32) * np.float32(16.0), np.float32(1e-3))
+            t = torch.tensor([math.log(float(x)) for x in u.reshape(-1)], dtype=torch.float32)
+        elif name.endswith("dt_bias"):
+            t = torch.ones(shape, dtype=torch.float32)
+        else:
+            base = 1.0 if leaf.endswith("linear_attn.norm") else 0.0
+            v = np.full(shape, base, np.float32)
+            if norm_std > 0:
+                v = v + rng.standard_normal(shape, dtype=np.float32) * np.float32(norm_std)
+            t = torch.from_numpy(v).to(torch.bfloat16)
+        out[name] = t.reshape(shape)
+
+    def fill(job):
+        t, i, j, r0, r1 = job
+        rng = np.random.default_rng([seed, i, j])
+        blk = rng.standard_normal((r1 - r0,) + tuple(t.shape[1:]), dtype=np.float32)
+        blk *= np.float32(std)
+        t[r0:r1] = torch.from_numpy(blk).to(torch.bfloat16)
+
+    threads = max(1, min(32, len(os.sched_getaffinity(0))))
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(fill, jobs))
+    save_file(out, str(path / "model.safetensors"), metadata={"format": "pt"})
     with open(path / "config.json", "w") as f:
         json.dump(cfg, f, indent=1)
     return str(path)

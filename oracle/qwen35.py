@@ -202,6 +202,43 @@ def causal_gqa_attention(q, gate, k, v, scale=1.0 / 16.0, bf16_p=False):
     return o * sigmoid(gate)
 
 
+def gated_attention_layer(h_state, h_branch, own_base, Wqkv, Wo, q_norm_eff, k_norm_eff, Hq,
+                          Hkv, rot, theta, eps, D=256, rnd=None):
+    """One gated GQA attention layer (projection to o_proj) over a shared
+    state and packed branches, as the engine runs it (REF
+    src/engine/forward.c:99-118, src/kernels/attention.cu:41-100, :138-332):
+    the state's tokens (positions 0..P-1) attend causally among themselves,
+    branch token n (position P + its index in its branch) attends to the
+    whole state plus [own_base[n], n].
+
+    h_state [P, H], h_branch [N, H]: the layer inputs (after the input norm);
+    Wqkv [Hq*2D + 2*Hkv*D, H] row-fused q|gate (per head), k, v; Wo [H, Hq*D].
+    rnd: None for float64 throughout, or a bf16 rounding function applied at
+    the reference engine's rounding points (projection output, q after its
+    scale, K cache, probabilities, attention output, o_proj output).
+    Returns (out_state [P, H], out_branch [N, H]).
+    Pinned by tests/test_attention_layer.py against transformers'
+    Qwen3_5Attention over every [state ++ branch] at config 1's shapes."""
+    e = rnd is not None
+    r = rnd if e else (lambda x: x)
+    P, N = len(h_state), len(h_branch)
+    own_base = np.asarray(own_base)
+    pos_b = P + np.arange(N) - own_base
+    qs, gs, ks, vs = attn_prep(r(np.asarray(h_state, np.float64) @ Wqkv.T), q_norm_eff,
+                               k_norm_eff, np.arange(P), Hq, Hkv, rot, theta, eps, D)
+    qb, gb, kb, vb = attn_prep(r(np.asarray(h_branch, np.float64) @ Wqkv.T), q_norm_eff,
+                               k_norm_eff, pos_b, Hq, Hkv, rot, theta, eps, D)
+    if e:
+        sc = D ** -0.5 * LOG2E
+        qs, qb, ks, kb = r(qs * sc), r(qb * sc), r(ks), r(kb)
+        kw = dict(scale=np.log(2.0), bf16_p=True)
+    else:
+        kw = dict(scale=D ** -0.5)
+    o_s = causal_gqa_attention(qs, gs, ks, vs, **kw) if P else np.zeros((0, Hq, D))
+    o_b = shared_prefix_attention(qb, gb, ks, vs, kb, vb, own_base, **kw)
+    return r(r(o_s.reshape(P, Hq * D)) @ Wo.T), r(r(o_b.reshape(N, Hq * D)) @ Wo.T)
+
+
 # --------------------------------------------------------------------------
 # Gated DeltaNet
 # --------------------------------------------------------------------------

@@ -142,9 +142,11 @@ def test_attention_key_split_matches_oracle(seed, Hq, Hkv, P, seg_lens):
 
 
 def test_attention_branch_isolation():
-    """A branch's output does not depend on its siblings (bit-exact: the
-    kernel's per-row arithmetic does not depend on which rows share a tile
-    only through the visible keys)."""
+    """A branch's output does not depend on its siblings. Not bit for bit:
+    alone, the branch's rows sit at other positions of the 32-token tiles and
+    its own keys start at another offset inside a 64-key tile, which changes
+    the order of the fp32 sums (and the split of the state keys), so the
+    check is to the kernel's bf16 tolerance."""
     o = ops()
     Hq, Hkv, P = 8, 2, 130
     q, gate, ks, vs, ko, vo, ob = make_case(11, Hq, Hkv, P, [7, 20, 9])

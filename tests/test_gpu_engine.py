@@ -155,7 +155,8 @@ def test_branch_isolation(engine):
     alone = engine.eval([target])[0]
     evil = Branch([77] * 30, [100, 200, 300, 400])
     together = engine.eval([target] + [evil] * 15)[0]
-    # GEMM tile choices differ with the batch size: bf16-level jitter only
+    # GEMM tile choices differ with the batch size: bf16-level jitter only,
+    # so the comparison is within a tolerance, not bit for bit
     np.testing.assert_allclose(together, alone, atol=2e-2)
 
 
@@ -250,3 +251,22 @@ def test_graph_replays_match_eager(ckpt):
     finally:
         e.close()
         ref.close()
+
+
+def test_graph_key_tells_packed_from_unpacked(engine, monkeypatch):
+    """Branches of 33-64 tokens fill one GDN chunk each whether or not the
+    chunk table is packed, so both tables have the same chunk count but lay
+    the uploaded metadata out differently. A shape captured packed must not
+    be replayed for the unpacked table (and back): every call, eager,
+    captured or replayed, gives the same logits."""
+    rng = np.random.default_rng(31)
+    prefix = rand_ids(rng, 60)
+    brs = [Branch(rand_ids(rng, 40), rand_ids(rng, 5)) for _ in range(6)]
+    engine.prefill(prefix)
+    monkeypatch.setenv("CUJEV_GDN_PACK_MIN_UNITS", "0")
+    first = engine.eval(brs)
+    for pack_min in ("0", "0", "-1", "-1", "-1", "0", "-1"):
+        monkeypatch.setenv("CUJEV_GDN_PACK_MIN_UNITS", pack_min)
+        got = engine.eval(brs)
+        for a, b in zip(got, first):
+            np.testing.assert_array_equal(a, b, err_msg=f"pack_min={pack_min}")

@@ -35,17 +35,27 @@ def bf(x):
 
 
 class Layer:
-    """Seeded GDN layer parameters (fused projection output is the input)."""
+    """Seeded GDN layer parameters (fused projection output is the input).
 
-    def __init__(self, seed, Hk, Hv):
+    config2=True gives config 2's gates: A_neg_exp = -1 and dt_bias = 0, so
+    g = -softplus(a) with a ~ N(0, 1) from the projection columns, and
+    beta = sigmoid(b) with b ~ N(0, 1); otherwise A = U(0.5, 4) and
+    dt_bias = U(-1, 1) (faster decay). Conv weights are N(0, 0.5**2) and the
+    pre-conv inputs N(0, 1), rounded to bf16, in both."""
+
+    def __init__(self, seed, Hk, Hv, config2=False):
         rng = np.random.default_rng(seed)
         self.Hk, self.Hv = Hk, Hv
         self.C = (2 * Hk + Hv) * DK
         self.W = self.C + Hv * DV + 2 * Hv
         self.conv_w = (rng.standard_normal((self.C, 4)) * 0.5).astype(np.float32)
-        self.A_log = np.log(rng.uniform(0.5, 4.0, Hv)).astype(np.float32)
+        if config2:
+            self.A_log = np.zeros(Hv, np.float32)
+            self.dt_bias = np.zeros(Hv, np.float32)
+        else:
+            self.A_log = np.log(rng.uniform(0.5, 4.0, Hv)).astype(np.float32)
+            self.dt_bias = rng.uniform(-1.0, 1.0, Hv).astype(np.float32)
         self.A_neg = (-np.exp(self.A_log.astype(np.float64))).astype(np.float32)
-        self.dt_bias = rng.uniform(-1.0, 1.0, Hv).astype(np.float32)
         self.norm_w = (1.0 + 0.1 * rng.standard_normal(DV)).astype(np.float32)
         self.eps = 1e-6
         self.rng = rng
@@ -229,23 +239,34 @@ def test_gdn_layer_equals_conv_then_scan(case):
 
 
 def test_gdn_capacity_shape():
-    """Config 2: Hk 16 / Hv 32, prefill T=2048 then 64 branches x 16 tokens
-    from the final state. Oracle on the full prefill and on 8 branches."""
+    """Config 2 on the path the engine runs: Hk 16 / Hv 32, config 2's gates
+    (g = -softplus(N(0,1)), beta = sigmoid(N(0,1))), a T = 2048 prefill
+    through the one-call layer (conv + gates inside phase A, state and conv
+    tail written), then 64 branches x 16 tokens from that state with the
+    branches packed four to a 64-token chunk, as the engine's eval packs
+    them. Oracle: the float64 recurrent form over the whole prefill (y and
+    S) and over 8 of the branches."""
     o = ops()
-    L = Layer(2, 16, 32)
+    L = Layer(2, 16, 32, config2=True)
     T = 2048
     prefix = L.proj(T)
-    got_p = run_gpu(o, L, prefix, [T], write_state=True)
+    print("config 2 prefill T=2048 (fused layer)", flush=True)
+    got_p = run_gpu(o, L, prefix, [T], write_state=True, fused=True)
     y, S, tail = oracle_segment(L, prefix, None, None)
     ey, es = rel_err(got_p["y"], y), rel_err(got_p["S"], S)
-    print(f"prefill 2048: y {ey:.3e} S {es:.3e}")
+    print(f"prefill 2048: y {ey:.3e} S {es:.3e}", flush=True)
     assert ey <= TOL and es <= TOL
+    np.testing.assert_array_equal(got_p["tail"], tail.astype(np.float32))
     seg_lens = [16] * 64
     br = L.proj(1024)
-    got = run_gpu(o, L, br, seg_lens, conv_in=got_p["tail"], S_in=got_p["S"])
+    print("config 2 branches 64 x 16 (fused layer, packed chunks)", flush=True)
+    got = run_gpu(o, L, br, seg_lens, conv_in=got_p["tail"], S_in=got_p["S"], fused=True,
+                  pack=True)
+    worst = 0.0
     for b in range(0, 64, 8):
         seg = br[16 * b: 16 * b + 16]
         y_ref, _, _ = oracle_segment(L, seg, tail, S)
         e = rel_err(got["y"][16 * b: 16 * b + 16], y_ref)
-        print(f"branch {b}: {e:.3e}")
-        assert e <= TOL
+        worst = max(worst, e)
+        assert e <= TOL, (b, e)
+    print(f"branches: worst y {worst:.3e}", flush=True)
