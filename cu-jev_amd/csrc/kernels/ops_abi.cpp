@@ -2,8 +2,10 @@
  * argument checks around the launchers of kernels.h. */
 #include "../../../include/cujev_ops.h"
 #include "kernels.h"
+#include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdarg.h>
+#include <mutex>
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -170,6 +172,67 @@ EXPORT int cujev_op_attention_ws(const void *q, const void *gate, int gate_tok_s
                                 own_base, N, Hq, Hkv, (bf16_t *)out, ws, ws_bytes,
                                 (hipStream_t)stream),
                     "attention");
+}
+
+/* ---- attention with no allocation ----------------------------------------
+ * The key-split partials of cujev_op_attention_noalloc live in `scratch`, a
+ * file-scope device array (each GPU the library runs on holds its own copy
+ * until the process ends). Host code never uses the array's name as an
+ * address: on its first call on a device, with that device current, the
+ * entry point asks the runtime for that device's address of the array and
+ * keeps it per device. Every call on one GPU shares the array: calls that
+ * overlap on one GPU race. Nothing in it has to start at zero (every split
+ * writes l and mu of each of its rows; o is read only where l > 0). */
+static __device__ __align__(256) unsigned char scratch[CUJEV_OPS_ATTN_NOALLOC_SCRATCH_BYTES];
+
+#define CUJEV_OPS_MAX_DEVICES 64
+static std::mutex g_scratch_mu;
+static void *g_scratch_dev[CUJEV_OPS_MAX_DEVICES]; /* per device ordinal */
+
+static int scratch_address(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return fail(4, "attention_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= CUJEV_OPS_MAX_DEVICES)
+        return fail(7, "attention_noalloc: device %d is beyond the %d this library tracks", dev,
+                    CUJEV_OPS_MAX_DEVICES);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(4, "attention_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                        dev, hipGetErrorString(e));
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return 0;
+}
+
+EXPORT int cujev_op_attention_noalloc(const void *q, const void *gate, int gate_tok_stride,
+                                      int gate_head_stride, const void *pk, const void *pvt,
+                                      int P, int p_stride, const void *ok, const void *ovt,
+                                      int o_stride, const int32_t *own_base, int N, int Hq,
+                                      int Hkv, void *out, void *stream) {
+    if (N < 0 || P < 0 || Hkv <= 0)
+        return fail(1, "attention_noalloc: bad arguments");
+    const size_t need = cujev_attention_ws_bytes(N, Hq, cujev_attention_splits(N, Hkv, P));
+    if (need > CUJEV_OPS_ATTN_NOALLOC_SCRATCH_BYTES)
+        return fail(6,
+                    "attention_noalloc: N=%d, Hq=%d, Hkv=%d, P=%d needs %zu bytes of key-split "
+                    "partials; the static scratch holds %zu",
+                    N, Hq, Hkv, P, need, (size_t)CUJEV_OPS_ATTN_NOALLOC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    const int st = scratch_address(&ws);
+    if (st != 0)
+        return st;
+    return launched(k_attention((const bf16_t *)q, (const bf16_t *)gate, gate_tok_stride,
+                                gate_head_stride, (const bf16_t *)pk, (const bf16_t *)pvt, P,
+                                p_stride, (const bf16_t *)ok, (const bf16_t *)ovt, o_stride,
+                                own_base, N, Hq, Hkv, (bf16_t *)out, ws,
+                                CUJEV_OPS_ATTN_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream),
+                    "attention_noalloc");
 }
 
 EXPORT int cujev_op_gdn_conv_prep(const void *proj, int proj_stride, const float *conv_w,

@@ -34,6 +34,8 @@ _SIGS = {
     "cujev_op_attention": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P],
     "cujev_op_attention_ws": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P,
                               C.c_size_t, _P],
+    "cujev_op_attention_noalloc": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I,
+                                   _P, _P],
     "cujev_op_gdn_conv_prep": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P,
                                _P, _P],
     "cujev_op_gemm_small": [_P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _P],
@@ -142,6 +144,16 @@ def attention(q, gate, gate_tok_stride, gate_head_stride, pk, pvt, P, p_stride, 
               _ptr(own_base), N, Hq, Hkv, _ptr(out), _ptr(ws), ws.numel(), _stream())
         return
     _call("cujev_op_attention", _ptr(q), _ptr(gate), gate_tok_stride, gate_head_stride,
+          _ptr(pk), _ptr(pvt), int(P), p_stride, _ptr(ok), _ptr(ovt), o_stride, _ptr(own_base),
+          N, Hq, Hkv, _ptr(out), _stream())
+
+
+def attention_noalloc(q, gate, gate_tok_stride, gate_head_stride, pk, pvt, P, p_stride, ok, ovt,
+                      o_stride, own_base, Hq, Hkv, out):
+    """attention_ws with the key-split partials in the library's static
+    per-GPU scratch (no allocation by the call)."""
+    N = q.shape[0]
+    _call("cujev_op_attention_noalloc", _ptr(q), _ptr(gate), gate_tok_stride, gate_head_stride,
           _ptr(pk), _ptr(pvt), int(P), p_stride, _ptr(ok), _ptr(ovt), o_stride, _ptr(own_base),
           N, Hq, Hkv, _ptr(out), _stream())
 

@@ -120,6 +120,24 @@ int cujev_op_attention_ws(const void *q, const void *gate, int gate_tok_stride,
                           size_t ws_bytes, void *stream);
 size_t cujev_ops_attention_ws_bytes(int N, int Hq, int Hkv, int P);
 
+/* No counterpart in the reference. cujev_op_attention_ws for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same kernels and results, with the
+ * key-split partials in a static device array the library holds, one per
+ * GPU, until the process ends. It calls no hipMalloc / hipFree. Limit: the
+ * partials of one call must fit CUJEV_OPS_ATTN_NOALLOC_SCRATCH_BYTES; every
+ * shape the kernel accepts does (splits x N x Hq <= 32768 rows of 258
+ * floats, since the kernel needs Hq = 4 Hkv), and a larger need is rejected
+ * with status 6. Every call on one GPU shares the array, so calls that
+ * overlap on one GPU (other streams, other threads) race; serialise them.
+ * The stream must belong to the current device. */
+#define CUJEV_OPS_ATTN_NOALLOC_SCRATCH_BYTES 33816576u /* 32.25 MiB */
+int cujev_op_attention_noalloc(const void *q, const void *gate, int gate_tok_stride,
+                               int gate_head_stride, const void *pk, const void *pvt, int P,
+                               int p_stride, const void *ok, const void *ovt, int o_stride,
+                               const int32_t *own_base, int N, int Hq, int Hkv, void *out,
+                               void *stream);
+
 /* Replaces reference src/kernels/kernels.h:214-215 (k_gdn_conv) and :221-223
  * (k_gdn_prep), fused. proj rows [q Hk*128 | k Hk*128 | v Hv*128 | z | b | a].
  * Conv (width 4) + SiLU with taps before a segment taken from conv_in [C][3]
