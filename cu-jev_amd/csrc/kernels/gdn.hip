@@ -6,18 +6,24 @@
  * transformers' torch_chunk_gated_delta_rule (modeling_qwen3_5.py:249-327).
  *
  * Pipeline per layer (all tokens of all segments in one launch each):
- *   gdn_conv_prep  conv(4) + SiLU, l2norm(q,k) with q * 128^-1/2, g, beta
- *                  -> bf16 q,k [N][Hk][128], v [N][Hv][128]; fp32 g, beta.
- *   gdn_chunk_a    per (64-token chunk, v-head), fully parallel:
- *                  G = cumsum g, A = tril(beta_i k_i.k_j e^{G_i-G_j}, -1),
+ *   gdn_conv_prep  (two-call form) conv(4) + SiLU, l2norm(q,k) with
+ *                  q * 128^-1/2, g, beta -> fp32 q,k [N][Hk][128],
+ *                  v [N][Hv][128], g, beta. The one-call layer computes the
+ *                  same inside gdn_chunk_a.
+ *   gdn_chunk_a    per (64-token chunk, k-head), fully parallel, for every
+ *                  v-head of the k-head: G = cumsum g,
+ *                  A = tril(beta_i k_i.k_j e^{G_i-G_j}, -1),
  *                  T = (I+A)^-1 by blocked forward substitution (fp32),
- *                  W = T diag(beta e^G) K, U = T diag(beta) V (bf16 MFMA),
- *                  QKm = tril(q_i.k_j e^{G_i-G_j})           -> bf16 in HBM.
+ *                  W = T diag(beta e^G) K, U = T diag(beta) V,
+ *                  QKm = tril(q_i.k_j e^{G_i-G_j})  -> HBM in phase B's
+ *                  fragment order (bf16; U fp32; QKm and (K e^{G_last-G})^T
+ *                  as bf16 hi + lo pairs).
  *   gdn_chunk_b    per (segment, v-head), sequential over the segment's
- *                  chunks; wave w owns 32 columns of S (fp32, registers):
+ *                  chunks; a workgroup owns 32 columns of S (fp32, registers):
  *                  V' = U - W S;  O = (Q e^G) S + QKm V';
- *                  S = e^{G_last} S + (K e^{G_last-G})^T V'  (bf16 MFMA),
- *                  then y = w * bf16(rmsnorm(O)) * silu(z) straight to bf16.
+ *                  S = e^{G_last} S + (K e^{G_last-G})^T V'  (bf16 MFMA, V'
+ *                  and the two operands above as hi + lo products), O fp32,
+ *                  then y = w * bf16(rmsnorm(O)) * silu(z) to bf16.
  * Every segment starts from S_in (the state's S, read-only) or 0 and the
  * conv taps before a segment come from the state's conv tail (or 0): branches
  * never copy the state.
@@ -55,7 +61,7 @@ __global__ __launch_bounds__(256) void gdn_conv_prep_kernel(
     const bf16 *__restrict__ proj, int ps, const float *__restrict__ conv_w,
     const float *__restrict__ conv_in, const int32_t *__restrict__ own_base,
     const float *__restrict__ A_neg_exp, const float *__restrict__ dt_bias, int N, int Hk, int Hv,
-    bf16 *__restrict__ qo, bf16 *__restrict__ ko, bf16 *__restrict__ vo, float *__restrict__ go,
+    float *__restrict__ qo, float *__restrict__ ko, float *__restrict__ vo, float *__restrict__ go,
     float *__restrict__ bo) {
     const int nheads = 2 * Hk + Hv;
     const int ntb = (N + PREP_T - 1) / PREP_T;
@@ -109,7 +115,7 @@ __global__ __launch_bounds__(256) void gdn_conv_prep_kernel(
     }
 
     /* ---- conv + SiLU (+ l2 norm) ---- */
-    bf16 *dst;
+    float *dst;
     float scale = 1.f;
     const bool norm = head < 2 * Hk;
     if (head < Hk) {
@@ -167,11 +173,9 @@ __global__ __launch_bounds__(256) void gdn_conv_prep_kernel(
                 ss += __shfl_xor(ss, o, 64);
             inv = rsqrtf(ss + 1e-6f) * scale;
         }
-        bf16x8 out;
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            out[e] = f2bf(y[e] * inv);
-        *(bf16x8 *)(dst + (size_t)n * tok_stride + 8 * s) = out;
+        float *d = dst + (size_t)n * tok_stride + 8 * s;
+        *(float4 *)d = make_float4(y[0] * inv, y[1] * inv, y[2] * inv, y[3] * inv);
+        *(float4 *)(d + 4) = make_float4(y[4] * inv, y[5] * inv, y[6] * inv, y[7] * inv);
     }
 }
 
@@ -197,45 +201,78 @@ __global__ void gdn_conv_tail_kernel(const bf16 *__restrict__ proj, int ps,
 /* ---------------------------------------------------------------------- */
 /* phase A: intra-chunk WY/UT factors, written in phase B's operand layouts */
 /* ---------------------------------------------------------------------- */
-/* One workgroup (4 waves) per (chunk, v-head), LDS under 80 KiB so two
- * share a CU:
- *   1. q, k (k-head), v rows -> LDS; wave 0 forms G = cumsum g and the
- *      per-token scales beta e^G, beta, e^{G_last - G}.
- *   2. K K^T and Q K^T (bf16 MFMA); A = tril(beta_i e^{G_i-G_j} k_i.k_j, -1)
- *      (fp32) and the masked QK^T (bf16) -> LDS; Q e^G and QK^T leave.
- *   3. T = (I + A)^-1 in place, fp32: the four 16x16 diagonal blocks by
- *      forward substitution, then T_10 = -T_11 (A_10 T_00) inside each 32x32
- *      diagonal block, then the same at 64 with 32x32 blocks.
- *   4. W = T (beta e^G K), U = T (beta V) on MFMA. Their B operands need
- *      tokens on the k axis: D = K I (an exact identity product) gives that
- *      layout in registers, rows in the accumulator order 4h+0..3, 8+4h+0..3
- *      of every 16, so T is read with its columns in that order. The same
- *      D tiles scaled by e^{G_last - G} are (k e^{G_last-G})^T, stored
- *      straight from registers after one cross-half exchange.
- *   5. W and U staged row-major in the freed q / v rows, then stored in
- *      fragment order.
+
+/* ---------------------------------------------------------------------- */
+/* phase A: intra-chunk WY/UT factors, written in phase B's operand layouts */
+/* ---------------------------------------------------------------------- */
+/* One workgroup (8 waves) per (chunk, k-head) serves every v-head that reads
+ * this k-head (Hv / Hk of them, one after the other):
+ *   1. q and k rows of the k-head (conv + SiLU + l2 norm and q * 128^-1/2,
+ *      or read from gdn_conv_prep's fp32 output) staged in LDS as bf16
+ *      pairs hi + lo (hi = bf16(x), lo = bf16(x - hi): x to ~16 bits);
+ *   2. raw K K^T (hi parts) and Q K^T (hi.hi + hi.lo + lo.hi MFMAs) in fp32,
+ *      computed once for all the v-heads;
+ *   then per v-head:
+ *   3. gates: G = cumsum g (restarted at segment starts), beta e^G, beta,
+ *      e^{G_last - G}; the v-head's v rows (hi + lo);
+ *   4. q e^G (bf16) and the masked QK^T (hi + lo) leave; A = tril(beta_i
+ *      e^{G_i-G_j} k_i.k_j, -1) (fp32);
+ *   5. T = (I + A)^-1 in place (fp32, blocked forward substitution); beside
+ *      it (K e^{G_last-G})^T from the exact k rows leaves as hi + lo;
+ *   6. W = T (beta e^G K) (bf16) and U = T (beta V) with V exact (hi and lo
+ *      MFMAs; U kept fp32), staged row-major, then stored in the fragment
+ *      order phase B reads.
+ * Which operands carry lo parts follows from where a bf16 rounding moves
+ * the layer output: q and k in QK^T, v in U, k in (K e^{G_last-G})^T, and
+ * U, QK^T, (K e^{G_last-G})^T and V' themselves each cost about as much as
+ * the reference's own bf16 round trip in the gated norm; K K^T, W, T,
+ * q e^G and the bf16 copy of S that the W S and q e^G S products read each
+ * cost under a tenth of that.
  * A chunk may hold several whole segments (chunk_starts marks where each
  * begins): G restarts at every segment start and A and QK^T are kept
  * block-diagonal, so the segments do not see each other. This is valid for
- * branches that all continue one state and write no final state: phase B then
- * needs nothing per segment. */
-struct __attribute__((aligned(16))) ChunkA_Smem {
-    bf16 K[CH][DK + 8];   /* k rows                     */
-    bf16 Q[CH][DK + 8];   /* q rows, later W            */
-    bf16 V[CH][DV + 8];   /* v rows, later U            */
-    float AT[CH][CH + 4]; /* A, then T in place (rows 16-byte aligned) */
-    bf16 QK[CH][CH + 8];  /* masked QK^T staging        */
-    float G[CH], sK[CH], sKg[CH], sV[CH];
+ * branches that all continue one state and write no final state: phase B
+ * then needs nothing per segment. */
+constexpr int PA_THREADS = 512;
+constexpr int PA_MAX_REP = 4; /* v-heads per k-head (one gate wave each) */
+constexpr int PA_CONV_STAGE = 8 * 16 * 4 + 3 * 128; /* floats of one slice's weights + tail */
+
+struct __attribute__((aligned(16))) PairA_Smem {
+    bf16 Kh[CH][DK + 8], Kl[CH][DK + 8]; /* k rows, hi and lo parts                 */
+    bf16 Xh[CH][DK + 8], Xl[CH][DK + 8]; /* q rows, then the v-head's v rows; then
+                                            U staging (fp32 [CH][DV + 4])          */
+    float KK[CH][CH + 4];                /* conv staging of q, k; then raw k_i.k_j  */
+    float QK[CH][CH + 4];                /* raw q_i.k_j                              */
+    float AT[CH][CH + 4];                /* A, then T in place; then W staging      */
+    float cs[PA_CONV_STAGE];             /* conv staging of the v slice             */
+    /* per v-head of the k-head: G, beta e^G, e^{G_last - G}, beta */
+    float G[PA_MAX_REP][CH], sK[PA_MAX_REP][CH], sKg[PA_MAX_REP][CH], sV[PA_MAX_REP][CH];
     int Sid[CH]; /* segment of each token inside a packed chunk (1-based) */
 };
-static_assert(sizeof(ChunkA_Smem) <= 80 * 1024, "two phase-A workgroups per CU");
+static_assert(sizeof(PairA_Smem) <= 160 * 1024, "phase A fits one CU's LDS");
+static_assert(2 * sizeof(bf16) * CH * (DK + 8) >= sizeof(float) * CH * (DV + 4), "U staging");
+static_assert(sizeof(float) * CH * (CH + 4) >= sizeof(bf16) * CH * (DK + 8), "W staging");
 
 DEV bf16x8 ld8(const bf16 *p) { return *(const bf16x8 *)p; }
-typedef __attribute__((address_space(3))) float4 lds_f4;
 DEV float4 rd4(const float *p) { return *(const float4 *)p; }
 DEV void wr4(float *p, float4 v) { *(float4 *)p = v; }
 DEV float4 f4fma(float a, float4 b, float4 c) {
     return make_float4(fmaf(a, b.x, c.x), fmaf(a, b.y, c.y), fmaf(a, b.z, c.z), fmaf(a, b.w, c.w));
+}
+/* x, through an empty asm: the compiler cannot treat what is derived from it
+ * as loop-invariant (keeps per-iteration index math inside a loop instead
+ * of hoisting dozens of indices out of it into scratch memory). */
+DEV int opaque(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+/* hi = bf16(x), lo = bf16(x - hi) */
+struct bfpair {
+    bf16 hi, lo;
+};
+DEV bfpair split2(float x) {
+    const bf16 hi = f2bf(x);
+    return {hi, f2bf(x - bf2f(hi))};
 }
 
 /* X[r][c0..c0+3] = sum_{k<n} P[r][k] Q[k][c0..c0+3] over fp32 LDS rows of pitch CH+4 */
@@ -265,7 +302,7 @@ struct ConvSrc {
 };
 
 /* The state's new conv tail (prefill): extra workgroups of the phase B grid
- * copy it, beside the recurrence, which leaves half the CUs idle. */
+ * copy it, beside the recurrence, which leaves most CUs idle. */
 struct TailJob {
     const bf16 *proj;
     int ps;
@@ -274,21 +311,15 @@ struct TailJob {
     int seg0_len, C;
 };
 
-/* The three 128-channel slices a phase-A workgroup needs (q and k of its
- * k-head, v of its v-head) through conv + SiLU (+ l2 norm and scale), with
- * gdn_conv_prep_kernel's arithmetic step for step. Thread = (token block
- * tid/16 of 4 tokens, channels 8(tid%16)..+7 of every slice). The 7
- * pre-conv rows of each slice are loaded first; the conv weights and the
- * state's tail (the same for all token blocks) go through LDS once:
- * cw[slice][e][s] float4 and ct[slice][j][e][s] for channel 8s + e. */
-DEV int slice_c0(int sl, int Hk, int hk, int hv) {
-    return sl == 0 ? hk * DK : sl == 1 ? (Hk + hk) * DK : (2 * Hk + hv) * DK;
-}
-
+/* Conv weights and the state's tail (the same for every token block) of
+ * `nsl` 128-channel slices starting at channel c0[sl] -> LDS:
+ * cw[(sl*8 + e)*16 + s] float4 and ct[(sl*3 + j)*128 + e*16 + s] for
+ * channel 8s + e of slice sl. */
 template <bool TAIL>
-DEV void conv_stage(const ConvSrc &cv, int Hk, int hk, int hv, int tid, float *cw, float *ct) {
-    for (int i = tid; i < 3 * DK; i += 256) {
-        const int sl = i / DK, c = i % DK, cg = slice_c0(sl, Hk, hk, hv) + c;
+DEV void conv_stage(const ConvSrc &cv, const int *c0, int nsl, int tid, int nthr, float *cw,
+                    float *ct) {
+    for (int i = tid; i < nsl * DK; i += nthr) {
+        const int sl = i / DK, c = i % DK, cg = c0[sl] + c;
         const int slot = (sl * 8 + (c & 7)) * 16 + (c >> 3);
         *(float4 *)&cw[slot * 4] = *(const float4 *)(cv.conv_w + (size_t)cg * 4);
         if constexpr (TAIL) {
@@ -299,11 +330,13 @@ DEV void conv_stage(const ConvSrc &cv, int Hk, int hk, int hv, int tid, float *c
     }
 }
 
+/* 32-bit element offsets (rows x stride stays far below 2^31): one register
+ * per row address instead of two. */
 DEV void conv_rows(const ConvSrc &cv, int c0, int n0, bf16x8 (&x)[7]) {
 #pragma unroll
     for (int i = 0; i < 7; i++) {
         const int row = min(max(n0 - 3 + i, 0), cv.N - 1);
-        x[i] = ld8(cv.proj + (size_t)row * cv.ps + c0);
+        x[i] = ld8(cv.proj + (unsigned)(row * cv.ps + c0));
     }
 }
 
@@ -323,10 +356,15 @@ DEV float sum16_dpp(float v) {
     return v;
 }
 
+/* One 128-channel slice of 4 consecutive tokens (token block tb of the
+ * chunk) through conv + SiLU (+ l2 norm and scale), with gdn_conv_prep's
+ * arithmetic step for step; the fp32 results go to LDS as hi + lo. Lane s
+ * of the 16-lane group owns channels 8s..8s+7; sl indexes the staged
+ * weights / tail. */
 template <bool TAIL>
 DEV void conv_slice(const bf16x8 (&x)[7], const int (&base)[4], const float *cw, const float *ct,
                     int sl, bool norm, float scale, int t0, int L, int tb, int s,
-                    bf16 (*dst)[DK + 8]) {
+                    bf16 (*dh)[DK + 8], bf16 (*dl)[DK + 8]) {
     float w[8][4];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
@@ -402,371 +440,485 @@ DEV void conv_slice(const bf16x8 (&x)[7], const int (&base)[4], const float *cw,
             ss = sum16_dpp(ss);
             inv = rsqrtf(ss + 1e-6f) * scale;
         }
-        bf16x8 out;
+        bf16x8 oh, ol;
 #pragma unroll
         for (int e = 0; e < 8; e++)
-            out[e] = f2bf(tt < L ? y[e] * inv : 0.f);
-        *(bf16x8 *)&dst[tt][8 * s] = out;
+            { const bfpair sp_ = split2(tt < L ? y[e] * inv : 0.f); oh[e] = sp_.hi; ol[e] = sp_.lo; }
+        *(bf16x8 *)&dh[tt][8 * s] = oh;
+        *(bf16x8 *)&dl[tt][8 * s] = ol;
     }
 }
 
-/* SRC 0: q, k, v, g, beta read from gdn_conv_prep's outputs; 1: computed
+/* fp32 rows [CH][128] of gdn_conv_prep's output (row stride `rs` floats,
+ * rows t >= L zero) -> LDS hi + lo, over `nthr` threads. */
+DEV void rows_f32(const float *src, size_t rs, int L, int tid, int nthr, bf16 (*dh)[DK + 8],
+                  bf16 (*dl)[DK + 8]) {
+    for (int i = tid; i < CH * 16; i += nthr) {
+        const int t = i >> 4, c8 = (i & 15) * 8;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+        if (t < L) {
+            a = *(const float4 *)(src + t * rs + c8);
+            b = *(const float4 *)(src + t * rs + c8 + 4);
+        }
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        bf16x8 oh, ol;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            { const bfpair sp_ = split2(v[e]); oh[e] = sp_.hi; ol[e] = sp_.lo; }
+        *(bf16x8 *)&dh[t][c8] = oh;
+        *(bf16x8 *)&dl[t][c8] = ol;
+    }
+}
+
+/* SRC 0: q, k, v, g, beta read from gdn_conv_prep's outputs (fp32); 1: computed
  * here from the pre-conv projection rows (zeros before a segment); 2: the
  * same with the state's conv tail before each segment. */
 template <int SRC>
-__global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
-    const bf16 *__restrict__ qh, const bf16 *__restrict__ kh_, const bf16 *__restrict__ vh,
+__global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
+    const float *__restrict__ qh, const float *__restrict__ kh_, const float *__restrict__ vh,
     const float *__restrict__ g, const float *__restrict__ beta, ConvSrc cv,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
     const uint64_t *__restrict__ chunk_starts, int Hk, int Hv,
     bf16 *__restrict__ Wo, bf16 *__restrict__ Qgo, bf16 *__restrict__ QKo,
-    bf16 *__restrict__ KgTo, bf16 *__restrict__ Uo, float *__restrict__ Glo) {
-    __shared__ ChunkA_Smem sm;
-    const int ch = blockIdx.x, hv = blockIdx.y;
-    const int hk = hv / (Hv / Hk);
+    bf16 *__restrict__ KgTo, float *__restrict__ Uo, float *__restrict__ Glo) {
+    __shared__ PairA_Smem sm;
+    const int ch = blockIdx.x, hk = blockIdx.y;
+    const int rep = Hv / Hk;
     const int t0 = chunk_tok0[ch], L = chunk_len[ch];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, col = lane & 31;
-    const size_t cb = (size_t)ch * Hv + hv;
+    const int grp = tid >> 4, s16 = tid & 15; /* 32 groups of 16 lanes */
+    const int nblk = (L + 3) >> 2;            /* 4-token blocks holding tokens */
+    const int C = (2 * Hk + Hv) * DK;
+    /* segments packed into the chunk: bit t set where token t starts one */
+    const uint64_t starts = chunk_starts ? chunk_starts[ch] | 1ull : 1ull;
+    const uint64_t upto = lane == 63 ? ~0ull : (2ull << lane) - 1;
 
-    /* ---- 1. rows and gates ---- */
-    {
-        float gv = 0.f, bv = 0.f;
-        if constexpr (SRC == 0) {
-            bf16x8 kv[4], qv[4], vv[4];
+    /* ---- 1. q and k rows (hi + lo) ---- */
+    if constexpr (SRC == 0) {
+        rows_f32(qh + ((size_t)t0 * Hk + hk) * DK, (size_t)Hk * DK, L, tid, PA_THREADS, sm.Xh,
+                 sm.Xl);
+        rows_f32(kh_ + ((size_t)t0 * Hk + hk) * DK, (size_t)Hk * DK, L, tid, PA_THREADS, sm.Kh,
+                 sm.Kl);
+    } else {
+        constexpr bool TAIL = SRC == 2;
+        /* (slice, 4-token block) tasks, one per 16-lane group: every
+         * pre-conv row in flight first, then weights and tail into LDS */
+        const int ntask = 2 * nblk;
+        bf16x8 xr[7];
+        int base[4];
+        if (grp < ntask) {
+            const int sl = grp / nblk, n0 = t0 + 4 * (grp - sl * nblk);
+            conv_rows(cv, (sl == 0 ? hk : Hk + hk) * DK + 8 * s16, n0, xr);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int i = tid + 256 * j, t = i >> 4, c8 = (i & 15) * 8;
-                kv[j] = qv[j] = vv[j] = bf16x8{};
-                if (t < L) {
-                    kv[j] = ld8(kh_ + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
-                    qv[j] = ld8(qh + ((size_t)(t0 + t) * Hk + hk) * DK + c8);
-                    vv[j] = ld8(vh + ((size_t)(t0 + t) * Hv + hv) * DV + c8);
-                }
-            }
-            if (wave == 0 && lane < L) {
+            for (int j = 0; j < 4; j++)
+                base[j] = cv.own_base[min(n0 + j, cv.N - 1)];
+        }
+        float *cw = &sm.KK[0][0], *ct = cw + 2 * 8 * 16 * 4;
+        const int c0s[2] = {hk * DK, (Hk + hk) * DK};
+        conv_stage<TAIL>(cv, c0s, 2, tid, PA_THREADS, cw, ct);
+        const int zrows = CH - 4 * nblk; /* rows of blocks without tokens: zeros */
+        for (int i = tid; i < 4 * zrows * 16; i += PA_THREADS) {
+            const int a = i / (zrows * 16), rem = i - a * zrows * 16;
+            bf16(*z)[DK + 8] = a == 0 ? sm.Xh : a == 1 ? sm.Xl : a == 2 ? sm.Kh : sm.Kl;
+            *(bf16x8 *)&z[4 * nblk + (rem >> 4)][8 * (rem & 15)] = bf16x8{};
+        }
+        lds_barrier();
+        if (grp < ntask) {
+            const int sl = grp / nblk, tb = grp - sl * nblk;
+            conv_slice<TAIL>(xr, base, cw, ct, sl, true,
+                             sl == 0 ? 0.08838834764831845f /* 128^-1/2 */ : 1.f, t0, L, tb, s16,
+                             sl == 0 ? sm.Xh : sm.Kh, sl == 0 ? sm.Xl : sm.Kl);
+        }
+    }
+    if (wave == 7)
+        sm.Sid[lane] = __builtin_popcountll(starts & upto);
+    /* gates of the k-head's v-heads, wave 4 + r for v-head r */
+    if (wave >= 4 && wave - 4 < rep) {
+        const int r = wave - 4, hv = hk * rep + r;
+        float gv = 0.f, bv = 0.f;
+        if (lane < L) {
+            if constexpr (SRC == 0) {
                 gv = g[(size_t)(t0 + lane) * Hv + hv];
                 bv = beta[(size_t)(t0 + lane) * Hv + hv];
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int i = tid + 256 * j, t = i >> 4, c8 = (i & 15) * 8;
-                *(bf16x8 *)&sm.K[t][c8] = kv[j];
-                *(bf16x8 *)&sm.Q[t][c8] = qv[j];
-                *(bf16x8 *)&sm.V[t][c8] = vv[j];
-            }
-        } else {
-            constexpr bool TAIL = SRC == 2;
-            const int C = (2 * Hk + Hv) * DK;
-            if (wave == 0 && lane < L) {
-                const bf16 *ab = cv.proj + (size_t)(t0 + lane) * cv.ps + C + Hv * DV; /* b, a */
+            } else {
+                const bf16 *ab = cv.proj + (size_t)(t0 + lane) * cv.ps + C + Hv * DV;
                 bv = sigmoid_f(bf2f(ab[hv]));
                 gv = cv.A_neg_exp[hv] * softplus_f(bf2f(ab[Hv + hv]) + cv.dt_bias[hv]);
             }
-            /* (slice, 4-token block) tasks over the 16-lane groups: only
-             * blocks holding tokens are computed, so a short chunk spreads
-             * its few tasks over all groups (64 tokens: one block, three
-             * slices per group). All pre-conv rows go in flight first, then
-             * the weights and tail into LDS (the A/T area is free until
-             * step 2). */
-            const int nblk = (L + 3) >> 2, ntask = 3 * nblk;
-            const int grp = tid >> 4, s16 = tid & 15;
-            bf16x8 xr[3][7];
-            int base[3][4];
-#pragma unroll
-            for (int r = 0; r < 3; r++) {
-                const int t = grp + 16 * r;
-                if (t < ntask) {
-                    const int sl = t / nblk, n0 = t0 + 4 * (t - sl * nblk);
-                    conv_rows(cv, slice_c0(sl, Hk, hk, hv) + 8 * s16, n0, xr[r]);
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        base[r][j] = cv.own_base[min(n0 + j, cv.N - 1)];
-                }
-            }
-            float *cw = &sm.AT[0][0], *ct = cw + 3 * 8 * 16 * 4;
-            conv_stage<TAIL>(cv, Hk, hk, hv, tid, cw, ct);
-            /* rows of token blocks without tokens: zeros */
-            const int zrows = CH - 4 * nblk;
-            for (int i = tid; i < 3 * zrows * 16; i += 256) {
-                const int a = i / (zrows * 16), rem = i - a * zrows * 16;
-                bf16(*z)[DK + 8] = a == 0 ? sm.Q : a == 1 ? sm.K : sm.V;
-                *(bf16x8 *)&z[4 * nblk + (rem >> 4)][8 * (rem & 15)] = bf16x8{};
-            }
-            lds_barrier();
-#pragma unroll
-            for (int r = 0; r < 3; r++) {
-                const int t = grp + 16 * r;
-                if (t < ntask) {
-                    const int sl = t / nblk, tb = t - sl * nblk;
-                    conv_slice<TAIL>(xr[r], base[r], cw, ct, sl, sl < 2,
-                                     sl == 0 ? 0.08838834764831845f /* 128^-1/2 */ : 1.f, t0, L,
-                                     tb, s16, sl == 0 ? sm.Q : sl == 1 ? sm.K : sm.V);
-                }
-            }
         }
-        if (wave == 0) {
-            /* segments packed into the chunk: st = first token of this
-             * lane's segment, en = its last (63 for the chunk's last one) */
-            const uint64_t starts = chunk_starts ? chunk_starts[ch] | 1ull : 1ull;
-            const uint64_t upto = lane == 63 ? ~0ull : (2ull << lane) - 1;
-            const int st = 63 - __builtin_clzll(starts & upto);
-            const uint64_t later = starts & ~upto;
-            const int en = later ? __builtin_ctzll(later) - 1 : 63;
-            /* cumulative sum restarted at each segment start */
+        /* st = first token of this lane's segment, en = its last */
+        const int st = 63 - __builtin_clzll(starts & upto);
+        const uint64_t later = starts & ~upto;
+        const int en = later ? __builtin_ctzll(later) - 1 : 63;
 #pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const float up = __shfl_up(gv, o, 64);
-                if (lane - o >= st)
-                    gv += up;
-            }
-            const float gl = __shfl(gv, en, 64);
-            sm.Sid[lane] = __builtin_popcountll(starts & upto);
-            sm.G[lane] = gv;
-            sm.sK[lane] = bv * fast_exp(gv);
-            sm.sKg[lane] = fast_exp(gl - gv);
-            sm.sV[lane] = bv;
-            Glo[cb * 64 + lane] = gl; /* one copy per lane of phase B's waves */
+        for (int o = 1; o < 64; o <<= 1) { /* cumulative sum restarted per segment */
+            const float up = __shfl_up(gv, o, 64);
+            if (lane - o >= st)
+                gv += up;
         }
+        const float gl = __shfl(gv, en, 64);
+        sm.G[r][lane] = gv;
+        sm.sK[r][lane] = bv * fast_exp(gv);
+        sm.sKg[r][lane] = fast_exp(gl - gv);
+        sm.sV[r][lane] = bv;
+        Glo[((size_t)ch * Hv + hv) * 64 + lane] = gl; /* one copy per lane of phase B's waves */
     }
     lds_barrier();
 
-    /* ---- 2. K K^T, Q K^T; wave w owns the 32x32 tile (w>>1, w&1) ---- */
+    /* ---- 2. raw Q K^T (split) on waves 0-2, K K^T on waves 3, 6, 7: the
+     * lower 32x32 tiles (0,0), (1,0), (1,1) | q e^G of every v-head (waves
+     * 4-7, 16x16x32 A-fragment order: entry i holds row 16(i/256) + i%16,
+     * columns 32((i/64)%4) + 8((i/16)%4) .. +7) ---- */
+    const int u = tid - 256; /* waves 4-7: 0..255 */
     {
-        const int ti = wave >> 1, tj = wave & 1;
-        floatx16 kk = {}, qk = {};
-        if (ti >= tj) {
+        const bool isqk = wave < 3;
+        const int job = wave < 3 ? wave : wave == 3 ? 0 : wave >= 6 ? wave - 5 : -1;
+        if (job >= 0) {
+            const int ti = job == 0 ? 0 : 1, tj = job == 2 ? 1 : 0;
+            floatx16 acc = {};
 #pragma unroll
             for (int ks = 0; ks < DK / 16; ks++) {
                 const int c = 16 * ks + 8 * h;
-                const bf16x8 ak = *(const bf16x8 *)&sm.K[32 * ti + col][c];
-                const bf16x8 aq = *(const bf16x8 *)&sm.Q[32 * ti + col][c];
-                const bf16x8 bk = *(const bf16x8 *)&sm.K[32 * tj + col][c];
-                kk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, bk, kk, 0, 0, 0);
-                qk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, bk, qk, 0, 0, 0);
+                const bf16x8 bkh = ld8(&sm.Kh[32 * tj + col][c]);
+                if (isqk) {
+                    const bf16x8 aqh = ld8(&sm.Xh[32 * ti + col][c]);
+                    const bf16x8 aql = ld8(&sm.Xl[32 * ti + col][c]);
+                    const bf16x8 bkl = ld8(&sm.Kl[32 * tj + col][c]);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aqh, bkh, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aqh, bkl, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aql, bkh, acc, 0, 0, 0);
+                } else {
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld8(&sm.Kh[32 * ti + col][c]),
+                                                                  bkh, acc, 0, 0, 0);
+                }
+            }
+            float(*dst)[CH + 4] = isqk ? sm.QK : sm.KK;
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                dst[32 * ti + 8 * (r >> 2) + 4 * h + (r & 3)][32 * tj + col] = acc[r];
+        }
+        if (wave >= 4) {
+            const int t = u & 15, c8 = 32 * ((u >> 6) & 3) + 8 * ((u >> 4) & 3);
+            for (int r = 0; r < rep; r++) {
+                const size_t cb = (size_t)ch * Hv + hk * rep + r;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const bf16x8 a = ld8(&sm.Xh[16 * j + t][c8]), b = ld8(&sm.Xl[16 * j + t][c8]);
+                    const float eg = fast_exp(sm.G[r][16 * j + t]);
+                    bf16x8 o;
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        o[e] = f2bf((bf2f(a[e]) + bf2f(b[e])) * eg);
+                    *(bf16x8 *)(Qgo + (cb * 1024 + u + 256 * j) * 8) = o;
+                }
             }
         }
-        const int j = 32 * tj + col;
-        const float Gj = sm.G[j];
-        const int Sj = sm.Sid[j];
-        /* rows i = 32ti + 8m + 4h + 0..3: their G and beta four at a time,
-         * read unconditionally (a read under the mask becomes a branch) */
-        float Gi[16], Bi[16];
-        int Si[16];
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const float4 a = rd4(&sm.G[32 * ti + 8 * m + 4 * h]);
-            const float4 b = rd4(&sm.sV[32 * ti + 8 * m + 4 * h]);
-            const int4 c = *(const int4 *)&sm.Sid[32 * ti + 8 * m + 4 * h];
-            Gi[4 * m] = a.x, Gi[4 * m + 1] = a.y, Gi[4 * m + 2] = a.z, Gi[4 * m + 3] = a.w;
-            Bi[4 * m] = b.x, Bi[4 * m + 1] = b.y, Bi[4 * m + 2] = b.z, Bi[4 * m + 3] = b.w;
-            Si[4 * m] = c.x, Si[4 * m + 1] = c.y, Si[4 * m + 2] = c.z, Si[4 * m + 3] = c.w;
-        }
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int i = 32 * ti + 8 * (r >> 2) + 4 * h + (r & 3);
-            const float dec = fast_exp(fminf(Gi[r] - Gj, 0.f));
-            const bool same = Si[r] == Sj; /* tokens of one segment interact */
-            sm.AT[i][j] = i > j && same ? Bi[r] * kk[r] * dec : 0.f;
-            sm.QK[i][j] = f2bf(i >= j && same ? qk[r] * dec : 0.f);
-        }
     }
-    lds_barrier();
-    /* q e^G and the masked QK^T leave in 16x16x32 A-fragment order: entry
-     * i = (row block w, k-step s, lane l) holds row 16w + l%16, columns
-     * 32s + 8(l/16)..+7 */
+    lds_barrier(); /* raw products in LDS; the q rows may be overwritten */
+
+    bf16x8 eye[2]; /* B operand of the identity, k = 16s + 8h + e */
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int i = tid + 256 * j;
-        const int t = 16 * (i >> 8) + (i & 15), c8 = 32 * ((i >> 6) & 3) + 8 * ((i >> 4) & 3);
-        const float eg = fast_exp(sm.G[t]);
-        const bf16x8 qv = *(const bf16x8 *)&sm.Q[t][c8];
-        bf16x8 r;
+    for (int s = 0; s < 2; s++)
 #pragma unroll
         for (int e = 0; e < 8; e++)
-            r[e] = f2bf(bf2f(qv[e]) * eg);
-        *(bf16x8 *)(Qgo + (cb * 1024 + i) * 8) = r;
-    }
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int i = tid + 256 * j;
-        const int r = 16 * (i >> 7) + (i & 15), c8 = 32 * ((i >> 6) & 1) + 8 * ((i >> 4) & 3);
-        *(bf16x8 *)(QKo + (cb * 512 + i) * 8) = *(const bf16x8 *)&sm.QK[r][c8];
-    }
+            eye[s][e] = f2bf(16 * s + 8 * h + e == col ? 1.f : 0.f);
+    /* token of accumulator slot r of 32-row tile tb */
+    auto tok = [&](int tb, int r) { return 32 * tb + 8 * (r >> 2) + 4 * h + (r & 3); };
 
-    /* ---- 3. T = (I + A)^-1 in place ----
-     * 3a: wave w inverts diagonal block w, lane c < 16 owning column c; the
-     * block is read (all lanes, broadcast) before any lane writes it. */
-    if (lane < 16) {
-        const int b0 = 16 * wave, c = lane;
-        float t[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            float acc = 0.f;
-#pragma unroll
-            for (int k4 = 0; k4 < i; k4 += 4) {
-                const float4 a = rd4(&sm.AT[b0 + i][b0 + k4]);
-                acc = fmaf(a.x, t[k4], acc);
-                if (k4 + 1 < i)
-                    acc = fmaf(a.y, t[k4 + 1], acc);
-                if (k4 + 2 < i)
-                    acc = fmaf(a.z, t[k4 + 2], acc);
-                if (k4 + 3 < i)
-                    acc = fmaf(a.w, t[k4 + 3], acc);
-            }
-            t[i] = (i == c ? 1.f : 0.f) - acc;
-        }
-        /* stores only after every read of the block: the reads can all be
-         * issued up front (a store in the loop would keep them in order) */
-#pragma unroll
-        for (int i = 0; i < 16; i++)
-            if (i >= c)
-                sm.AT[b0 + i][b0 + c] = t[i];
-    }
-    lds_barrier();
-    /* 3b: inside 32x32 diagonal block p (wave p): T_10 = -T_11 (A_10 T_00),
-     * 16x16 blocks; lane = (row l/4, columns 4(l%4)..+3) */
-    if (wave < 2) {
-        const int p0 = 32 * wave, r = lane >> 2, c0 = 4 * (lane & 3);
-        float *a10 = &sm.AT[p0 + 16 + r][p0];
-        const float4 x = row_times<16>(a10, &sm.AT[p0][p0 + c0]);
-        wr4(a10 + c0, x);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const float4 y = row_times<16>(&sm.AT[p0 + 16 + r][p0 + 16], &sm.AT[p0 + 16][p0 + c0]);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        wr4(a10 + c0, make_float4(-y.x, -y.y, -y.z, -y.w));
-    }
-    lds_barrier();
-    /* 3c: T_10 = -T_11 (A_10 T_00) with 32x32 blocks; lane = (row 8w + l/8,
-     * columns 4(l%8)..+3). A chunk of at most 32 tokens has A_10 = 0 and so
-     * T_10 = 0, which the A/T array already holds; only padding rows read it. */
-    if (L > 32) {
-        const int r = 32 + 8 * wave + (lane >> 3), c0 = 4 * (lane & 7);
-        const float4 x = row_times<32>(&sm.AT[r][0], &sm.AT[0][c0]);
-        lds_barrier();
-        wr4(&sm.AT[r][c0], x);
-        lds_barrier();
-        const float4 y = row_times<32>(&sm.AT[r][32], &sm.AT[32][c0]);
-        lds_barrier();
-        wr4(&sm.AT[r][c0], make_float4(-y.x, -y.y, -y.z, -y.w));
-    }
-    lds_barrier();
+    for (int r = 0; r < rep; r++) {
+        const int hv = hk * rep + r;
+        const size_t cb = (size_t)ch * Hv + hv;
+        const float *Gr = sm.G[r], *sKr = sm.sK[r], *sKgr = sm.sKg[r], *sVr = sm.sV[r];
+        /* per-iteration copies of the lane indices (see opaque()) */
+        const int tid = opaque(threadIdx.x), lane = tid & 63;
+        const int h = lane >> 5, col = lane & 31, grp = tid >> 4, s16 = tid & 15;
+        const int u = tid - 256;
+        auto tok = [&](int tb, int r_) { return 32 * tb + 8 * (r_ >> 2) + 4 * h + (r_ & 3); };
 
-    /* ---- 4. W = T (beta e^G K), U = T (beta V), (k e^{Glast-G})^T ----
-     * wave w: dk (= dv) block 32w, both 32-row halves of W and U. */
-    {
-        bf16x8 eye[2]; /* B operand of the identity, k = 16s + 8h + e */
+        /* ---- 3. the v-head's v rows (waves 0-3) ---- */
+        constexpr bool CONV = SRC != 0;
+        bf16x8 xr[7];
+        int base[4];
+        if (wave < 4) {
+            if constexpr (SRC == 0) {
+                rows_f32(vh + ((size_t)t0 * Hv + hv) * DV, (size_t)Hv * DV, L, tid, 256, sm.Xh,
+                         sm.Xl);
+            } else {
+                constexpr bool TAIL = SRC == 2;
+                if (grp < nblk) {
+                    const int n0 = t0 + 4 * grp;
+                    conv_rows(cv, (2 * Hk + hv) * DK + 8 * s16, n0, xr);
 #pragma unroll
-        for (int s = 0; s < 2; s++)
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                eye[s][e] = f2bf(16 * s + 8 * h + e == col ? 1.f : 0.f);
-        floatx16 dK[2], dV[2]; /* D[tb] = rows 32tb.. of K (V), columns 32w.. */
-#pragma unroll
-        for (int tb = 0; tb < 2; tb++) {
-            dK[tb] = dV[tb] = floatx16{};
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-                const int c = 32 * wave + 16 * s + 8 * h;
-                dK[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    *(const bf16x8 *)&sm.K[32 * tb + col][c], eye[s], dK[tb], 0, 0, 0);
-                dV[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    *(const bf16x8 *)&sm.V[32 * tb + col][c], eye[s], dV[tb], 0, 0, 0);
+                    for (int j = 0; j < 4; j++)
+                        base[j] = cv.own_base[min(n0 + j, cv.N - 1)];
+                }
+                const int c0s[1] = {(2 * Hk + hv) * DK};
+                conv_stage<TAIL>(cv, c0s, 1, tid, 256, sm.cs, sm.cs + 8 * 16 * 4);
+                const int zrows = CH - 4 * nblk;
+                for (int i = tid; i < 2 * zrows * 16; i += 256) {
+                    const int a = i / (zrows * 16), rem = i - a * zrows * 16;
+                    bf16(*z)[DK + 8] = a == 0 ? sm.Xh : sm.Xl;
+                    *(bf16x8 *)&z[4 * nblk + (rem >> 4)][8 * (rem & 15)] = bf16x8{};
+                }
             }
         }
-        /* token of accumulator slot r of tile tb */
-        auto tok = [&](int tb, int r) { return 32 * tb + 8 * (r >> 2) + 4 * h + (r & 3); };
-        /* per-token scales of this lane's accumulator slots: slot r of tile tb
-         * is token 32tb + 8(r/4) + 4h + r%4, four consecutive tokens a read */
-        float sk[2][16], sv[2][16], skg[2][16];
-#pragma unroll
-        for (int tb = 0; tb < 2; tb++)
-#pragma unroll
-            for (int m = 0; m < 4; m++) {
-                const int t = 32 * tb + 8 * m + 4 * h;
-                const float4 a = rd4(&sm.sK[t]), b = rd4(&sm.sV[t]), c = rd4(&sm.sKg[t]);
-                sk[tb][4 * m] = a.x, sk[tb][4 * m + 1] = a.y, sk[tb][4 * m + 2] = a.z, sk[tb][4 * m + 3] = a.w;
-                sv[tb][4 * m] = b.x, sv[tb][4 * m + 1] = b.y, sv[tb][4 * m + 2] = b.z, sv[tb][4 * m + 3] = b.w;
-                skg[tb][4 * m] = c.x, skg[tb][4 * m + 1] = c.y, skg[tb][4 * m + 2] = c.z, skg[tb][4 * m + 3] = c.w;
+        lds_barrier();
+
+        /* ---- 4. v rows (waves 0-3, conv form) | masked QK^T and A
+         * (waves 4-7) ---- */
+        if (wave < 4) {
+            if constexpr (CONV) {
+                if (grp < nblk)
+                    conv_slice<SRC == 2>(xr, base, sm.cs, sm.cs + 8 * 16 * 4, 0, false, 1.f, t0, L,
+                                         grp, s16, sm.Xh, sm.Xl);
             }
-        bf16x8 xk[4], xv[4];
+        } else {
+            /* masked QK^T = tril(q_i.k_j e^{G_i-G_j}) within a segment, as hi
+             * and lo 16x16x32 A fragments: entry i holds row 16(i/128) + i%16,
+             * columns 32((i/64)%2) + 8((i/16)%4) .. +7 */
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const int tb = ks >> 1, r0 = 8 * (ks & 1);
+            for (int j = 0; j < 2; j++) {
+                const int i = u + 256 * j;
+                const int rr = 16 * (i >> 7) + (i & 15), c8 = 32 * ((i >> 6) & 1) + 8 * ((i >> 4) & 3);
+                const float Gi = Gr[rr];
+                const int Si = sm.Sid[rr];
+                const float4 q0 = rd4(&sm.QK[rr][c8]), q1 = rd4(&sm.QK[rr][c8 + 4]);
+                const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                bf16x8 oh, ol;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                xk[ks][e] = f2bf(dK[tb][r0 + e] * sk[tb][r0 + e]);
-                xv[ks][e] = f2bf(dV[tb][r0 + e] * sv[tb][r0 + e]);
+                for (int e = 0; e < 8; e++) {
+                    const int cj = c8 + e;
+                    const bool keep = rr >= cj && Si == sm.Sid[cj];
+                    const float v = keep ? qv[e] * fast_exp(fminf(Gi - Gr[cj], 0.f)) : 0.f;
+                    { const bfpair sp_ = split2(v); oh[e] = sp_.hi; ol[e] = sp_.lo; }
+                }
+                *(bf16x8 *)(QKo + (cb * 1024 + i) * 8) = oh;
+                *(bf16x8 *)(QKo + (cb * 1024 + 512 + i) * 8) = ol;
             }
-        }
-        /* (k e^{Glast-G})^T as 32x32x16 A fragments (row dk = 32w + l%32,
-         * tokens 16s + 8(l/32)..+7): the lane pair (l, l^32) trades halves */
+            /* A = tril(beta_i e^{G_i-G_j} k_i.k_j, -1) within a segment, zero
+             * elsewhere (the inverse reads the upper part of its blocks):
+             * row u/4, columns 16(u%4) .. +15 */
+            {
+                const int ri = u >> 2, c16b = 16 * (u & 3);
+                const float Gi = Gr[ri], bi = sVr[ri];
+                const int Si = sm.Sid[ri];
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const int tb = s >> 1, r0 = 8 * (s & 1);
-            float v[8];
+                for (int c4 = 0; c4 < 16; c4 += 4) {
+                    const float4 kk = rd4(&sm.KK[ri][c16b + c4]);
+                    const float kv[4] = {kk.x, kk.y, kk.z, kk.w};
+                    float a[4];
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-                v[e] = dK[tb][r0 + e] * skg[tb][r0 + e];
-            /* h=0 holds tokens +0..3 | +8..11, h=1 holds +4..7 | +12..15 */
-            uint32_t p0[2], p1[2];
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                p0[e] = __builtin_bit_cast(uint32_t, bf16x2{f2bf(v[2 * e]), f2bf(v[2 * e + 1])});
-                p1[e] = __builtin_bit_cast(uint32_t, bf16x2{f2bf(v[4 + 2 * e]), f2bf(v[5 + 2 * e])});
-            }
-            uint32_t o[4];
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const uint32_t x1 = (uint32_t)__shfl_xor((int)p1[e], 32, 64);
-                const uint32_t x0 = (uint32_t)__shfl_xor((int)p0[e], 32, 64);
-                o[e] = h ? x1 : p0[e];
-                o[2 + e] = h ? p1[e] : x0;
-            }
-            *(u32x4 *)(KgTo + (cb * 1024 + (wave * 4 + s) * 64 + lane) * 8) =
-                u32x4{o[0], o[1], o[2], o[3]};
-        }
-        floatx16 w[2] = {}, u[2] = {};
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-#pragma unroll
-            for (int mi = 0; mi < 2; mi++) {
-                const float *tr = &sm.AT[32 * mi + col][16 * ks + 4 * h];
-                const float4 a0 = rd4(tr), a1 = rd4(tr + 8);
-                const bf16x8 a = {f2bf(a0.x), f2bf(a0.y), f2bf(a0.z), f2bf(a0.w),
-                                  f2bf(a1.x), f2bf(a1.y), f2bf(a1.z), f2bf(a1.w)};
-                w[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xk[ks], w[mi], 0, 0, 0);
-                u[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xv[ks], u[mi], 0, 0, 0);
+                    for (int e = 0; e < 4; e++) {
+                        const int cj = c16b + c4 + e;
+                        const bool keep = ri > cj && Si == sm.Sid[cj];
+                        a[e] = keep ? bi * kv[e] * fast_exp(fminf(Gi - Gr[cj], 0.f)) : 0.f;
+                    }
+                    wr4(&sm.AT[ri][c16b + c4], make_float4(a[0], a[1], a[2], a[3]));
+                }
             }
         }
-        lds_barrier(); /* every wave is done with the v rows */
+        lds_barrier();
+
+        /* ---- 5. T = (I + A)^-1 in place (waves 0-3) | (K e^{G_last-G})^T
+         * as hi + lo (waves 4-7, dk block 32(w-4)) ----
+         * 5a: wave w < 4 inverts diagonal block w, lane c < 16 owning column
+         * c; the block is read (all lanes, broadcast) before any lane writes. */
+        if (wave < 4) {
+            if (lane < 16) {
+                const int b0 = 16 * wave, c = lane;
+                float t[16];
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
+                for (int i = 0; i < 16; i++) {
+                    float acc = 0.f;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int i = tok(mi, r);
-                sm.Q[i][32 * wave + col] = f2bf(w[mi][r]);
-                sm.V[i][32 * wave + col] = f2bf(u[mi][r]);
+                    for (int k4 = 0; k4 < i; k4 += 4) {
+                        const float4 a = rd4(&sm.AT[b0 + i][b0 + k4]);
+                        acc = fmaf(a.x, t[k4], acc);
+                        if (k4 + 1 < i)
+                            acc = fmaf(a.y, t[k4 + 1], acc);
+                        if (k4 + 2 < i)
+                            acc = fmaf(a.z, t[k4 + 2], acc);
+                        if (k4 + 3 < i)
+                            acc = fmaf(a.w, t[k4 + 3], acc);
+                    }
+                    t[i] = (i == c ? 1.f : 0.f) - acc;
+                }
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    if (i >= c)
+                        sm.AT[b0 + i][b0 + c] = t[i];
+            }
+        } else {
+            const int w4 = wave - 4;
+            floatx16 dK[2];
+#pragma unroll
+            for (int tb = 0; tb < 2; tb++) {
+                dK[tb] = floatx16{};
+#pragma unroll
+                for (int s = 0; s < 2; s++) { /* identity products: exact */
+                    const int c = 32 * w4 + 16 * s + 8 * h;
+                    dK[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld8(&sm.Kh[32 * tb + col][c]),
+                                                                     eye[s], dK[tb], 0, 0, 0);
+                    dK[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld8(&sm.Kl[32 * tb + col][c]),
+                                                                     eye[s], dK[tb], 0, 0, 0);
+                }
+            }
+            /* 32x32x16 A fragments (row dk = 32 w4 + l%32, tokens 16s +
+             * 8(l/32)..+7): the lane pair (l, l^32) trades halves */
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const int tb = s >> 1, r0 = 8 * (s & 1);
+                bf16 vh_[8], vl_[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    { const bfpair sp_ = split2(dK[tb][r0 + e] * sKgr[tok(tb, r0 + e)]); vh_[e] = sp_.hi; vl_[e] = sp_.lo; }
+#pragma unroll
+                for (int part = 0; part < 2; part++) {
+                    const bf16 *v = part ? vl_ : vh_;
+                    uint32_t p0[2], p1[2];
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        p0[e] = __builtin_bit_cast(uint32_t, bf16x2{v[2 * e], v[2 * e + 1]});
+                        p1[e] = __builtin_bit_cast(uint32_t, bf16x2{v[4 + 2 * e], v[5 + 2 * e]});
+                    }
+                    uint32_t o[4];
+#pragma unroll
+                    for (int e = 0; e < 2; e++) { /* h=0 holds tokens +0..3 | +8..11 */
+                        const uint32_t x1 = (uint32_t)__shfl_xor((int)p1[e], 32, 64);
+                        const uint32_t x0 = (uint32_t)__shfl_xor((int)p0[e], 32, 64);
+                        o[e] = h ? x1 : p0[e];
+                        o[2 + e] = h ? p1[e] : x0;
+                    }
+                    *(u32x4 *)(KgTo + (cb * 2048 + part * 1024 + (w4 * 4 + s) * 64 + lane) * 8) =
+                        u32x4{o[0], o[1], o[2], o[3]};
+                }
             }
         }
-    }
-    lds_barrier();
-    /* ---- 5. W in the fragment order of q e^G; U as 16x16 accumulator
-     * fragments: entry i = (32-column block cbk, row block w, lane l) holds
-     * rows 16w + 4(l/16) + 0..3 of columns 32cbk + l%16 (values 0..3) and
-     * 32cbk + 16 + l%16 (values 4..7) ---- */
+        lds_barrier();
+        /* 5b: inside 32x32 diagonal block p (wave p): T_10 = -T_11 (A_10 T_00),
+         * 16x16 blocks; lane = (row l/4, columns 4(l%4)..+3) */
+        if (wave < 2) {
+            const int p0 = 32 * wave, rr = lane >> 2, c0 = 4 * (lane & 3);
+            float *a10 = &sm.AT[p0 + 16 + rr][p0];
+            const float4 x = row_times<16>(a10, &sm.AT[p0][p0 + c0]);
+            wr4(a10 + c0, x);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            const float4 y = row_times<16>(&sm.AT[p0 + 16 + rr][p0 + 16], &sm.AT[p0 + 16][p0 + c0]);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            wr4(a10 + c0, make_float4(-y.x, -y.y, -y.z, -y.w));
+        }
+        lds_barrier();
+        /* 5c: T_10 = -T_11 (A_10 T_00) with 32x32 blocks; lane = (row 8w +
+         * l/8, columns 4(l%8)..+3). A chunk of at most 32 tokens has A_10 = 0
+         * and so T_10 = 0, which the array already holds. Every wave passes
+         * the same barriers; waves 4-7 have no rows. */
+        if (L > 32) {
+            const int rr = 32 + 8 * wave + (lane >> 3), c0 = 4 * (lane & 7);
+            float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (wave < 4)
+                x = row_times<32>(&sm.AT[rr][0], &sm.AT[0][c0]);
+            lds_barrier();
+            if (wave < 4)
+                wr4(&sm.AT[rr][c0], x);
+            lds_barrier();
+            float4 y = x;
+            if (wave < 4)
+                y = row_times<32>(&sm.AT[rr][32], &sm.AT[32][c0]);
+            lds_barrier();
+            if (wave < 4)
+                wr4(&sm.AT[rr][c0], make_float4(-y.x, -y.y, -y.z, -y.w));
+            lds_barrier();
+        }
+
+        /* ---- 6. W = T (beta e^G K) on waves 0-3 (dk block 32w, K hi) and
+         * U = T (beta V) on waves 4-7 (dv block 32(w-4), V hi + lo) ---- */
+        {
+            const int w4 = wave & 3;
+            const bool isw = wave < 4;
+            floatx16 dX[2]; /* rows 32tb.. of K (or V), columns 32 w4.. */
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int i = tid + 256 * j;
-        const int t = 16 * (i >> 8) + (i & 15), c8 = 32 * ((i >> 6) & 3) + 8 * ((i >> 4) & 3);
-        *(bf16x8 *)(Wo + (cb * 1024 + i) * 8) = *(const bf16x8 *)&sm.Q[t][c8];
-        const int tu = 16 * ((i >> 6) & 3) + 4 * ((i >> 4) & 3), cu = 32 * (i >> 8) + (i & 15);
-        bf16x8 r;
+            for (int tb = 0; tb < 2; tb++) {
+                dX[tb] = floatx16{};
 #pragma unroll
-        for (int e = 0; e < 8; e++)
-            r[e] = sm.V[tu + (e & 3)][cu + 16 * (e >> 2)];
-        *(bf16x8 *)(Uo + (cb * 1024 + i) * 8) = r;
+                for (int s = 0; s < 2; s++) {
+                    const int c = 32 * w4 + 16 * s + 8 * h;
+                    if (isw) {
+                        dX[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            ld8(&sm.Kh[32 * tb + col][c]), eye[s], dX[tb], 0, 0, 0);
+                    } else {
+                        dX[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            ld8(&sm.Xh[32 * tb + col][c]), eye[s], dX[tb], 0, 0, 0);
+                        dX[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            ld8(&sm.Xl[32 * tb + col][c]), eye[s], dX[tb], 0, 0, 0);
+                    }
+                }
+            }
+            /* B operands: token k-steps ks (tile ks/2, rows 8(ks%2)..), the
+             * per-token scale beta e^G (K) or beta (V); V also keeps lo */
+            bf16x8 xb[4], xl[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                const int tb = ks >> 1, r0 = 8 * (ks & 1);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int t = tok(tb, r0 + e);
+                    const float x = dX[tb][r0 + e] * (isw ? sKr[t] : sVr[t]);
+                    { const bfpair sp_ = split2(x); xb[ks][e] = sp_.hi; xl[ks][e] = sp_.lo; }
+                }
+            }
+            floatx16 acc[2] = {};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++) {
+                    /* T row 32mi + col, columns in the accumulator order */
+                    const float *tr = &sm.AT[32 * mi + col][16 * ks + 4 * h];
+                    const float4 a0 = rd4(tr), a1 = rd4(tr + 8);
+                    const bf16x8 a = {f2bf(a0.x), f2bf(a0.y), f2bf(a0.z), f2bf(a0.w),
+                                      f2bf(a1.x), f2bf(a1.y), f2bf(a1.z), f2bf(a1.w)};
+                    acc[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xb[ks], acc[mi], 0, 0, 0);
+                    if (!isw)
+                        acc[mi] =
+                            __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xl[ks], acc[mi], 0, 0, 0);
+                }
+            }
+            lds_barrier(); /* every wave is done with T and the v rows */
+            bf16(*Wst)[DK + 8] = reinterpret_cast<bf16(*)[DK + 8]>(&sm.AT[0][0]);
+            float(*Ust)[DV + 4] = reinterpret_cast<float(*)[DV + 4]>(&sm.Xh[0][0]);
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int rr = 0; rr < 16; rr++) {
+                    if (isw)
+                        Wst[tok(mi, rr)][32 * w4 + col] = f2bf(acc[mi][rr]);
+                    else
+                        Ust[tok(mi, rr)][32 * w4 + col] = acc[mi][rr];
+                }
+        }
+        lds_barrier();
+        /* ---- 7. W in the fragment order of q e^G; U (fp32) as 16x16
+         * accumulator fragments: entry i = (32-column block i/256, row block
+         * (i/64)%4, lane i%64) holds rows 16((i/64)%4) + 4((i/16)%4) + 0..3 of
+         * columns 32(i/256) + i%16 (values 0..3) and +16 (values 4..7) ---- */
+        {
+            bf16(*Wst)[DK + 8] = reinterpret_cast<bf16(*)[DK + 8]>(&sm.AT[0][0]);
+            float(*Ust)[DV + 4] = reinterpret_cast<float(*)[DV + 4]>(&sm.Xh[0][0]);
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int i = tid + PA_THREADS * j;
+                const int t = 16 * (i >> 8) + (i & 15), c8 = 32 * ((i >> 6) & 3) + 8 * ((i >> 4) & 3);
+                *(bf16x8 *)(Wo + (cb * 1024 + i) * 8) = ld8(&Wst[t][c8]);
+                const int tu = 16 * ((i >> 6) & 3) + 4 * ((i >> 4) & 3), cu = 32 * (i >> 8) + (i & 15);
+                float *dst = Uo + (cb * 1024 + i) * 8;
+                *(float4 *)dst = make_float4(Ust[tu][cu], Ust[tu + 1][cu], Ust[tu + 2][cu],
+                                             Ust[tu + 3][cu]);
+                *(float4 *)(dst + 4) = make_float4(Ust[tu][cu + 16], Ust[tu + 1][cu + 16],
+                                                   Ust[tu + 2][cu + 16], Ust[tu + 3][cu + 16]);
+            }
+        }
+        lds_barrier(); /* the next v-head rewrites G, AT and the v rows */
     }
 }
 
@@ -779,31 +931,35 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_a_kernel(
  * accumulator) and chunk tokens 16w..16w+15. Per chunk:
  *   S (bf16) -> LDS as S^T; barrier
  *   V'_w = U_w - W_w S,  O_w = (Q e^G)_w S          (16x16x32, 16 MFMAs)
- *   V'_w (bf16) -> LDS as V'^T; barrier
- *   S_w = e^{G_last} S_w + (K e^{G_last-G})^T_w V'  (32x32x16, 4 MFMAs)
- *   O_w += QKm_w V'                                  (16x16x32, 4 MFMAs)
+ *   V'_w as hi + lo (bf16) -> LDS as V'^T; barrier
+ *   S_w = e^{G_last} S_w + (K e^{G_last-G})^T_w V'  (32x32x16; hi.hi,
+ *                                                    hi.lo, lo.hi: 12 MFMAs)
+ *   O_w += QKm_w V'                                  (16x16x32, likewise 12)
+ *   O (fp32) out through a per-wave LDS tile.
  * Phase A stored every operand in fragment order, so each lane loads its
- * fragments with 16-byte reads straight into registers, two chunks ahead.
+ * fragments with 16-byte reads straight into registers, one chunk ahead.
  * The NCB workgroups of one unit share those operands; block numbering puts
  * them on one XCD (blockIdx % 8 picks the XCD), so their L2 serves the
  * repeats. */
 constexpr int NCB = DV / 32;
 
 struct BOps {
-    bf16x8 w[4], qg[4], qk[2], kg[4], u;
+    bf16x8 w[4], qg[4], qkh[2], qkl[2], kgh[4], kgl[4];
+    float4 u[2];
     float gl;
 };
 
 __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
     const bf16x8 *__restrict__ Wi, const bf16x8 *__restrict__ Qgi, const bf16x8 *__restrict__ QKi,
-    const bf16x8 *__restrict__ KgTi, const bf16x8 *__restrict__ Ui, const float *__restrict__ Gli,
+    const bf16x8 *__restrict__ KgTi, const float4 *__restrict__ Ui, const float *__restrict__ Gli,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
     const int32_t *__restrict__ seg_chunk0, const int32_t *__restrict__ seg_nchunk,
     const float *__restrict__ S_in, float *__restrict__ S_out, int Hv, int units,
-    bf16 *__restrict__ o, TailJob tail) {
-    __shared__ __attribute__((aligned(16))) bf16 sT[32][DK + 8];  /* S^T [column][dk]     */
-    __shared__ __attribute__((aligned(16))) bf16 vT[32][CH + 8];  /* V'^T [column][token] */
-    __shared__ __attribute__((aligned(16))) bf16 ost[4][16][40];  /* per-wave O tile      */
+    float *__restrict__ o, TailJob tail) {
+    __shared__ __attribute__((aligned(16))) bf16 sT[32][DK + 8];   /* S^T [column][dk]        */
+    __shared__ __attribute__((aligned(16))) bf16 vTh[32][CH + 8];  /* V'^T hi [column][token] */
+    __shared__ __attribute__((aligned(16))) bf16 vTl[32][CH + 8];  /* V'^T lo                 */
+    __shared__ __attribute__((aligned(16))) float ost[4][16][36];  /* per-wave O tile         */
 
     const int bid = blockIdx.x;
     const int nmain = NCB * ((units + 7) / 8) * 8;
@@ -823,10 +979,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
         }
         return;
     }
-    const int u = (bid & 7) + 8 * ((bid >> 3) / NCB), cbk = (bid >> 3) % NCB;
-    if (u >= units)
+    const int un = (bid & 7) + 8 * ((bid >> 3) / NCB), cbk = (bid >> 3) % NCB;
+    if (un >= units)
         return;
-    const int seg = u / Hv, hv = u - seg * Hv;
+    const int seg = un / Hv, hv = un - seg * Hv;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5, c32 = lane & 31, q4 = lane >> 4, c16 = lane & 15;
@@ -840,8 +996,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
     }
     /* consume S here, before any operand prefetch is in flight: S then enters
      * the chunk loop as a VALU result, and the loop's waits only cover the
-     * operand set a step uses (a pending load there would turn the loop-head
-     * wait into vmcnt(0), draining the prefetches every round) */
+     * operand set a step uses */
 #pragma unroll
     for (int r = 0; r < 16; r++)
         S[r] += 0.f;
@@ -851,21 +1006,26 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
         const size_t cb = (size_t)ch * Hv + hv;
         const bf16x8 *w = Wi + cb * 1024 + wave * 256 + lane;
         const bf16x8 *qg = Qgi + cb * 1024 + wave * 256 + lane;
-        const bf16x8 *kg = KgTi + cb * 1024 + wave * 256 + lane;
-        const bf16x8 *qk = QKi + cb * 512 + wave * 128 + lane;
+        const bf16x8 *kg = KgTi + cb * 2048 + wave * 256 + lane;
+        const bf16x8 *qk = QKi + cb * 1024 + wave * 128 + lane;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             op.w[s] = w[64 * s];
-            op.kg[s] = kg[64 * s];
+            op.kgh[s] = kg[64 * s];
+            op.kgl[s] = kg[1024 + 64 * s];
         }
-        op.u = Ui[cb * 1024 + (cbk * 4 + wave) * 64 + lane];
+        const float4 *up = Ui + (cb * 1024 + (cbk * 4 + wave) * 64 + lane) * 2;
+        op.u[0] = up[0];
+        op.u[1] = up[1];
         op.gl = Gli[cb * 64 + lane];
 #pragma unroll
         for (int s = 0; s < 4; s++)
             op.qg[s] = qg[64 * s];
 #pragma unroll
-        for (int s = 0; s < 2; s++)
-            op.qk[s] = qk[64 * s];
+        for (int s = 0; s < 2; s++) {
+            op.qkh[s] = qk[64 * s];
+            op.qkl[s] = qk[512 + 64 * s];
+        }
     };
 
     /* A segment's chunks are consecutive 64-token slices: token offsets
@@ -901,66 +1061,78 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
 #pragma unroll
             for (int jb = 0; jb < 2; jb++)
                 O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qg[s], sb[s][jb], O[jb], 0, 0, 0);
+        const float uf[8] = {op.u[0].x, op.u[0].y, op.u[0].z, op.u[0].w,
+                             op.u[1].x, op.u[1].y, op.u[1].z, op.u[1].w};
 #pragma unroll
         for (int jb = 0; jb < 2; jb++) {
-            bf16x4 p;
+            bf16x4 ph, pl;
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                p[i] = f2bf(bf2f(op.u[4 * jb + i]) - V[jb][i]);
-            *(bf16x4 *)&vT[16 * jb + c16][16 * wave + 4 * q4] = p;
+                { const bfpair sp_ = split2(uf[4 * jb + i] - V[jb][i]); ph[i] = sp_.hi; pl[i] = sp_.lo; }
+            *(bf16x4 *)&vTh[16 * jb + c16][16 * wave + 4 * q4] = ph;
+            *(bf16x4 *)&vTl[16 * jb + c16][16 * wave + 4 * q4] = pl;
         }
         lds_barrier();
-        bf16x8 vb[4], vb2[2][2];
+        bf16x8 vbh[4], vbl[4], v2h[2][2], v2l[2][2];
 #pragma unroll
-        for (int s = 0; s < 4; s++)
-            vb[s] = *(const bf16x8 *)&vT[c32][16 * s + 8 * h];
+        for (int s = 0; s < 4; s++) {
+            vbh[s] = *(const bf16x8 *)&vTh[c32][16 * s + 8 * h];
+            vbl[s] = *(const bf16x8 *)&vTl[c32][16 * s + 8 * h];
+        }
 #pragma unroll
         for (int s = 0; s < 2; s++)
 #pragma unroll
-            for (int jb = 0; jb < 2; jb++)
-                vb2[s][jb] = *(const bf16x8 *)&vT[16 * jb + c16][32 * s + 8 * q4];
+            for (int jb = 0; jb < 2; jb++) {
+                v2h[s][jb] = *(const bf16x8 *)&vTh[16 * jb + c16][32 * s + 8 * q4];
+                v2l[s][jb] = *(const bf16x8 *)&vTl[16 * jb + c16][32 * s + 8 * q4];
+            }
         S = S * dec;
 #pragma unroll
-        for (int s = 0; s < 4; s++)
-            S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kg[s], vb[s], S, 0, 0, 0);
+        for (int s = 0; s < 4; s++) {
+            S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgh[s], vbh[s], S, 0, 0, 0);
+            S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgh[s], vbl[s], S, 0, 0, 0);
+            S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgl[s], vbh[s], S, 0, 0, 0);
+        }
 #pragma unroll
         for (int s = 0; s < 2; s++)
 #pragma unroll
-            for (int jb = 0; jb < 2; jb++)
-                O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qk[s], vb2[s][jb], O[jb], 0, 0, 0);
-        /* O (bf16) through this wave's LDS tile: 16-byte stores, 64 bytes a row */
+            for (int jb = 0; jb < 2; jb++) {
+                O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qkh[s], v2h[s][jb], O[jb], 0, 0, 0);
+                O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qkh[s], v2l[s][jb], O[jb], 0, 0, 0);
+                O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qkl[s], v2h[s][jb], O[jb], 0, 0, 0);
+            }
+        /* O (fp32) through this wave's LDS tile: 32-byte stores, 128 bytes a row */
 #pragma unroll
         for (int jb = 0; jb < 2; jb++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                ost[wave][4 * q4 + i][16 * jb + c16] = f2bf(O[jb][i]);
+                ost[wave][4 * q4 + i][16 * jb + c16] = O[jb][i];
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int r = lane >> 2, c8 = 8 * (lane & 3);
-        const bf16x8 ov = *(const bf16x8 *)&ost[wave][r][c8];
-        if (16 * wave + r < L)
-            *(bf16x8 *)(o + ((size_t)(t0 + 16 * wave + r) * Hv + hv) * DV + col0 + c8) = ov;
+        const float4 o0 = *(const float4 *)&ost[wave][r][c8];
+        const float4 o1 = *(const float4 *)&ost[wave][r][c8 + 4];
+        if (16 * wave + r < L) {
+            float *dst = o + ((size_t)(t0 + 16 * wave + r) * Hv + hv) * DV + col0 + c8;
+            *(float4 *)dst = o0;
+            *(float4 *)(dst + 4) = o1;
+        }
     };
 
-    /* three operand sets in rotation: chunk ci + 2 loads while ci runs. The
+    /* two operand sets in rotation: chunk ci + 1 loads while ci runs. The
      * loads are unconditional (past the end they repeat the last chunk) so
      * the compiler's wait counts stay exact: a load skipped on one path makes
      * the next use wait for every load in flight. */
     if (nc > 0) {
         auto cl = [&](int ci) { return c0 + min(ci, nc - 1); };
-        BOps A, B, C;
+        BOps A, B;
         load(cl(0), A);
-        load(cl(1), B);
-        for (int ci = 0; ci < nc; ci += 3) {
-            load(cl(ci + 2), C);
+        for (int ci = 0; ci < nc; ci += 2) {
+            load(cl(ci + 1), B);
             step(c0 + ci, A);
             if (ci + 1 >= nc)
                 break;
-            load(cl(ci + 3), A);
+            load(cl(ci + 2), A);
             step(c0 + ci + 1, B);
-            if (ci + 2 >= nc)
-                break;
-            load(cl(ci + 4), B);
-            step(c0 + ci + 2, C);
         }
     }
     if (S_out && seg == 0) {
@@ -977,27 +1149,31 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
 /* ---------------------------------------------------------------------- */
 /* Every segment starts from the same S_in and nothing carries over between
  * them, so a workgroup takes one v-head and spw consecutive segments (as many
- * as keep about SB_WGS workgroups busy): S^T (bf16) goes to LDS once, then
- * per segment wave w (of 8: short per-wave chains, since a few branches
- * give few workgroups) computes columns 16w..16w+15 of
- *   V' = U - W S,  O = (Q e^G) S + QKm V'
- * for the 16-row blocks that hold tokens (the same 16x16x32 steps and
- * operand fragments as gdn_chunk_b_kernel), and the workgroup applies the
- * gated RMSNorm of gdn_norm_gate_kernel to the segment's rows. */
+ * as keep about SB_WGS workgroups busy). Wave w (of 8: short per-wave chains,
+ * since a few branches give few workgroups) owns state columns 16w..16w+15:
+ * its S^T fragments (bf16) are read once into registers, then per segment it
+ * computes those columns of
+ *   V' = U - W S (hi + lo),  O = (Q e^G) S + QKm V'
+ * for the 16-row blocks that hold tokens (the fragments and split products
+ * of gdn_chunk_b_kernel), and the workgroup applies the gated RMSNorm of
+ * gdn_norm_gate_kernel to the segment's fp32 rows. */
 constexpr int SB_WGS = 512;
 constexpr int SB_THREADS = 512; /* 8 waves, 16 state columns each */
 
 __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
     const bf16x8 *__restrict__ Wi, const bf16x8 *__restrict__ Qgi, const bf16x8 *__restrict__ QKi,
-    const bf16x8 *__restrict__ Ui, const int32_t *__restrict__ chunk_tok0,
+    const float4 *__restrict__ Ui, const int32_t *__restrict__ chunk_tok0,
     const int32_t *__restrict__ chunk_len, const int32_t *__restrict__ seg_chunk0,
     const int32_t *__restrict__ seg_nchunk, int nseg, int spw, const float *__restrict__ S_in,
-    int Hv,
-    const bf16 *__restrict__ z, int zs, const float *__restrict__ nw, float eps,
+    int Hv, const bf16 *__restrict__ z, int zs, const float *__restrict__ nw, float eps,
     bf16 *__restrict__ y) {
-    __shared__ __attribute__((aligned(16))) bf16 sT[DV][DK + 8]; /* S^T [column][dk]       */
-    __shared__ __attribute__((aligned(16))) bf16 vT[DV][CH + 8]; /* V'^T [column][token]   */
-    __shared__ __attribute__((aligned(16))) bf16 ob[CH][DV + 8]; /* O (bf16) [token][column] */
+    /* S^T staging at the start, then each segment's fp32 O rows */
+    __shared__ __attribute__((aligned(16))) unsigned char so_raw[sizeof(bf16) * DV * (DK + 8)];
+    __shared__ __attribute__((aligned(16))) bf16 vTh[DV][CH + 8]; /* V'^T hi [column][token] */
+    __shared__ __attribute__((aligned(16))) bf16 vTl[DV][CH + 8]; /* V'^T lo                 */
+    bf16(*sT)[DK + 8] = reinterpret_cast<bf16(*)[DK + 8]>(so_raw);
+    float(*ob)[DV + 4] = reinterpret_cast<float(*)[DV + 4]>(so_raw);
+    static_assert(sizeof(float) * CH * (DV + 4) <= sizeof(bf16) * DV * (DK + 8), "O staging");
 
     const int hv = blockIdx.y, sg0 = blockIdx.x * spw;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1028,9 +1204,16 @@ __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
     }
     /* V'^T rows past a segment's last 16-row block may be read by the QKm
      * step (times an exact zero of the causal mask): keep them finite */
-    for (int i = tid; i < DV * (CH + 8) / 8; i += SB_THREADS)
-        ((bf16x8 *)&vT[0][0])[i] = bf16x8{};
+    for (int i = tid; i < DV * (CH + 8) / 8; i += SB_THREADS) {
+        ((bf16x8 *)&vTh[0][0])[i] = bf16x8{};
+        ((bf16x8 *)&vTl[0][0])[i] = bf16x8{};
+    }
     lds_barrier();
+    bf16x8 sb[4]; /* this wave's S^T fragments, the same for every segment */
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+        sb[s] = *(const bf16x8 *)&sT[col0 + c16][32 * s + 8 * q4];
+    lds_barrier(); /* sT's space now holds O */
 
     float wl[8];
 #pragma unroll
@@ -1063,20 +1246,21 @@ __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
             }
             /* U fragment of the 32-column block holding these 16 columns:
              * values 0..3 its first 16 columns, 4..7 the second */
-            const bf16x8 u = Ui[cb * 1024 + ((wave >> 1) * 4 + rb) * 64 + lane];
-            const int jh = 4 * (wave & 1);
+            const float4 *up = Ui + (cb * 1024 + ((wave >> 1) * 4 + rb) * 64 + lane) * 2;
+            const float4 uu = up[wave & 1];
             floatx4 V = {};
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                const bf16x8 sb = *(const bf16x8 *)&sT[col0 + c16][32 * s + 8 * q4];
-                V = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[s], sb, V, 0, 0, 0);
-                O[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qg[s], sb, O[rb], 0, 0, 0);
+                V = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[s], sb[s], V, 0, 0, 0);
+                O[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qg[s], sb[s], O[rb], 0, 0, 0);
             }
-            bf16x4 p;
+            const float uf[4] = {uu.x, uu.y, uu.z, uu.w};
+            bf16x4 ph, pl;
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                p[i] = f2bf(bf2f(u[jh + i]) - V[i]);
-            *(bf16x4 *)&vT[col0 + c16][16 * rb + 4 * q4] = p;
+                { const bfpair sp_ = split2(uf[i] - V[i]); ph[i] = sp_.hi; pl[i] = sp_.lo; }
+            *(bf16x4 *)&vTh[col0 + c16][16 * rb + 4 * q4] = ph;
+            *(bf16x4 *)&vTl[col0 + c16][16 * rb + 4 * q4] = pl;
         }
         /* the wave reads back only its own columns of V'^T: LDS order suffices */
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1088,26 +1272,32 @@ __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
             for (int s = 0; s < 2; s++) {
                 if (s >= nks)
                     continue;
-                const bf16x8 qk = QKi[cb * 512 + rb * 128 + 64 * s + lane];
-                const bf16x8 vb = *(const bf16x8 *)&vT[col0 + c16][32 * s + 8 * q4];
-                O[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qk, vb, O[rb], 0, 0, 0);
+                const bf16x8 qkh = QKi[cb * 1024 + rb * 128 + 64 * s + lane];
+                const bf16x8 qkl = QKi[cb * 1024 + 512 + rb * 128 + 64 * s + lane];
+                const bf16x8 vh_ = *(const bf16x8 *)&vTh[col0 + c16][32 * s + 8 * q4];
+                const bf16x8 vl_ = *(const bf16x8 *)&vTl[col0 + c16][32 * s + 8 * q4];
+                O[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qkh, vh_, O[rb], 0, 0, 0);
+                O[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qkh, vl_, O[rb], 0, 0, 0);
+                O[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qkl, vh_, O[rb], 0, 0, 0);
             }
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                ob[16 * rb + 4 * q4 + i][col0 + c16] = f2bf(O[rb][i]);
+                ob[16 * rb + 4 * q4 + i][col0 + c16] = O[rb][i];
         }
         lds_barrier();
         /* gated RMSNorm, 16 lanes per token row (as gdn_norm_gate_kernel) */
         for (int r0 = 0; r0 < L; r0 += SB_THREADS / 16) {
             const int t = r0 + (tid >> 4), sl = tid & 15;
             if (t < L) { /* whole 16-lane groups */
-                const bf16x8 ov = *(const bf16x8 *)&ob[t][8 * sl];
+                const float4 o0 = *(const float4 *)&ob[t][8 * sl];
+                const float4 o1 = *(const float4 *)&ob[t][8 * sl + 4];
+                const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
                 const size_t n = (size_t)t0 + t;
                 const bf16 *zr = z + n * zs + hv * DV + 8 * sl;
                 float ss = 0.f;
 #pragma unroll
                 for (int e = 0; e < 8; e++)
-                    ss += bf2f(ov[e]) * bf2f(ov[e]);
+                    ss += ov[e] * ov[e];
 #pragma unroll
                 for (int m = 1; m < 16; m <<= 1)
                     ss += __shfl_xor(ss, m, 64);
@@ -1115,7 +1305,7 @@ __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
                 bf16x8 res;
 #pragma unroll
                 for (int e = 0; e < 8; e++)
-                    res[e] = f2bf(bf2f(f2bf(bf2f(ov[e]) * inv)) * wl[e] * silu_f(bf2f(zr[e])));
+                    res[e] = f2bf(bf2f(f2bf(ov[e] * inv)) * wl[e] * silu_f(bf2f(zr[e])));
                 *(bf16x8 *)(y + (n * Hv + hv) * DV + 8 * sl) = res;
             }
         }
@@ -1123,10 +1313,11 @@ __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
     }
 }
 
-/* y = bf16( w * bf16(o * rsqrt(mean o^2 + eps)) * silu(z) ): 16 lanes per
- * (token, v-head) row, 8 columns a lane. REF src/kernels/gdn.cu:193-216. */
+/* y = bf16( w * bf16(o * rsqrt(mean o^2 + eps)) * silu(z) ) from the fp32
+ * output o: 16 lanes per (token, v-head) row, 8 columns a lane.
+ * REF src/kernels/gdn.cu:193-216. */
 template <bool VEC>
-__global__ __launch_bounds__(256) void gdn_norm_gate_kernel(const bf16 *__restrict__ o,
+__global__ __launch_bounds__(256) void gdn_norm_gate_kernel(const float *__restrict__ o,
                                                             const bf16 *__restrict__ z, int zs,
                                                             const float *__restrict__ w, float eps,
                                                             int rows, int Hv,
@@ -1136,7 +1327,9 @@ __global__ __launch_bounds__(256) void gdn_norm_gate_kernel(const bf16 *__restri
     if (row >= rows)
         return; /* whole 16-lane groups leave together */
     const int n = row / Hv, hv = row - n * Hv;
-    const bf16x8 ov = *(const bf16x8 *)(o + (size_t)row * DV + 8 * s);
+    const float4 o0 = *(const float4 *)(o + (size_t)row * DV + 8 * s);
+    const float4 o1 = *(const float4 *)(o + (size_t)row * DV + 8 * s + 4);
+    const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
     const bf16 *zr = z + (size_t)n * zs + hv * DV + 8 * s;
     bf16x8 zv;
     if constexpr (VEC) {
@@ -1153,7 +1346,7 @@ __global__ __launch_bounds__(256) void gdn_norm_gate_kernel(const bf16 *__restri
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; e++)
-        ss += bf2f(ov[e]) * bf2f(ov[e]);
+        ss += ov[e] * ov[e];
 #pragma unroll
     for (int m = 1; m < 16; m <<= 1)
         ss += __shfl_xor(ss, m, 64);
@@ -1161,7 +1354,7 @@ __global__ __launch_bounds__(256) void gdn_norm_gate_kernel(const bf16 *__restri
     bf16x8 r;
 #pragma unroll
     for (int e = 0; e < 8; e++)
-        r[e] = f2bf(bf2f(f2bf(bf2f(ov[e]) * inv)) * wl[e] * silu_f(bf2f(zv[e])));
+        r[e] = f2bf(bf2f(f2bf(ov[e] * inv)) * wl[e] * silu_f(bf2f(zv[e])));
     *(bf16x8 *)(y + (size_t)row * DV + 8 * s) = r;
 }
 
@@ -1172,8 +1365,8 @@ using namespace CUJEV_KNS;
 extern "C" hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const float *conv_w,
                                       const float *conv_in, float *conv_out, int seg0_len,
                                       const int32_t *own_base, const float *A_neg_exp,
-                                      const float *dt_bias, int N, int Hk, int Hv, bf16_t *q,
-                                      bf16_t *k, bf16_t *v, float *g, float *beta,
+                                      const float *dt_bias, int N, int Hk, int Hv, float *q,
+                                      float *k, float *v, float *g, float *beta,
                                       hipStream_t stream) {
     if (N <= 0)
         return hipSuccess;
@@ -1186,7 +1379,7 @@ extern "C" hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const
                     : (conv_in ? gdn_conv_prep_kernel<false, true> : gdn_conv_prep_kernel<false, false>);
     hipLaunchKernelGGL(kern, dim3((unsigned)CEIL_DIV(groups, 16)), dim3(256), 0, stream,
                        (const bf16 *)proj, proj_stride, conv_w, conv_in, own_base, A_neg_exp,
-                       dt_bias, N, Hk, Hv, (bf16 *)q, (bf16 *)k, (bf16 *)v, g, beta);
+                       dt_bias, N, Hk, Hv, q, k, v, g, beta);
     if (conv_out) {
         const int C = nheads * DK;
         hipLaunchKernelGGL(gdn_conv_tail_kernel, dim3((unsigned)CEIL_DIV(C, 256)), dim3(256), 0,
@@ -1211,7 +1404,7 @@ static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *
                                tail.conv_out, tail.seg0_len, tail.C);
         hipLaunchKernelGGL(gdn_short_b_kernel, dim3((unsigned)CEIL_DIV(units, spw), (unsigned)Hv),
                            dim3(SB_THREADS), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
-                           (const bf16x8 *)ws->QK, (const bf16x8 *)ws->U, ck->chunk_tok0,
+                           (const bf16x8 *)ws->QK, (const float4 *)ws->U, ck->chunk_tok0,
                            ck->chunk_len, packed ? nullptr : ck->seg_chunk0,
                            packed ? nullptr : ck->seg_nchunk, units, spw, S_in, Hv,
                            (const bf16 *)z, z_stride, norm_w, eps, (bf16 *)y);
@@ -1223,32 +1416,30 @@ static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *
     const int ntail = tail.conv_out ? CEIL_DIV(tail.C, 256) : 0;
     hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)(NCB * CEIL_DIV(units, 8) * 8 + ntail)),
                        dim3(256), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
-                       (const bf16x8 *)ws->QK, (const bf16x8 *)ws->KgT, (const bf16x8 *)ws->U,
+                       (const bf16x8 *)ws->QK, (const bf16x8 *)ws->KgT, (const float4 *)ws->U,
                        ws->Glast, ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk,
-                       S_in, S_out, Hv, units, (bf16 *)ws->O, tail);
+                       S_in, S_out, Hv, units, ws->O, tail);
     const int rows = N * Hv;
     const bool zvec = z_stride % 8 == 0 && ((uintptr_t)z & 15) == 0;
     hipLaunchKernelGGL(zvec ? gdn_norm_gate_kernel<true> : gdn_norm_gate_kernel<false>,
-                       dim3((unsigned)CEIL_DIV(rows, 16)), dim3(256), 0, stream,
-                       (const bf16 *)ws->O, (const bf16 *)z, z_stride, norm_w, eps, rows, Hv,
-                       (bf16 *)y);
+                       dim3((unsigned)CEIL_DIV(rows, 16)), dim3(256), 0, stream, ws->O,
+                       (const bf16 *)z, z_stride, norm_w, eps, rows, Hv, (bf16 *)y);
     return hipGetLastError();
 }
 
-extern "C" hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const float *g,
+extern "C" hipError_t k_gdn_scan(const float *q, const float *k, const float *v, const float *g,
                                  const float *beta, const cujev_chunks *ck, const float *S_in,
                                  float *S_out, const bf16_t *z, int z_stride, const float *norm_w,
                                  float eps, int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *ws,
                                  int N, hipStream_t stream) {
     if (ck->num_chunks <= 0 || N <= 0)
         return hipSuccess;
-    if (Hk <= 0 || Hv % Hk != 0 || (ck->chunk_starts && S_out))
+    if (Hk <= 0 || Hv % Hk != 0 || Hv / Hk > PA_MAX_REP || (ck->chunk_starts && S_out))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gdn_chunk_a_kernel<0>, dim3((unsigned)ck->num_chunks, (unsigned)Hv),
-                       dim3(256), 0, stream, (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, g,
-                       beta, ConvSrc{}, ck->chunk_tok0, ck->chunk_len, ck->chunk_starts, Hk, Hv,
-                       (bf16 *)ws->W, (bf16 *)ws->Qg, (bf16 *)ws->QK, (bf16 *)ws->KgT,
-                       (bf16 *)ws->U, ws->Glast);
+    hipLaunchKernelGGL(gdn_chunk_a_kernel<0>, dim3((unsigned)ck->num_chunks, (unsigned)Hk),
+                       dim3(PA_THREADS), 0, stream, q, k, v, g, beta, ConvSrc{}, ck->chunk_tok0,
+                       ck->chunk_len, ck->chunk_starts, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->Qg,
+                       (bf16 *)ws->QK, (bf16 *)ws->KgT, ws->U, ws->Glast);
     return gdn_phase_b(ck, S_in, S_out, z, z_stride, norm_w, eps, Hv, y, ws, N, TailJob{},
                        stream);
 }
@@ -1262,7 +1453,8 @@ extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const flo
                                   hipStream_t stream) {
     if (N <= 0)
         return hipSuccess;
-    if (Hk <= 0 || Hv % Hk != 0 || (ck->chunk_starts && S_out) || proj_stride % 8 != 0 ||
+    if (Hk <= 0 || Hv % Hk != 0 || Hv / Hk > PA_MAX_REP || (ck->chunk_starts && S_out) ||
+        proj_stride % 8 != 0 ||
         ((uintptr_t)proj & 15) != 0)
         return hipErrorInvalidValue;
     const int C = (2 * Hk + Hv) * DK;
@@ -1278,11 +1470,11 @@ extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const flo
     /* the conv tail rides along with phase B */
     const TailJob tail{(const bf16 *)proj, proj_stride, conv_in, conv_out, seg0_len, C};
     hipLaunchKernelGGL(conv_in ? gdn_chunk_a_kernel<2> : gdn_chunk_a_kernel<1>,
-                       dim3((unsigned)ck->num_chunks, (unsigned)Hv), dim3(256), 0, stream,
-                       (const bf16 *)nullptr, (const bf16 *)nullptr, (const bf16 *)nullptr,
+                       dim3((unsigned)ck->num_chunks, (unsigned)Hk), dim3(PA_THREADS), 0, stream,
+                       (const float *)nullptr, (const float *)nullptr, (const float *)nullptr,
                        (const float *)nullptr, (const float *)nullptr, cv, ck->chunk_tok0,
                        ck->chunk_len, ck->chunk_starts, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->Qg,
-                       (bf16 *)ws->QK, (bf16 *)ws->KgT, (bf16 *)ws->U, ws->Glast);
+                       (bf16 *)ws->QK, (bf16 *)ws->KgT, ws->U, ws->Glast);
     return gdn_phase_b(ck, S_in, S_out, proj + C, proj_stride, norm_w, eps, Hv, y, ws, N, tail,
                        stream);
 }

@@ -82,14 +82,14 @@ size_t cujev_attention_ws_max(int max_tokens, int Hq, int Hkv);
  * z Hv*128 | b Hv | a Hv]. Conv (width 4, no bias) + SiLU over the first
  * C = (2Hk+Hv)*128 columns; taps before a segment start (local index from
  * own_base) come from conv_in[C][3] (NULL = zeros). Then q,k l2-normalised
- * (q also * 128^-1/2) -> bf16 q,k [N][Hk][128], v bf16 [N][Hv][128],
+ * (q also * 128^-1/2) -> fp32 q,k [N][Hk][128], v fp32 [N][Hv][128],
  * g = A_neg_exp * softplus(a + dt_bias), beta = sigmoid(b) -> fp32 [N][Hv].
  * If conv_out != NULL the last three pre-conv inputs of the first segment
  * (tokens [0, seg0_len)) are written there as [C][3]. */
 hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const float *conv_w,
                            const float *conv_in, float *conv_out, int seg0_len,
                            const int32_t *own_base, const float *A_neg_exp, const float *dt_bias,
-                           int N, int Hk, int Hv, bf16_t *q, bf16_t *k, bf16_t *v, float *g,
+                           int N, int Hk, int Hv, float *q, float *k, float *v, float *g,
                            float *beta, hipStream_t stream);
 
 /* 64-token chunks of the packed segments; chunks never cross a segment. */
@@ -112,27 +112,30 @@ typedef struct cujev_chunks {
  * first phase in the MFMA operand-fragment order of the sequential second
  * phase, so each of its lanes reads 16 contiguous bytes per fragment and a
  * wave reads 1 KiB runs:
- *   W, q e^G   [64][128] as 16x16x32 A fragments (4 row blocks x 4 k-steps)
- *   QK^T masked [64][64] as 16x16x32 A fragments (4 x 2)
- *   (k e^{Glast-G})^T [128][64] as 32x32x16 A fragments (4 x 4)
- *   U          [64][128] as 16x16 accumulator fragments per 32-column block
- * all bf16, plus the chunk's total log-decay (one copy per lane). O is the unnormalised output
- * [N][Hv][128] bf16 before the gated norm. */
+ *   W, q e^G   [64][128] as 16x16x32 A fragments (4 row blocks x 4 k-steps), bf16
+ *   QK^T masked [64][64] as 16x16x32 A fragments (4 x 2), bf16 hi then lo
+ *   (k e^{Glast-G})^T [128][64] as 32x32x16 A fragments (4 x 4), bf16 hi then lo
+ *   U          [64][128] as 16x16 accumulator fragments per 32-column block, fp32
+ * plus the chunk's total log-decay (one copy per lane). O is the fp32 output
+ * [N][Hv][128] before the gated norm. */
 typedef struct cujev_gdn_scratch {
     void *W;      /* bf16 [chunks][Hv][1024][8] */
     void *Qg;     /* bf16 [chunks][Hv][1024][8] */
-    void *QK;     /* bf16 [chunks][Hv][512][8]  */
-    void *KgT;    /* bf16 [chunks][Hv][1024][8] */
-    void *U;      /* bf16 [chunks][Hv][1024][8] */
+    void *QK;     /* bf16 [chunks][Hv][2][512][8]  */
+    void *KgT;    /* bf16 [chunks][Hv][2][1024][8] */
+    float *U;     /* fp32 [chunks][Hv][1024][8] */
     float *Glast; /* [chunks][Hv][64] (64 equal copies) */
-    void *O;      /* bf16 [N][Hv][128] */
+    float *O;     /* fp32 [N][Hv][128] */
 } cujev_gdn_scratch;
 
 static inline size_t cujev_align256(size_t x) { return (x + 255) / 256 * 256; }
 static inline size_t cujev_gdn_scratch_bytes(int num_chunks, int Hv, int N) {
     const size_t ch = (size_t)num_chunks * Hv;
-    return 4 * cujev_align256(ch * 64 * 128 * 2) + cujev_align256(ch * 64 * 64 * 2) +
-           cujev_align256(ch * 64 * 4) + cujev_align256((size_t)N * Hv * 128 * 2);
+    return 2 * cujev_align256(ch * 64 * 128 * 2) /* W, Qg */ +
+           cujev_align256(ch * 64 * 64 * 2 * 2) /* QK hi + lo */ +
+           cujev_align256(ch * 64 * 128 * 2 * 2) /* KgT hi + lo */ +
+           cujev_align256(ch * 64 * 128 * 4) /* U */ + cujev_align256(ch * 64 * 4) +
+           cujev_align256((size_t)N * Hv * 128 * 4);
 }
 /* Carve the scratch of cujev_gdn_scratch_bytes() starting at `base`. */
 static inline cujev_gdn_scratch cujev_gdn_scratch_carve(void *base, int num_chunks, int Hv) {
@@ -143,15 +146,15 @@ static inline cujev_gdn_scratch cujev_gdn_scratch_carve(void *base, int num_chun
     p += cujev_align256(ch * 64 * 128 * 2);
     s.Qg = p;
     p += cujev_align256(ch * 64 * 128 * 2);
-    s.KgT = p;
-    p += cujev_align256(ch * 64 * 128 * 2);
-    s.U = p;
-    p += cujev_align256(ch * 64 * 128 * 2);
     s.QK = p;
-    p += cujev_align256(ch * 64 * 64 * 2);
+    p += cujev_align256(ch * 64 * 64 * 2 * 2);
+    s.KgT = p;
+    p += cujev_align256(ch * 64 * 128 * 2 * 2);
+    s.U = (float *)p;
+    p += cujev_align256(ch * 64 * 128 * 4);
     s.Glast = (float *)p;
     p += cujev_align256(ch * 64 * 4);
-    s.O = p;
+    s.O = (float *)p;
     return s;
 }
 
@@ -160,7 +163,7 @@ static inline cujev_gdn_scratch cujev_gdn_scratch_carve(void *base, int num_chun
  * receives the final state of segment 0. The output goes through the gated
  * RMSNorm: y[n, hv*128 + c] = bf16( bf16(o * rsqrt(mean o^2 + eps))
  *                                   * norm_w[c] * silu(z[n*z_stride + hv*128 + c]) ). */
-hipError_t k_gdn_scan(const bf16_t *q, const bf16_t *k, const bf16_t *v, const float *g,
+hipError_t k_gdn_scan(const float *q, const float *k, const float *v, const float *g,
                       const float *beta, const cujev_chunks *chunks, const float *S_in,
                       float *S_out, const bf16_t *z, int z_stride, const float *norm_w, float eps,
                       int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *scratch, int N,

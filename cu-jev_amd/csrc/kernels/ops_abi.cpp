@@ -244,7 +244,7 @@ EXPORT int cujev_op_gdn_conv_prep(const void *proj, int proj_stride, const float
         return fail(1, "gdn_conv_prep: bad arguments");
     return launched(k_gdn_conv_prep((const bf16_t *)proj, proj_stride, conv_w, conv_in, conv_out,
                                     seg0_len, own_base, A_neg_exp, dt_bias, N, Hk, Hv,
-                                    (bf16_t *)q, (bf16_t *)k, (bf16_t *)v, g, beta,
+                                    (float *)q, (float *)k, (float *)v, g, beta,
                                     (hipStream_t)stream),
                     "gdn_conv_prep");
 }
@@ -293,7 +293,7 @@ EXPORT int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const 
     cujev_chunks ck = {chunk_tok0, chunk_len,   seg_chunk0,     seg_nchunk,
                        num_chunks, num_segments, max_seg_chunks, chunk_starts};
     cujev_gdn_scratch ws = cujev_gdn_scratch_carve(scratch, num_chunks, Hv);
-    return launched(k_gdn_scan((const bf16_t *)q, (const bf16_t *)k, (const bf16_t *)v, g, beta,
+    return launched(k_gdn_scan((const float *)q, (const float *)k, (const float *)v, g, beta,
                                &ck, S_in, S_out, (const bf16_t *)z, z_stride, norm_w, eps, Hk, Hv,
                                (bf16_t *)y, &ws, N, (hipStream_t)stream),
                     "gdn_scan");

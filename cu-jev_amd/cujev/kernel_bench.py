@@ -87,9 +87,9 @@ def gdn_case(fused=True):
     dt_bias = torch.zeros(Hv, device=dev)
     norm_w = torch.ones(128, device=dev)
     own_base = torch.zeros(T, dtype=torch.int32, device=dev)
-    q = torch.empty(T, Hk, 128, dtype=torch.bfloat16, device=dev)
+    q = torch.empty(T, Hk, 128, dtype=torch.float32, device=dev)
     k = torch.empty_like(q)
-    v = torch.empty(T, Hv, 128, dtype=torch.bfloat16, device=dev)
+    v = torch.empty(T, Hv, 128, dtype=torch.float32, device=dev)
     gg = torch.empty(T, Hv, device=dev)
     beta = torch.empty_like(gg)
     conv_out = torch.empty(C, 3, device=dev)
@@ -132,9 +132,9 @@ def gdn_branch_case(B=64, L=16, fused=True):
     norm_w = torch.ones(128, device=dev)
     S_in = torch.randn(Hv, 128, 128, device=dev, generator=g) * 0.1
     own_base = (torch.arange(N, device=dev, dtype=torch.int32) // L) * L
-    q = torch.empty(N, Hk, 128, dtype=torch.bfloat16, device=dev)
+    q = torch.empty(N, Hk, 128, dtype=torch.float32, device=dev)
     k = torch.empty_like(q)
-    v = torch.empty(N, Hv, 128, dtype=torch.bfloat16, device=dev)
+    v = torch.empty(N, Hv, 128, dtype=torch.float32, device=dev)
     gg = torch.empty(N, Hv, device=dev)
     beta = torch.empty_like(gg)
     y = torch.empty(N, Hv * 128, dtype=torch.bfloat16, device=dev)

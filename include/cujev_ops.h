@@ -141,9 +141,9 @@ int cujev_op_attention_noalloc(const void *q, const void *gate, int gate_tok_str
 /* Replaces reference src/kernels/kernels.h:214-215 (k_gdn_conv) and :221-223
  * (k_gdn_prep), fused. proj rows [q Hk*128 | k Hk*128 | v Hv*128 | z | b | a].
  * Conv (width 4) + SiLU with taps before a segment taken from conv_in [C][3]
- * (NULL = zeros); own_base[n] = first token of n's segment. Outputs bf16
+ * (NULL = zeros); own_base[n] = first token of n's segment. Outputs fp32
  * q, k [N][Hk][128] (l2-normalised, q * 128^-1/2), v [N][Hv][128], fp32
- * g, beta [N][Hv]. conv_out (may be NULL) gets the last three pre-conv inputs
+ * g, beta [N][Hv] (the scan keeps q, k, v at about 16 significant bits). conv_out (may be NULL) gets the last three pre-conv inputs
  * of tokens [0, seg0_len) as [C][3]. conv_w fp32 [C][4]. */
 int cujev_op_gdn_conv_prep(const void *proj, int proj_stride, const float *conv_w,
                            const float *conv_in, float *conv_out, int seg0_len,
@@ -168,6 +168,7 @@ size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv, int N);
  * segments of at most 64 tokens into one chunk; bit t is set where token t of
  * the chunk starts a segment. Only with S_out == NULL: every segment continues
  * S_in, and seg_chunk0 / seg_nchunk / num_segments are not read.
+ * q, k, v are cujev_op_gdn_conv_prep's fp32 outputs. Hv / Hk <= 4.
  * scratch: cujev_ops_gdn_scratch_bytes(num_chunks, Hv, N) bytes, 256-aligned. */
 int cujev_op_gdn_scan(const void *q, const void *k, const void *v, const float *g,
                       const float *beta, const int32_t *chunk_tok0, const int32_t *chunk_len,

@@ -15,6 +15,10 @@ from oracle import qwen35 as orc  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
+# RMS relative error bar of the layer output and state at config 2: the
+# output's own bf16 rounding and the gated norm's bf16 round trip (which the
+# reference keeps) give about 2e-3; the scan adds little above them.
+RMS_TOL = 3e-3
 DK = DV = 128
 
 
@@ -28,6 +32,12 @@ def rel_err(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def rms_rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.sqrt(np.mean((a - b) ** 2) / np.mean(b ** 2)))
 
 
 def bf(x):
@@ -85,9 +95,9 @@ def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False, te
     pd = bf(proj).to(dev)
     own_base = np.repeat(np.cumsum([0] + list(seg_lens[:-1])), seg_lens).astype(np.int32)
     t = lambda a: torch.as_tensor(a).to(dev)
-    q = torch.empty(N, L.Hk, DK, dtype=torch.bfloat16, device=dev)
+    q = torch.empty(N, L.Hk, DK, dtype=torch.float32, device=dev)
     k = torch.empty_like(q)
-    v = torch.empty(N, L.Hv, DV, dtype=torch.bfloat16, device=dev)
+    v = torch.empty(N, L.Hv, DV, dtype=torch.float32, device=dev)
     g = torch.empty(N, L.Hv, dtype=torch.float32, device=dev)
     beta = torch.empty_like(g)
     cin = t(conv_in.astype(np.float32)) if conv_in is not None else None
@@ -254,8 +264,10 @@ def test_gdn_capacity_shape():
     got_p = run_gpu(o, L, prefix, [T], write_state=True, fused=True)
     y, S, tail = oracle_segment(L, prefix, None, None)
     ey, es = rel_err(got_p["y"], y), rel_err(got_p["S"], S)
-    print(f"prefill 2048: y {ey:.3e} S {es:.3e}", flush=True)
+    ry, rs = rms_rel(got_p["y"], y), rms_rel(got_p["S"], S)
+    print(f"prefill 2048: y {ey:.3e} (RMS {ry:.3e})  S {es:.3e} (RMS {rs:.3e})", flush=True)
     assert ey <= TOL and es <= TOL
+    assert ry <= RMS_TOL and rs <= RMS_TOL
     np.testing.assert_array_equal(got_p["tail"], tail.astype(np.float32))
     seg_lens = [16] * 64
     br = L.proj(1024)
