@@ -201,25 +201,23 @@ __global__ void gdn_conv_tail_kernel(const bf16 *__restrict__ proj, int ps,
 /* ---------------------------------------------------------------------- */
 /* phase A: intra-chunk WY/UT factors, written in phase B's operand layouts */
 /* ---------------------------------------------------------------------- */
-
-/* ---------------------------------------------------------------------- */
-/* phase A: intra-chunk WY/UT factors, written in phase B's operand layouts */
-/* ---------------------------------------------------------------------- */
-/* One workgroup (8 waves) per (chunk, k-head) serves every v-head that reads
- * this k-head (Hv / Hk of them, one after the other):
+/* One workgroup (8 waves) per (chunk, k-head, pair of the k-head's v-heads):
  *   1. q and k rows of the k-head (conv + SiLU + l2 norm and q * 128^-1/2,
  *      or read from gdn_conv_prep's fp32 output) staged in LDS as bf16
- *      pairs hi + lo (hi = bf16(x), lo = bf16(x - hi): x to ~16 bits);
+ *      pairs hi + lo (hi = bf16(x), lo = bf16(x - hi): x to ~16 bits); the
+ *      gates of both v-heads: G = cumsum g (restarted at segment starts),
+ *      beta e^G, beta, e^{G_last - G};
  *   2. raw K K^T (hi parts) and Q K^T (hi.hi + hi.lo + lo.hi MFMAs) in fp32,
- *      computed once for all the v-heads;
- *   then per v-head:
- *   3. gates: G = cumsum g (restarted at segment starts), beta e^G, beta,
- *      e^{G_last - G}; the v-head's v rows (hi + lo);
- *   4. q e^G (bf16) and the masked QK^T (hi + lo) leave; A = tril(beta_i
- *      e^{G_i-G_j} k_i.k_j, -1) (fp32);
- *   5. T = (I + A)^-1 in place (fp32, blocked forward substitution); beside
- *      it (K e^{G_last-G})^T from the exact k rows leaves as hi + lo;
- *   6. W = T (beta e^G K) (bf16) and U = T (beta V) with V exact (hi and lo
+ *      shared by both v-heads; q e^G (bf16) of both v-heads leaves;
+ *   then waves 0-3 serve the first v-head and waves 4-7 the second, side by
+ *   side:
+ *   3. the masked QK^T (hi + lo) leaves; A = tril(beta_i e^{G_i-G_j}
+ *      k_i.k_j, -1) (fp32); (K e^{G_last-G})^T from the exact k rows leaves
+ *      as hi + lo;
+ *   4. the v rows of both v-heads (hi + lo) where the q rows and the raw
+ *      products were; T = (I + A)^-1 in place (fp32, blocked forward
+ *      substitution);
+ *   5. W = T (beta e^G K) (bf16) and U = T (beta V) with V exact (hi and lo
  *      MFMAs; U kept fp32), staged row-major, then stored in the fragment
  *      order phase B reads.
  * Which operands carry lo parts follows from where a bf16 rounding moves
@@ -234,23 +232,23 @@ __global__ void gdn_conv_tail_kernel(const bf16 *__restrict__ proj, int ps,
  * branches that all continue one state and write no final state: phase B
  * then needs nothing per segment. */
 constexpr int PA_THREADS = 512;
-constexpr int PA_MAX_REP = 4; /* v-heads per k-head (one gate wave each) */
-constexpr int PA_CONV_STAGE = 8 * 16 * 4 + 3 * 128; /* floats of one slice's weights + tail */
+constexpr int PA_STAGE1 = 8 * 16 * 4 + 3 * 128; /* floats of one slice's conv weights + tail */
 
 struct __attribute__((aligned(16))) PairA_Smem {
-    bf16 Kh[CH][DK + 8], Kl[CH][DK + 8]; /* k rows, hi and lo parts                 */
-    bf16 Xh[CH][DK + 8], Xl[CH][DK + 8]; /* q rows, then the v-head's v rows; then
-                                            U staging (fp32 [CH][DV + 4])          */
-    float KK[CH][CH + 4];                /* conv staging of q, k; then raw k_i.k_j  */
-    float QK[CH][CH + 4];                /* raw q_i.k_j                              */
-    float AT[CH][CH + 4];                /* A, then T in place; then W staging      */
-    float cs[PA_CONV_STAGE];             /* conv staging of the v slice             */
-    /* per v-head of the k-head: G, beta e^G, e^{G_last - G}, beta */
-    float G[PA_MAX_REP][CH], sK[PA_MAX_REP][CH], sKg[PA_MAX_REP][CH], sV[PA_MAX_REP][CH];
+    bf16 Kh[CH][DK + 8], Kl[CH][DK + 8]; /* k rows, hi and lo parts                   */
+    /* X: q rows (hi, lo); then the first v-head's v rows; then its U staging
+     * (fp32 [CH][DV + 4]). Y: raw k_i.k_j and q_i.k_j (fp32 [CH][CH + 4]
+     * each); then the second v-head's v rows; then its U staging. */
+    bf16 Xh[CH][DK + 8], Xl[CH][DK + 8];
+    bf16 Yh[CH][DK + 8], Yl[CH][DK + 8];
+    float AT[2][CH][CH + 4];             /* A, then T in place; then W staging    */
+    float cs[2 * PA_STAGE1];             /* conv weights and tails of two slices  */
+    float G[2][CH], sK[2][CH], sKg[2][CH], sV[2][CH]; /* per v-head of the pair */
     int Sid[CH]; /* segment of each token inside a packed chunk (1-based) */
 };
 static_assert(sizeof(PairA_Smem) <= 160 * 1024, "phase A fits one CU's LDS");
 static_assert(2 * sizeof(bf16) * CH * (DK + 8) >= sizeof(float) * CH * (DV + 4), "U staging");
+static_assert(sizeof(bf16) * CH * (DK + 8) >= sizeof(float) * CH * (CH + 4), "raw products");
 static_assert(sizeof(float) * CH * (CH + 4) >= sizeof(bf16) * CH * (DK + 8), "W staging");
 
 DEV bf16x8 ld8(const bf16 *p) { return *(const bf16x8 *)p; }
@@ -472,18 +470,21 @@ DEV void rows_f32(const float *src, size_t rs, int L, int tid, int nthr, bf16 (*
 
 /* SRC 0: q, k, v, g, beta read from gdn_conv_prep's outputs (fp32); 1: computed
  * here from the pre-conv projection rows (zeros before a segment); 2: the
- * same with the state's conv tail before each segment. */
+ * same with the state's conv tail before each segment. Grid: (chunk,
+ * k-head x pairs of its v-heads); npairs = ceil(Hv / Hk / 2). */
 template <int SRC>
 __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
     const float *__restrict__ qh, const float *__restrict__ kh_, const float *__restrict__ vh,
     const float *__restrict__ g, const float *__restrict__ beta, ConvSrc cv,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
-    const uint64_t *__restrict__ chunk_starts, int Hk, int Hv,
+    const uint64_t *__restrict__ chunk_starts, int Hk, int Hv, int npairs,
     bf16 *__restrict__ Wo, bf16 *__restrict__ Qgo, bf16 *__restrict__ QKo,
     bf16 *__restrict__ KgTo, float *__restrict__ Uo, float *__restrict__ Glo) {
     __shared__ PairA_Smem sm;
-    const int ch = blockIdx.x, hk = blockIdx.y;
+    const int ch = blockIdx.x, hk = blockIdx.y / npairs, pr = blockIdx.y - hk * npairs;
     const int rep = Hv / Hk;
+    const int hv0 = hk * rep + 2 * pr;   /* the pair's first v-head */
+    const int nh = min(2, rep - 2 * pr); /* 1 or 2 v-heads */
     const int t0 = chunk_tok0[ch], L = chunk_len[ch];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -491,11 +492,20 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
     const int grp = tid >> 4, s16 = tid & 15; /* 32 groups of 16 lanes */
     const int nblk = (L + 3) >> 2;            /* 4-token blocks holding tokens */
     const int C = (2 * Hk + Hv) * DK;
+    /* the v-head of this wave's group (waves 0-3: first, 4-7: second) */
+    const int hg = wave >> 2, w4 = wave & 3;
+    const bool hact = hg < nh;
+    const size_t cbg = (size_t)ch * Hv + hv0 + hg;
     /* segments packed into the chunk: bit t set where token t starts one */
     const uint64_t starts = chunk_starts ? chunk_starts[ch] | 1ull : 1ull;
     const uint64_t upto = lane == 63 ? ~0ull : (2ull << lane) - 1;
+    bf16(*Vh)[DK + 8] = hg ? sm.Yh : sm.Xh; /* this group's v rows (step 4 on) */
+    bf16(*Vl)[DK + 8] = hg ? sm.Yl : sm.Xl;
+    float(*KK)[CH + 4] = reinterpret_cast<float(*)[CH + 4]>(&sm.Yh[0][0]);
+    float(*QK)[CH + 4] = reinterpret_cast<float(*)[CH + 4]>(&sm.Yl[0][0]);
+    float(*AT)[CH + 4] = sm.AT[hg];
 
-    /* ---- 1. q and k rows (hi + lo) ---- */
+    /* ---- 1. q and k rows (hi + lo); gates of the pair (waves 4, 5) ---- */
     if constexpr (SRC == 0) {
         rows_f32(qh + ((size_t)t0 * Hk + hk) * DK, (size_t)Hk * DK, L, tid, PA_THREADS, sm.Xh,
                  sm.Xl);
@@ -515,9 +525,8 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
             for (int j = 0; j < 4; j++)
                 base[j] = cv.own_base[min(n0 + j, cv.N - 1)];
         }
-        float *cw = &sm.KK[0][0], *ct = cw + 2 * 8 * 16 * 4;
         const int c0s[2] = {hk * DK, (Hk + hk) * DK};
-        conv_stage<TAIL>(cv, c0s, 2, tid, PA_THREADS, cw, ct);
+        conv_stage<TAIL>(cv, c0s, 2, tid, PA_THREADS, sm.cs, sm.cs + 2 * 8 * 16 * 4);
         const int zrows = CH - 4 * nblk; /* rows of blocks without tokens: zeros */
         for (int i = tid; i < 4 * zrows * 16; i += PA_THREADS) {
             const int a = i / (zrows * 16), rem = i - a * zrows * 16;
@@ -527,16 +536,15 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
         lds_barrier();
         if (grp < ntask) {
             const int sl = grp / nblk, tb = grp - sl * nblk;
-            conv_slice<TAIL>(xr, base, cw, ct, sl, true,
+            conv_slice<TAIL>(xr, base, sm.cs, sm.cs + 2 * 8 * 16 * 4, sl, true,
                              sl == 0 ? 0.08838834764831845f /* 128^-1/2 */ : 1.f, t0, L, tb, s16,
                              sl == 0 ? sm.Xh : sm.Kh, sl == 0 ? sm.Xl : sm.Kl);
         }
     }
     if (wave == 7)
         sm.Sid[lane] = __builtin_popcountll(starts & upto);
-    /* gates of the k-head's v-heads, wave 4 + r for v-head r */
-    if (wave >= 4 && wave - 4 < rep) {
-        const int r = wave - 4, hv = hk * rep + r;
+    if (wave >= 4 && wave - 4 < nh) {
+        const int r = wave - 4, hv = hv0 + r;
         float gv = 0.f, bv = 0.f;
         if (lane < L) {
             if constexpr (SRC == 0) {
@@ -568,16 +576,30 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
     lds_barrier();
 
     /* ---- 2. raw Q K^T (split) on waves 0-2, K K^T on waves 3, 6, 7: the
-     * lower 32x32 tiles (0,0), (1,0), (1,1) | q e^G of every v-head (waves
+     * lower 32x32 tiles (0,0), (1,0), (1,1) | q e^G of both v-heads (waves
      * 4-7, 16x16x32 A-fragment order: entry i holds row 16(i/256) + i%16,
-     * columns 32((i/64)%4) + 8((i/16)%4) .. +7) ---- */
-    const int u = tid - 256; /* waves 4-7: 0..255 */
+     * columns 32((i/64)%4) + 8((i/16)%4) .. +7) | every group: the pre-conv
+     * rows of its v-conv task (slice = v-head grp/16, block grp%16) ---- */
+    constexpr bool CONV = SRC != 0;
+    bf16x8 vr[7];
+    int vbase[4];
+    const int vsl = grp >> 4, vtb = grp & 15;
+    const bool vtask = CONV && vsl < nh && vtb < nblk;
+    if constexpr (CONV) {
+        if (vtask) {
+            const int n0 = t0 + 4 * vtb;
+            conv_rows(cv, (2 * Hk + hv0 + vsl) * DK + 8 * s16, n0, vr);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                vbase[j] = cv.own_base[min(n0 + j, cv.N - 1)];
+        }
+    }
     {
         const bool isqk = wave < 3;
         const int job = wave < 3 ? wave : wave == 3 ? 0 : wave >= 6 ? wave - 5 : -1;
+        floatx16 acc = {};
+        const int ti = job == 0 ? 0 : 1, tj = job == 2 ? 1 : 0;
         if (job >= 0) {
-            const int ti = job == 0 ? 0 : 1, tj = job == 2 ? 1 : 0;
-            floatx16 acc = {};
 #pragma unroll
             for (int ks = 0; ks < DK / 16; ks++) {
                 const int c = 16 * ks + 8 * h;
@@ -594,15 +616,11 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
                                                                   bkh, acc, 0, 0, 0);
                 }
             }
-            float(*dst)[CH + 4] = isqk ? sm.QK : sm.KK;
-#pragma unroll
-            for (int r = 0; r < 16; r++)
-                dst[32 * ti + 8 * (r >> 2) + 4 * h + (r & 3)][32 * tj + col] = acc[r];
         }
         if (wave >= 4) {
-            const int t = u & 15, c8 = 32 * ((u >> 6) & 3) + 8 * ((u >> 4) & 3);
-            for (int r = 0; r < rep; r++) {
-                const size_t cb = (size_t)ch * Hv + hk * rep + r;
+            const int u = tid - 256, t = u & 15, c8 = 32 * ((u >> 6) & 3) + 8 * ((u >> 4) & 3);
+            for (int r = 0; r < nh; r++) {
+                const size_t cb = (size_t)ch * Hv + hv0 + r;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const bf16x8 a = ld8(&sm.Xh[16 * j + t][c8]), b = ld8(&sm.Xl[16 * j + t][c8]);
@@ -615,8 +633,15 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
                 }
             }
         }
+        /* the raw products go where the second v-head's v rows will be */
+        if (job >= 0) {
+            float(*dst)[CH + 4] = isqk ? QK : KK;
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                dst[32 * ti + 8 * (r >> 2) + 4 * h + (r & 3)][32 * tj + col] = acc[r];
+        }
     }
-    lds_barrier(); /* raw products in LDS; the q rows may be overwritten */
+    lds_barrier();
 
     bf16x8 eye[2]; /* B operand of the identity, k = 16s + 8h + e */
 #pragma unroll
@@ -626,299 +651,274 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
             eye[s][e] = f2bf(16 * s + 8 * h + e == col ? 1.f : 0.f);
     /* token of accumulator slot r of 32-row tile tb */
     auto tok = [&](int tb, int r) { return 32 * tb + 8 * (r >> 2) + 4 * h + (r & 3); };
+    const float *Gg = sm.G[hg], *sKg_g = sm.sKg[hg];
 
-    for (int r = 0; r < rep; r++) {
-        const int hv = hk * rep + r;
-        const size_t cb = (size_t)ch * Hv + hv;
-        const float *Gr = sm.G[r], *sKr = sm.sK[r], *sKgr = sm.sKg[r], *sVr = sm.sV[r];
-        /* per-iteration copies of the lane indices (see opaque()) */
-        const int tid = opaque(threadIdx.x), lane = tid & 63;
-        const int h = lane >> 5, col = lane & 31, grp = tid >> 4, s16 = tid & 15;
-        const int u = tid - 256;
-        auto tok = [&](int tb, int r_) { return 32 * tb + 8 * (r_ >> 2) + 4 * h + (r_ & 3); };
-
-        /* ---- 3. the v-head's v rows (waves 0-3) ---- */
-        constexpr bool CONV = SRC != 0;
-        bf16x8 xr[7];
-        int base[4];
-        if (wave < 4) {
-            if constexpr (SRC == 0) {
-                rows_f32(vh + ((size_t)t0 * Hv + hv) * DV, (size_t)Hv * DV, L, tid, 256, sm.Xh,
-                         sm.Xl);
-            } else {
-                constexpr bool TAIL = SRC == 2;
-                if (grp < nblk) {
-                    const int n0 = t0 + 4 * grp;
-                    conv_rows(cv, (2 * Hk + hv) * DK + 8 * s16, n0, xr);
+    /* ---- 3. per group (its v-head): masked QK^T hi + lo, A, and
+     * (K e^{G_last-G})^T hi + lo for dk block 32 w4; the v-conv weights ---- */
+    if (hact) {
+        const int u = tid & 255;
+        /* masked QK^T = tril(q_i.k_j e^{G_i-G_j}) within a segment, as hi
+         * and lo 16x16x32 A fragments: entry i holds row 16(i/128) + i%16,
+         * columns 32((i/64)%2) + 8((i/16)%4) .. +7 */
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        base[j] = cv.own_base[min(n0 + j, cv.N - 1)];
-                }
-                const int c0s[1] = {(2 * Hk + hv) * DK};
-                conv_stage<TAIL>(cv, c0s, 1, tid, 256, sm.cs, sm.cs + 8 * 16 * 4);
-                const int zrows = CH - 4 * nblk;
-                for (int i = tid; i < 2 * zrows * 16; i += 256) {
-                    const int a = i / (zrows * 16), rem = i - a * zrows * 16;
-                    bf16(*z)[DK + 8] = a == 0 ? sm.Xh : sm.Xl;
-                    *(bf16x8 *)&z[4 * nblk + (rem >> 4)][8 * (rem & 15)] = bf16x8{};
-                }
+        for (int j = 0; j < 2; j++) {
+            const int i = u + 256 * j;
+            const int rr = 16 * (i >> 7) + (i & 15), c8 = 32 * ((i >> 6) & 1) + 8 * ((i >> 4) & 3);
+            const float Gi = Gg[rr];
+            const int Si = sm.Sid[rr];
+            const float4 q0 = rd4(&QK[rr][c8]), q1 = rd4(&QK[rr][c8 + 4]);
+            const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            bf16x8 oh, ol;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int cj = c8 + e;
+                const bool keep = rr >= cj && Si == sm.Sid[cj];
+                const bfpair sp = split2(keep ? qv[e] * fast_exp(fminf(Gi - Gg[cj], 0.f)) : 0.f);
+                oh[e] = sp.hi;
+                ol[e] = sp.lo;
             }
+            *(bf16x8 *)(QKo + (cbg * 1024 + i) * 8) = oh;
+            *(bf16x8 *)(QKo + (cbg * 1024 + 512 + i) * 8) = ol;
         }
-        lds_barrier();
-
-        /* ---- 4. v rows (waves 0-3, conv form) | masked QK^T and A
-         * (waves 4-7) ---- */
-        if (wave < 4) {
-            if constexpr (CONV) {
-                if (grp < nblk)
-                    conv_slice<SRC == 2>(xr, base, sm.cs, sm.cs + 8 * 16 * 4, 0, false, 1.f, t0, L,
-                                         grp, s16, sm.Xh, sm.Xl);
-            }
-        } else {
-            /* masked QK^T = tril(q_i.k_j e^{G_i-G_j}) within a segment, as hi
-             * and lo 16x16x32 A fragments: entry i holds row 16(i/128) + i%16,
-             * columns 32((i/64)%2) + 8((i/16)%4) .. +7 */
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int i = u + 256 * j;
-                const int rr = 16 * (i >> 7) + (i & 15), c8 = 32 * ((i >> 6) & 1) + 8 * ((i >> 4) & 3);
-                const float Gi = Gr[rr];
-                const int Si = sm.Sid[rr];
-                const float4 q0 = rd4(&sm.QK[rr][c8]), q1 = rd4(&sm.QK[rr][c8 + 4]);
-                const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-                bf16x8 oh, ol;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int cj = c8 + e;
-                    const bool keep = rr >= cj && Si == sm.Sid[cj];
-                    const float v = keep ? qv[e] * fast_exp(fminf(Gi - Gr[cj], 0.f)) : 0.f;
-                    { const bfpair sp_ = split2(v); oh[e] = sp_.hi; ol[e] = sp_.lo; }
-                }
-                *(bf16x8 *)(QKo + (cb * 1024 + i) * 8) = oh;
-                *(bf16x8 *)(QKo + (cb * 1024 + 512 + i) * 8) = ol;
-            }
-            /* A = tril(beta_i e^{G_i-G_j} k_i.k_j, -1) within a segment, zero
-             * elsewhere (the inverse reads the upper part of its blocks):
-             * row u/4, columns 16(u%4) .. +15 */
-            {
-                const int ri = u >> 2, c16b = 16 * (u & 3);
-                const float Gi = Gr[ri], bi = sVr[ri];
-                const int Si = sm.Sid[ri];
-#pragma unroll
-                for (int c4 = 0; c4 < 16; c4 += 4) {
-                    const float4 kk = rd4(&sm.KK[ri][c16b + c4]);
-                    const float kv[4] = {kk.x, kk.y, kk.z, kk.w};
-                    float a[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int cj = c16b + c4 + e;
-                        const bool keep = ri > cj && Si == sm.Sid[cj];
-                        a[e] = keep ? bi * kv[e] * fast_exp(fminf(Gi - Gr[cj], 0.f)) : 0.f;
-                    }
-                    wr4(&sm.AT[ri][c16b + c4], make_float4(a[0], a[1], a[2], a[3]));
-                }
-            }
-        }
-        lds_barrier();
-
-        /* ---- 5. T = (I + A)^-1 in place (waves 0-3) | (K e^{G_last-G})^T
-         * as hi + lo (waves 4-7, dk block 32(w-4)) ----
-         * 5a: wave w < 4 inverts diagonal block w, lane c < 16 owning column
-         * c; the block is read (all lanes, broadcast) before any lane writes. */
-        if (wave < 4) {
-            if (lane < 16) {
-                const int b0 = 16 * wave, c = lane;
-                float t[16];
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    float acc = 0.f;
-#pragma unroll
-                    for (int k4 = 0; k4 < i; k4 += 4) {
-                        const float4 a = rd4(&sm.AT[b0 + i][b0 + k4]);
-                        acc = fmaf(a.x, t[k4], acc);
-                        if (k4 + 1 < i)
-                            acc = fmaf(a.y, t[k4 + 1], acc);
-                        if (k4 + 2 < i)
-                            acc = fmaf(a.z, t[k4 + 2], acc);
-                        if (k4 + 3 < i)
-                            acc = fmaf(a.w, t[k4 + 3], acc);
-                    }
-                    t[i] = (i == c ? 1.f : 0.f) - acc;
-                }
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    if (i >= c)
-                        sm.AT[b0 + i][b0 + c] = t[i];
-            }
-        } else {
-            const int w4 = wave - 4;
-            floatx16 dK[2];
-#pragma unroll
-            for (int tb = 0; tb < 2; tb++) {
-                dK[tb] = floatx16{};
-#pragma unroll
-                for (int s = 0; s < 2; s++) { /* identity products: exact */
-                    const int c = 32 * w4 + 16 * s + 8 * h;
-                    dK[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld8(&sm.Kh[32 * tb + col][c]),
-                                                                     eye[s], dK[tb], 0, 0, 0);
-                    dK[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld8(&sm.Kl[32 * tb + col][c]),
-                                                                     eye[s], dK[tb], 0, 0, 0);
-                }
-            }
-            /* 32x32x16 A fragments (row dk = 32 w4 + l%32, tokens 16s +
-             * 8(l/32)..+7): the lane pair (l, l^32) trades halves */
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                const int tb = s >> 1, r0 = 8 * (s & 1);
-                bf16 vh_[8], vl_[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    { const bfpair sp_ = split2(dK[tb][r0 + e] * sKgr[tok(tb, r0 + e)]); vh_[e] = sp_.hi; vl_[e] = sp_.lo; }
-#pragma unroll
-                for (int part = 0; part < 2; part++) {
-                    const bf16 *v = part ? vl_ : vh_;
-                    uint32_t p0[2], p1[2];
-#pragma unroll
-                    for (int e = 0; e < 2; e++) {
-                        p0[e] = __builtin_bit_cast(uint32_t, bf16x2{v[2 * e], v[2 * e + 1]});
-                        p1[e] = __builtin_bit_cast(uint32_t, bf16x2{v[4 + 2 * e], v[5 + 2 * e]});
-                    }
-                    uint32_t o[4];
-#pragma unroll
-                    for (int e = 0; e < 2; e++) { /* h=0 holds tokens +0..3 | +8..11 */
-                        const uint32_t x1 = (uint32_t)__shfl_xor((int)p1[e], 32, 64);
-                        const uint32_t x0 = (uint32_t)__shfl_xor((int)p0[e], 32, 64);
-                        o[e] = h ? x1 : p0[e];
-                        o[2 + e] = h ? p1[e] : x0;
-                    }
-                    *(u32x4 *)(KgTo + (cb * 2048 + part * 1024 + (w4 * 4 + s) * 64 + lane) * 8) =
-                        u32x4{o[0], o[1], o[2], o[3]};
-                }
-            }
-        }
-        lds_barrier();
-        /* 5b: inside 32x32 diagonal block p (wave p): T_10 = -T_11 (A_10 T_00),
-         * 16x16 blocks; lane = (row l/4, columns 4(l%4)..+3) */
-        if (wave < 2) {
-            const int p0 = 32 * wave, rr = lane >> 2, c0 = 4 * (lane & 3);
-            float *a10 = &sm.AT[p0 + 16 + rr][p0];
-            const float4 x = row_times<16>(a10, &sm.AT[p0][p0 + c0]);
-            wr4(a10 + c0, x);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            const float4 y = row_times<16>(&sm.AT[p0 + 16 + rr][p0 + 16], &sm.AT[p0 + 16][p0 + c0]);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            wr4(a10 + c0, make_float4(-y.x, -y.y, -y.z, -y.w));
-        }
-        lds_barrier();
-        /* 5c: T_10 = -T_11 (A_10 T_00) with 32x32 blocks; lane = (row 8w +
-         * l/8, columns 4(l%8)..+3). A chunk of at most 32 tokens has A_10 = 0
-         * and so T_10 = 0, which the array already holds. Every wave passes
-         * the same barriers; waves 4-7 have no rows. */
-        if (L > 32) {
-            const int rr = 32 + 8 * wave + (lane >> 3), c0 = 4 * (lane & 7);
-            float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (wave < 4)
-                x = row_times<32>(&sm.AT[rr][0], &sm.AT[0][c0]);
-            lds_barrier();
-            if (wave < 4)
-                wr4(&sm.AT[rr][c0], x);
-            lds_barrier();
-            float4 y = x;
-            if (wave < 4)
-                y = row_times<32>(&sm.AT[rr][32], &sm.AT[32][c0]);
-            lds_barrier();
-            if (wave < 4)
-                wr4(&sm.AT[rr][c0], make_float4(-y.x, -y.y, -y.z, -y.w));
-            lds_barrier();
-        }
-
-        /* ---- 6. W = T (beta e^G K) on waves 0-3 (dk block 32w, K hi) and
-         * U = T (beta V) on waves 4-7 (dv block 32(w-4), V hi + lo) ---- */
+        /* A = tril(beta_i e^{G_i-G_j} k_i.k_j, -1) within a segment, zero
+         * elsewhere (the inverse reads the upper part of its blocks): row
+         * u/4, columns 16(u%4) .. +15 */
         {
-            const int w4 = wave & 3;
-            const bool isw = wave < 4;
-            floatx16 dX[2]; /* rows 32tb.. of K (or V), columns 32 w4.. */
+            const int ri = u >> 2, c16b = 16 * (u & 3);
+            const float Gi = Gg[ri], bi = sm.sV[hg][ri];
+            const int Si = sm.Sid[ri];
+#pragma unroll
+            for (int c4 = 0; c4 < 16; c4 += 4) {
+                const float4 kk = rd4(&KK[ri][c16b + c4]);
+                const float kv[4] = {kk.x, kk.y, kk.z, kk.w};
+                float a[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int cj = c16b + c4 + e;
+                    const bool keep = ri > cj && Si == sm.Sid[cj];
+                    a[e] = keep ? bi * kv[e] * fast_exp(fminf(Gi - Gg[cj], 0.f)) : 0.f;
+                }
+                wr4(&AT[ri][c16b + c4], make_float4(a[0], a[1], a[2], a[3]));
+            }
+        }
+        /* (K e^{G_last-G})^T as 32x32x16 A fragments (row dk = 32 w4 + l%32,
+         * tokens 16s + 8(l/32)..+7) from the exact k rows (identity
+         * products of hi and lo); the lane pair (l, l^32) trades halves */
+        floatx16 dK[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; tb++) {
+            dK[tb] = floatx16{};
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const int c = 32 * w4 + 16 * s + 8 * h;
+                dK[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld8(&sm.Kh[32 * tb + col][c]),
+                                                                 eye[s], dK[tb], 0, 0, 0);
+                dK[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld8(&sm.Kl[32 * tb + col][c]),
+                                                                 eye[s], dK[tb], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int tb = s >> 1, r0 = 8 * (s & 1);
+            bf16 vh_[8], vl_[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const bfpair sp = split2(dK[tb][r0 + e] * sKg_g[tok(tb, r0 + e)]);
+                vh_[e] = sp.hi;
+                vl_[e] = sp.lo;
+            }
+#pragma unroll
+            for (int part = 0; part < 2; part++) {
+                const bf16 *v = part ? vl_ : vh_;
+                uint32_t p0[2], p1[2];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    p0[e] = __builtin_bit_cast(uint32_t, bf16x2{v[2 * e], v[2 * e + 1]});
+                    p1[e] = __builtin_bit_cast(uint32_t, bf16x2{v[4 + 2 * e], v[5 + 2 * e]});
+                }
+                uint32_t o[4];
+#pragma unroll
+                for (int e = 0; e < 2; e++) { /* h=0 holds tokens +0..3 | +8..11 */
+                    const uint32_t x1 = (uint32_t)__shfl_xor((int)p1[e], 32, 64);
+                    const uint32_t x0 = (uint32_t)__shfl_xor((int)p0[e], 32, 64);
+                    o[e] = h ? x1 : p0[e];
+                    o[2 + e] = h ? p1[e] : x0;
+                }
+                *(u32x4 *)(KgTo + (cbg * 2048 + part * 1024 + (w4 * 4 + s) * 64 + lane) * 8) =
+                    u32x4{o[0], o[1], o[2], o[3]};
+            }
+        }
+    }
+    if constexpr (CONV) {
+        int c0s[2] = {(2 * Hk + hv0) * DK, (2 * Hk + hv0 + 1) * DK};
+        conv_stage<SRC == 2>(cv, c0s, nh, tid, PA_THREADS, sm.cs, sm.cs + 2 * 8 * 16 * 4);
+    }
+    lds_barrier(); /* the q rows and the raw products are no longer read */
+
+    /* ---- 4. the v rows of both v-heads (hi + lo) | T = (I + A)^-1 ----
+     * 4a: wave w4 of each group inverts diagonal block w4 of its A, lane
+     * c < 16 owning column c; the block is read (all lanes, broadcast)
+     * before any lane writes it. */
+    if constexpr (SRC == 0) {
+        for (int r = 0; r < nh; r++)
+            rows_f32(vh + ((size_t)t0 * Hv + hv0 + r) * DV, (size_t)Hv * DV, L, tid, PA_THREADS,
+                     r ? sm.Yh : sm.Xh, r ? sm.Yl : sm.Xl);
+    } else {
+        const int zrows = CH - 4 * nblk;
+        for (int i = tid; i < 2 * nh * zrows * 16; i += PA_THREADS) {
+            const int a = i / (zrows * 16), rem = i - a * zrows * 16;
+            bf16(*z)[DK + 8] = a == 0 ? sm.Xh : a == 1 ? sm.Xl : a == 2 ? sm.Yh : sm.Yl;
+            *(bf16x8 *)&z[4 * nblk + (rem >> 4)][8 * (rem & 15)] = bf16x8{};
+        }
+        if (vtask)
+            conv_slice<SRC == 2>(vr, vbase, sm.cs, sm.cs + 2 * 8 * 16 * 4, vsl, false, 1.f, t0, L,
+                                 vtb, s16, vsl ? sm.Yh : sm.Xh, vsl ? sm.Yl : sm.Xl);
+    }
+    if (hact && lane < 16) {
+        const int b0 = 16 * w4, c = lane;
+        float t[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float acc = 0.f;
+#pragma unroll
+            for (int k4 = 0; k4 < i; k4 += 4) {
+                const float4 a = rd4(&AT[b0 + i][b0 + k4]);
+                acc = fmaf(a.x, t[k4], acc);
+                if (k4 + 1 < i)
+                    acc = fmaf(a.y, t[k4 + 1], acc);
+                if (k4 + 2 < i)
+                    acc = fmaf(a.z, t[k4 + 2], acc);
+                if (k4 + 3 < i)
+                    acc = fmaf(a.w, t[k4 + 3], acc);
+            }
+            t[i] = (i == c ? 1.f : 0.f) - acc;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (i >= c)
+                AT[b0 + i][b0 + c] = t[i];
+    }
+    lds_barrier();
+    /* 4b: inside 32x32 diagonal block p (wave w4 = p): T_10 = -T_11 (A_10
+     * T_00), 16x16 blocks; lane = (row l/4, columns 4(l%4)..+3) */
+    if (hact && w4 < 2) {
+        const int p0 = 32 * w4, rr = lane >> 2, c0 = 4 * (lane & 3);
+        float *a10 = &AT[p0 + 16 + rr][p0];
+        const float4 x = row_times<16>(a10, &AT[p0][p0 + c0]);
+        wr4(a10 + c0, x);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const float4 y = row_times<16>(&AT[p0 + 16 + rr][p0 + 16], &AT[p0 + 16][p0 + c0]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wr4(a10 + c0, make_float4(-y.x, -y.y, -y.z, -y.w));
+    }
+    lds_barrier();
+    /* 4c: T_10 = -T_11 (A_10 T_00) with 32x32 blocks; lane = (row 8 w4 +
+     * l/8, columns 4(l%8)..+3). A chunk of at most 32 tokens has A_10 = 0
+     * and so T_10 = 0, which the array already holds. Every wave passes the
+     * same barriers. */
+    if (L > 32) {
+        const int rr = 32 + 8 * w4 + (lane >> 3), c0 = 4 * (lane & 7);
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (hact)
+            x = row_times<32>(&AT[rr][0], &AT[0][c0]);
+        lds_barrier();
+        if (hact)
+            wr4(&AT[rr][c0], x);
+        lds_barrier();
+        float4 y = x;
+        if (hact)
+            y = row_times<32>(&AT[rr][32], &AT[32][c0]);
+        lds_barrier();
+        if (hact)
+            wr4(&AT[rr][c0], make_float4(-y.x, -y.y, -y.z, -y.w));
+        lds_barrier();
+    }
+
+    /* ---- 5. per group: W = T (beta e^G K) (dk block 32 w4, K hi) and
+     * U = T (beta V) (dv block 32 w4, V hi + lo) ---- */
+    {
+        const float *sKr = sm.sK[hg], *sVr = sm.sV[hg];
+        floatx16 accw[2] = {}, accu[2] = {};
+        if (hact) {
+            floatx16 dX[2], dV[2]; /* rows 32tb.. of K (V), columns 32 w4.. */
 #pragma unroll
             for (int tb = 0; tb < 2; tb++) {
-                dX[tb] = floatx16{};
+                dX[tb] = dV[tb] = floatx16{};
 #pragma unroll
                 for (int s = 0; s < 2; s++) {
                     const int c = 32 * w4 + 16 * s + 8 * h;
-                    if (isw) {
-                        dX[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            ld8(&sm.Kh[32 * tb + col][c]), eye[s], dX[tb], 0, 0, 0);
-                    } else {
-                        dX[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            ld8(&sm.Xh[32 * tb + col][c]), eye[s], dX[tb], 0, 0, 0);
-                        dX[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            ld8(&sm.Xl[32 * tb + col][c]), eye[s], dX[tb], 0, 0, 0);
-                    }
+                    dX[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld8(&sm.Kh[32 * tb + col][c]),
+                                                                     eye[s], dX[tb], 0, 0, 0);
+                    dV[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld8(&Vh[32 * tb + col][c]),
+                                                                     eye[s], dV[tb], 0, 0, 0);
+                    dV[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld8(&Vl[32 * tb + col][c]),
+                                                                     eye[s], dV[tb], 0, 0, 0);
                 }
             }
-            /* B operands: token k-steps ks (tile ks/2, rows 8(ks%2)..), the
-             * per-token scale beta e^G (K) or beta (V); V also keeps lo */
-            bf16x8 xb[4], xl[4];
+            /* B operands: token k-steps ks (tile ks/2, rows 8(ks%2)..) times
+             * beta e^G (K) or beta (V, kept as hi + lo) */
+            bf16x8 xk[4], xvh[4], xvl[4];
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
                 const int tb = ks >> 1, r0 = 8 * (ks & 1);
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const int t = tok(tb, r0 + e);
-                    const float x = dX[tb][r0 + e] * (isw ? sKr[t] : sVr[t]);
-                    { const bfpair sp_ = split2(x); xb[ks][e] = sp_.hi; xl[ks][e] = sp_.lo; }
+                    xk[ks][e] = f2bf(dX[tb][r0 + e] * sKr[t]);
+                    const bfpair sp = split2(dV[tb][r0 + e] * sVr[t]);
+                    xvh[ks][e] = sp.hi;
+                    xvl[ks][e] = sp.lo;
                 }
             }
-            floatx16 acc[2] = {};
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
 #pragma unroll
                 for (int mi = 0; mi < 2; mi++) {
                     /* T row 32mi + col, columns in the accumulator order */
-                    const float *tr = &sm.AT[32 * mi + col][16 * ks + 4 * h];
+                    const float *tr = &AT[32 * mi + col][16 * ks + 4 * h];
                     const float4 a0 = rd4(tr), a1 = rd4(tr + 8);
                     const bf16x8 a = {f2bf(a0.x), f2bf(a0.y), f2bf(a0.z), f2bf(a0.w),
                                       f2bf(a1.x), f2bf(a1.y), f2bf(a1.z), f2bf(a1.w)};
-                    acc[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xb[ks], acc[mi], 0, 0, 0);
-                    if (!isw)
-                        acc[mi] =
-                            __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xl[ks], acc[mi], 0, 0, 0);
+                    accw[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xk[ks], accw[mi], 0, 0, 0);
+                    accu[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xvh[ks], accu[mi], 0, 0, 0);
+                    accu[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xvl[ks], accu[mi], 0, 0, 0);
                 }
             }
-            lds_barrier(); /* every wave is done with T and the v rows */
-            bf16(*Wst)[DK + 8] = reinterpret_cast<bf16(*)[DK + 8]>(&sm.AT[0][0]);
-            float(*Ust)[DV + 4] = reinterpret_cast<float(*)[DV + 4]>(&sm.Xh[0][0]);
+        }
+        lds_barrier(); /* every wave is done with T and the v rows */
+        if (hact) {
+            bf16(*Wst)[DK + 8] = reinterpret_cast<bf16(*)[DK + 8]>(&AT[0][0]);
+            float(*Ust)[DV + 4] = reinterpret_cast<float(*)[DV + 4]>(&Vh[0][0]);
 #pragma unroll
             for (int mi = 0; mi < 2; mi++)
 #pragma unroll
                 for (int rr = 0; rr < 16; rr++) {
-                    if (isw)
-                        Wst[tok(mi, rr)][32 * w4 + col] = f2bf(acc[mi][rr]);
-                    else
-                        Ust[tok(mi, rr)][32 * w4 + col] = acc[mi][rr];
+                    Wst[tok(mi, rr)][32 * w4 + col] = f2bf(accw[mi][rr]);
+                    Ust[tok(mi, rr)][32 * w4 + col] = accu[mi][rr];
                 }
         }
-        lds_barrier();
-        /* ---- 7. W in the fragment order of q e^G; U (fp32) as 16x16
-         * accumulator fragments: entry i = (32-column block i/256, row block
-         * (i/64)%4, lane i%64) holds rows 16((i/64)%4) + 4((i/16)%4) + 0..3 of
-         * columns 32(i/256) + i%16 (values 0..3) and +16 (values 4..7) ---- */
-        {
-            bf16(*Wst)[DK + 8] = reinterpret_cast<bf16(*)[DK + 8]>(&sm.AT[0][0]);
-            float(*Ust)[DV + 4] = reinterpret_cast<float(*)[DV + 4]>(&sm.Xh[0][0]);
+    }
+    lds_barrier();
+    /* ---- 6. W in the fragment order of q e^G; U (fp32) as 16x16
+     * accumulator fragments: entry i = (32-column block i/256, row block
+     * (i/64)%4, lane i%64) holds rows 16((i/64)%4) + 4((i/16)%4) + 0..3 of
+     * columns 32(i/256) + i%16 (values 0..3) and +16 (values 4..7) ---- */
+    if (hact) {
+        bf16(*Wst)[DK + 8] = reinterpret_cast<bf16(*)[DK + 8]>(&AT[0][0]);
+        float(*Ust)[DV + 4] = reinterpret_cast<float(*)[DV + 4]>(&Vh[0][0]);
+        const int u = tid & 255;
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int i = tid + PA_THREADS * j;
-                const int t = 16 * (i >> 8) + (i & 15), c8 = 32 * ((i >> 6) & 3) + 8 * ((i >> 4) & 3);
-                *(bf16x8 *)(Wo + (cb * 1024 + i) * 8) = ld8(&Wst[t][c8]);
-                const int tu = 16 * ((i >> 6) & 3) + 4 * ((i >> 4) & 3), cu = 32 * (i >> 8) + (i & 15);
-                float *dst = Uo + (cb * 1024 + i) * 8;
-                *(float4 *)dst = make_float4(Ust[tu][cu], Ust[tu + 1][cu], Ust[tu + 2][cu],
-                                             Ust[tu + 3][cu]);
-                *(float4 *)(dst + 4) = make_float4(Ust[tu][cu + 16], Ust[tu + 1][cu + 16],
-                                                   Ust[tu + 2][cu + 16], Ust[tu + 3][cu + 16]);
-            }
+        for (int j = 0; j < 4; j++) {
+            const int i = u + 256 * j;
+            const int t = 16 * (i >> 8) + (i & 15), c8 = 32 * ((i >> 6) & 3) + 8 * ((i >> 4) & 3);
+            *(bf16x8 *)(Wo + (cbg * 1024 + i) * 8) = ld8(&Wst[t][c8]);
+            const int tu = 16 * ((i >> 6) & 3) + 4 * ((i >> 4) & 3), cu = 32 * (i >> 8) + (i & 15);
+            float *dst = Uo + (cbg * 1024 + i) * 8;
+            *(float4 *)dst = make_float4(Ust[tu][cu], Ust[tu + 1][cu], Ust[tu + 2][cu],
+                                         Ust[tu + 3][cu]);
+            *(float4 *)(dst + 4) = make_float4(Ust[tu][cu + 16], Ust[tu + 1][cu + 16],
+                                               Ust[tu + 2][cu + 16], Ust[tu + 3][cu + 16]);
         }
-        lds_barrier(); /* the next v-head rewrites G, AT and the v rows */
     }
 }
 
@@ -1434,11 +1434,12 @@ extern "C" hipError_t k_gdn_scan(const float *q, const float *k, const float *v,
                                  int N, hipStream_t stream) {
     if (ck->num_chunks <= 0 || N <= 0)
         return hipSuccess;
-    if (Hk <= 0 || Hv % Hk != 0 || Hv / Hk > PA_MAX_REP || (ck->chunk_starts && S_out))
+    if (Hk <= 0 || Hv % Hk != 0 || (ck->chunk_starts && S_out))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gdn_chunk_a_kernel<0>, dim3((unsigned)ck->num_chunks, (unsigned)Hk),
+    const int npairs = CEIL_DIV(Hv / Hk, 2);
+    hipLaunchKernelGGL(gdn_chunk_a_kernel<0>, dim3((unsigned)ck->num_chunks, (unsigned)(Hk * npairs)),
                        dim3(PA_THREADS), 0, stream, q, k, v, g, beta, ConvSrc{}, ck->chunk_tok0,
-                       ck->chunk_len, ck->chunk_starts, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->Qg,
+                       ck->chunk_len, ck->chunk_starts, Hk, Hv, npairs, (bf16 *)ws->W, (bf16 *)ws->Qg,
                        (bf16 *)ws->QK, (bf16 *)ws->KgT, ws->U, ws->Glast);
     return gdn_phase_b(ck, S_in, S_out, z, z_stride, norm_w, eps, Hv, y, ws, N, TailJob{},
                        stream);
@@ -1453,8 +1454,7 @@ extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const flo
                                   hipStream_t stream) {
     if (N <= 0)
         return hipSuccess;
-    if (Hk <= 0 || Hv % Hk != 0 || Hv / Hk > PA_MAX_REP || (ck->chunk_starts && S_out) ||
-        proj_stride % 8 != 0 ||
+    if (Hk <= 0 || Hv % Hk != 0 || (ck->chunk_starts && S_out) || proj_stride % 8 != 0 ||
         ((uintptr_t)proj & 15) != 0)
         return hipErrorInvalidValue;
     const int C = (2 * Hk + Hv) * DK;
@@ -1469,12 +1469,14 @@ extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const flo
                      A_neg_exp,          dt_bias,     N};
     /* the conv tail rides along with phase B */
     const TailJob tail{(const bf16 *)proj, proj_stride, conv_in, conv_out, seg0_len, C};
+    const int npairs = CEIL_DIV(Hv / Hk, 2);
     hipLaunchKernelGGL(conv_in ? gdn_chunk_a_kernel<2> : gdn_chunk_a_kernel<1>,
-                       dim3((unsigned)ck->num_chunks, (unsigned)Hk), dim3(PA_THREADS), 0, stream,
+                       dim3((unsigned)ck->num_chunks, (unsigned)(Hk * npairs)), dim3(PA_THREADS), 0,
+                       stream,
                        (const float *)nullptr, (const float *)nullptr, (const float *)nullptr,
                        (const float *)nullptr, (const float *)nullptr, cv, ck->chunk_tok0,
-                       ck->chunk_len, ck->chunk_starts, Hk, Hv, (bf16 *)ws->W, (bf16 *)ws->Qg,
-                       (bf16 *)ws->QK, (bf16 *)ws->KgT, ws->U, ws->Glast);
+                       ck->chunk_len, ck->chunk_starts, Hk, Hv, npairs, (bf16 *)ws->W,
+                       (bf16 *)ws->Qg, (bf16 *)ws->QK, (bf16 *)ws->KgT, ws->U, ws->Glast);
     return gdn_phase_b(ck, S_in, S_out, proj + C, proj_stride, norm_w, eps, Hv, y, ws, N, tail,
                        stream);
 }

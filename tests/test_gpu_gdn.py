@@ -138,7 +138,9 @@ def run_gpu(o, L, proj, seg_lens, conv_in=None, S_in=None, write_state=False, te
 
 
 @pytest.mark.parametrize("seed,Hk,Hv,T", [(0, 2, 4, 1), (1, 2, 4, 63), (2, 2, 4, 64),
-                                          (3, 2, 4, 200), (4, 1, 2, 2)])
+                                          (3, 2, 4, 200), (4, 1, 2, 2),
+                                          # one and three v-heads per k-head
+                                          (5, 2, 2, 70), (6, 1, 3, 100)])
 def test_gdn_prefill_matches_oracle(seed, Hk, Hv, T):
     o = ops()
     print(f"prefill seed={seed} Hk={Hk} Hv={Hv} T={T}", flush=True)
