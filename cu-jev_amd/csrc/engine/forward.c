@@ -51,16 +51,31 @@ typedef struct {
 
 /* Projection GEMMs Y[N,M] = X[N,K] W^T. For few tokens (the eval, N <= 96)
  * the hand-written weight-streaming kernel reads the pre-tiled copy of the
- * weight (its time is the HBM stream of W); larger N (the prefill) goes to
- * hipBLASLt on the plain rows. CUJEV_SMALL_GEMM=0 sends everything to
- * hipBLASLt. */
+ * weight (its time is the HBM stream of W). Prefill token counts go to
+ * hipBLASLt on the plain rows, except where the hand-tiled prefill kernel
+ * (gemm_wide, same tiled copy) measured faster on MI355X: the fused
+ * gate|up + silu_mul projection up to 4096 tokens and down_proj, split over
+ * K into partials the residual add sums, up to 1536 tokens.
+ * CUJEV_SMALL_GEMM=0 / CUJEV_WIDE_GEMM=0 send those shapes to hipBLASLt. */
+static int env_on(const char *name) {
+    const char *e = getenv(name);
+    return !(e && *e == '0');
+}
+
 static int small_gemm_ok(int N, int M, int K) {
     static int cached = -1;
-    if (cached < 0) {
-        const char *e = getenv("CUJEV_SMALL_GEMM");
-        cached = !(e && *e == '0');
-    }
+    if (cached < 0)
+        cached = env_on("CUJEV_SMALL_GEMM");
     return cached && N <= CUJEV_GEMM_SMALL_MAX_N && cujev_gemm_small_splits(M, K) > 0;
+}
+
+#define CUJEV_WIDE_GATED_MAX_N 4096
+#define CUJEV_WIDE_RESID_MAX_N 1536
+static int wide_gemm_on(void) {
+    static int cached = -1;
+    if (cached < 0)
+        cached = env_on("CUJEV_WIDE_GEMM");
+    return cached;
 }
 
 static hipError_t proj_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, const bf16_t *Wt,
@@ -72,10 +87,14 @@ static hipError_t proj_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, co
 
 /* A projection whose output feeds the residual add (o_proj, out_proj,
  * down_proj: M = H). Returns through *y / *yp / *splits what the following
- * k_add_rmsnorm reads: bf16 rows, or the few-token GEMM's split-K partials. */
+ * k_add_rmsnorm reads: bf16 rows, or split-K fp32 partials in m->ypart.
+ * `wide`: the prefill kernel may take it (down_proj). */
 static hipError_t resid_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, const bf16_t *Wt,
-                             int N, int M, int K, const bf16_t **y, const float **yp,
+                             int N, int M, int K, int wide, const bf16_t **y, const float **yp,
                              int *splits) {
+    *y = m->y;
+    *yp = NULL;
+    *splits = 0;
     if (Wt && small_gemm_ok(N, M, K)) {
         const int sp = cujev_gemm_small_splits(M, K);
         if (sp > 1) {
@@ -84,11 +103,38 @@ static hipError_t resid_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, c
             *splits = sp;
             return k_gemm_small(X, K, Wt, N, M, K, 0, sp, NULL, 0, m->ypart, m->stream);
         }
+        return k_gemm_small(X, K, Wt, N, M, K, 0, 1, m->y, M, NULL, m->stream);
     }
-    *y = m->y;
-    *yp = NULL;
-    *splits = 0;
-    return proj_gemm(m, X, W, Wt, m->y, N, M, K);
+    if (Wt && wide && wide_gemm_on() && N <= CUJEV_WIDE_RESID_MAX_N) {
+        size_t cap = m->ypart_bytes / ((size_t)N * M * 4);
+        const int max_sp = cap > 8 ? 8 : (int)cap;
+        int rg, ng, sp;
+        if (max_sp >= 1 && cujev_gemm_wide_plan(N, M, K, 0, max_sp, &rg, &ng, &sp) == 0) {
+            if (sp > 1) {
+                *y = NULL;
+                *yp = m->ypart;
+                *splits = sp;
+                return k_gemm_wide(X, K, Wt, N, M, K, 0, rg, ng, sp, NULL, 0, m->ypart,
+                                   m->stream);
+            }
+            return k_gemm_wide(X, K, Wt, N, M, K, 0, rg, ng, 1, m->y, M, NULL, m->stream);
+        }
+    }
+    return k_gemm(m->gemm, X, W, m->y, 0, N, M, K, m->stream);
+}
+
+/* gate|up projection + silu_mul into m->act [N][I] */
+static hipError_t gate_up_gemm(cujev_model *m, const cujev_layer *ly, int N, int I, int H) {
+    if (ly->wt_gate_up && small_gemm_ok(N, 2 * I, H))
+        return k_gemm_small(m->xb, H, ly->wt_gate_up, N, 2 * I, H, 1, 1, m->act, I, NULL,
+                            m->stream);
+    int rg, ng, sp;
+    if (ly->wt_gate_up && wide_gemm_on() && N <= CUJEV_WIDE_GATED_MAX_N &&
+        cujev_gemm_wide_plan(N, 2 * I, H, 1, 1, &rg, &ng, &sp) == 0)
+        return k_gemm_wide(m->xb, H, ly->wt_gate_up, N, 2 * I, H, 1, rg, ng, 1, m->act, I, NULL,
+                           m->stream);
+    hipError_t e = proj_gemm(m, m->xb, ly->w_gate_up, NULL, m->proj, N, 2 * I, H);
+    return e != hipSuccess ? e : k_silu_mul(m->proj, m->act, N, I, m->stream);
 }
 
 /* The kernels of one forward (and the candidate readout); no host sync. */
@@ -132,7 +178,7 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
                               P, m->state_stride, kdst, vdst, kstride, a->base, N, m->Hq,
                               m->Hkv, m->mix_out, m->attn_ws, m->attn_ws_bytes, s),
                   "attention", l);
-            K_TRY(resid_gemm(m, m->mix_out, ly->w_o, ly->wt_o, N, H, m->Hq * m->D, &ry, &ryp,
+            K_TRY(resid_gemm(m, m->mix_out, ly->w_o, ly->wt_o, N, H, m->Hq * m->D, 0, &ry, &ryp,
                              &rsp),
                   "gemm o", l);
         } else {
@@ -145,20 +191,14 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
                               ly->A_neg_exp, ly->dt_bias, &a->chunks, S_in, S_out, ly->g_norm,
                               eps, m->Hk, m->Hv, m->mix_out, &gws, N, s),
                   "gdn_layer", l);
-            K_TRY(resid_gemm(m, m->mix_out, ly->w_out, ly->wt_out, N, H, m->V, &ry, &ryp, &rsp),
+            K_TRY(resid_gemm(m, m->mix_out, ly->w_out, ly->wt_out, N, H, m->V, 0, &ry, &ryp,
+                             &rsp),
                   "gemm out", l);
         }
         K_TRY(k_add_rmsnorm(m->x, ry, ryp, rsp, ly->post_norm, m->xb, N, H, eps, NULL, 0, s),
               "add+norm", l);
-        if (ly->wt_gate_up && small_gemm_ok(N, 2 * I, H)) { /* GEMM + silu_mul in one */
-            K_TRY(k_gemm_small(m->xb, H, ly->wt_gate_up, N, 2 * I, H, 1, 1, m->act, I, NULL, s),
-                  "gemm gate_up", l);
-        } else {
-            K_TRY(proj_gemm(m, m->xb, ly->w_gate_up, NULL, m->proj, N, 2 * I, H), "gemm gate_up",
-                  l);
-            K_TRY(k_silu_mul(m->proj, m->act, N, I, s), "silu_mul", l);
-        }
-        K_TRY(resid_gemm(m, m->act, ly->w_down, ly->wt_down, N, H, I, &ry, &ryp, &rsp),
+        K_TRY(gate_up_gemm(m, ly, N, I, H), "gemm gate_up", l);
+        K_TRY(resid_gemm(m, m->act, ly->w_down, ly->wt_down, N, H, I, 1, &ry, &ryp, &rsp),
               "gemm down", l);
         if (l + 1 < c->num_layers)
             K_TRY(k_add_rmsnorm(m->x, ry, ryp, rsp, m->layers[l + 1].in_norm, m->xb, N, H, eps,

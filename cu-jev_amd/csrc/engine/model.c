@@ -299,6 +299,16 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
     m->meta_ints = 3 * N + 3 * B + 4 * (size_t)m->max_chunks + B * (size_t)m->opts.max_candidates + B;
     m->gemm_ws_bytes = (size_t)64 << 20;
     m->attn_ws_bytes = cujev_attention_ws_max(m->max_tokens, m->Hq, m->Hkv);
+    /* split-K partials: the few-token GEMM's at most 8 splits of 96 tokens,
+     * and 64 MiB (or what 8 splits of all N tokens need, if less) for the
+     * prefill GEMM, which fits its split count to it */
+    {
+        const size_t small = (size_t)CUJEV_GEMM_SMALL_MAX_SPLITS * CUJEV_GEMM_SMALL_MAX_N * H * 4;
+        size_t wide = (size_t)64 << 20;
+        if (wide > 8 * N * H * 4)
+            wide = 8 * N * H * 4;
+        m->ypart_bytes = small > wide ? small : wide;
+    }
     struct {
         void **p;
         size_t bytes;
@@ -307,7 +317,7 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
         {(void **)&m->xb, N * H * 2},
         {(void **)&m->proj, N * (size_t)m->w_proj * 2},
         {(void **)&m->y, N * H * 2},
-        {(void **)&m->ypart, (size_t)CUJEV_GEMM_SMALL_MAX_SPLITS * CUJEV_GEMM_SMALL_MAX_N * H * 4},
+        {(void **)&m->ypart, m->ypart_bytes},
         {&m->attn_ws, m->attn_ws_bytes},
         {(void **)&m->q, N * (size_t)m->Hq * m->D * 2},
         {(void **)&m->mix_out, mix * 2},

@@ -82,7 +82,9 @@ struct cujev_model {
     bf16_t *xb;      /* [N,H] normed input */
     bf16_t *proj;    /* [N, w_proj] */
     bf16_t *y;       /* [N,H] */
-    float *ypart;    /* [CUJEV_GEMM_SMALL_MAX_SPLITS][CUJEV_GEMM_SMALL_MAX_N][H]: split-K partials of the few-token GEMMs */
+    float *ypart;    /* split-K partials [splits][N][H] of the residual projections */
+    size_t ypart_bytes; /* >= the few-token GEMM's 8 x 96 x H floats; the prefill GEMM
+                         * picks its split count to fit */
     void *attn_ws;   /* key-split partials of the attention for few-token evals */
     size_t attn_ws_bytes;
     bf16_t *q;       /* [N,Hq,256] prescaled */

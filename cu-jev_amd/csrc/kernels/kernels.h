@@ -224,6 +224,20 @@ hipError_t k_gemm_small(const bf16_t *X, int ldx, const bf16_t *W, int N, int M,
  * chunk * (M/16) + row group. */
 hipError_t k_gemm_small_tile(const bf16_t *W, int M, int K, bf16_t *Wt, hipStream_t stream);
 
+/* ---- tiled GEMM for prefill token counts (gemm_wide.hip) ------------------
+ * Same operands and outputs as k_gemm_small (tiled W, X rows of stride ldx,
+ * bf16 Y / gated act / fp32 partials P[splits][N][M]) for any N >= 1; M % 16
+ * == 0 (gated: M % 32), K % 128 == 0, (K / 128) % splits == 0, X and W each
+ * under 4 GiB. The tile is 64 RG weight rows (gated: 32 RG gate rows and the
+ * same up rows) x 32 NG tokens; cujev_gemm_wide_plan picks RG, NG and a split
+ * count <= max_splits (1 = no partials) for a shape and returns 0, or -1 for
+ * an unsupported shape. CUJEV_WIDE_PLAN="RG,NG,S" forces a plan. */
+int cujev_gemm_wide_plan(int N, int M, int K, int gated, int max_splits, int *RG, int *NG, int *S);
+int cujev_gemm_wide_supported(int RG, int NG, int gated);
+hipError_t k_gemm_wide(const bf16_t *X, int ldx, const bf16_t *Wt, int N, int M, int K, int gated,
+                       int RG, int NG, int splits, bf16_t *Y, int ldy, float *P,
+                       hipStream_t stream);
+
 /* ---- projection GEMMs (hipBLASLt) ------------------------------------------
  * Y[N,M] = X[N,K] . W[M,K]^T, bf16 in, fp32 accumulate, bf16 (f32out = 0) or
  * fp32 out. REF elementwise.cu:56-75. `workspace` (ws_bytes) is device memory

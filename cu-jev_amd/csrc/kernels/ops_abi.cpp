@@ -85,6 +85,24 @@ EXPORT int cujev_op_gemm_small(const void *X, int ldx, const void *W, int N, int
                     "gemm_small");
 }
 
+EXPORT int cujev_op_gemm_wide(const void *X, int ldx, const void *W, int N, int M, int K,
+                              int gated, int rg, int ng, int splits, void *Y, int ldy, float *P,
+                              void *stream) {
+    if (N < 0 || M <= 0 || K <= 0 || !X || !W || ldx < K || splits < 1 ||
+        (splits == 1 && (!Y || ldy < (gated ? M / 2 : M))) || (splits > 1 && !P))
+        return fail(1, "gemm_wide: bad arguments");
+    return launched(k_gemm_wide((const bf16_t *)X, ldx, (const bf16_t *)W, N, M, K, gated, rg, ng,
+                                splits, (bf16_t *)Y, ldy, P, (hipStream_t)stream),
+                    "gemm_wide");
+}
+
+EXPORT int cujev_ops_gemm_wide_plan(int N, int M, int K, int gated, int max_splits, int *rg,
+                                    int *ng, int *splits) {
+    if (!rg || !ng || !splits)
+        return -1;
+    return cujev_gemm_wide_plan(N, M, K, gated, max_splits, rg, ng, splits);
+}
+
 EXPORT int cujev_op_gemm_small_tile(const void *W, int M, int K, void *Wt, void *stream) {
     if (!W || !Wt || W == Wt || M <= 0 || K <= 0 || M % 16 || K % 128)
         return fail(1, "gemm_small_tile: bad arguments");

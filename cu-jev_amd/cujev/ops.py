@@ -40,6 +40,7 @@ _SIGS = {
                                _P, _P],
     "cujev_op_gemm_small": [_P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _P],
     "cujev_op_gemm_small_tile": [_P, _I, _I, _P, _P],
+    "cujev_op_gemm_wide": [_P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P],
     "cujev_op_add_rmsnorm": [_P, _P, _P, _I, _P, _P, _I, _I, _F, _P, _I, _P],
     "cujev_op_gdn_layer": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P,
                            _P, _P, _F, _I, _I, _I, _P, _P, _P],
@@ -68,6 +69,9 @@ def load():
     lib.cujev_ops_gdn_scratch_bytes.restype = C.c_size_t
     lib.cujev_ops_gemm_small_splits.argtypes = [_I, _I]
     lib.cujev_ops_gemm_small_splits.restype = _I
+    lib.cujev_ops_gemm_wide_plan.argtypes = [_I, _I, _I, _I, _I, C.POINTER(_I), C.POINTER(_I),
+                                             C.POINTER(_I)]
+    lib.cujev_ops_gemm_wide_plan.restype = _I
     lib.cujev_ops_attention_ws_bytes.argtypes = [_I, _I, _I, _I]
     lib.cujev_ops_attention_ws_bytes.restype = C.c_size_t
     lib.cujev_ops_blaslt_version.argtypes = []
@@ -86,7 +90,7 @@ def load():
 
 def exported_symbols():
     return ["cujev_ops_kv_stride", "cujev_ops_last_error", "cujev_ops_gdn_scratch_bytes",
-            "cujev_ops_gemm_small_splits", "cujev_ops_attention_ws_bytes",
+            "cujev_ops_gemm_small_splits", "cujev_ops_gemm_wide_plan", "cujev_ops_attention_ws_bytes",
             "cujev_ops_blaslt_version", "cujev_op_gemm_tune", *_SIGS]
 
 
@@ -279,6 +283,32 @@ def gemm_small(X, W, Y=None, P=None, splits=1, gated=False, N=None, K=None):
     _call("cujev_op_gemm_small", _ptr(X), X.stride(0), _ptr(W), int(N), int(M), int(K),
           int(bool(gated)), int(splits), _ptr(Y), Y.stride(0) if Y is not None else 0, _ptr(P),
           _stream())
+
+
+def gemm_wide_plan(N, M, K, gated=False, max_splits=1):
+    """(rg, ng, splits) the engine's planner picks for a prefill GEMM shape."""
+    a, b, c = _I(), _I(), _I()
+    if load().cujev_ops_gemm_wide_plan(int(N), int(M), int(K), int(bool(gated)), int(max_splits),
+                                       C.byref(a), C.byref(b), C.byref(c)) != 0:
+        raise OpsError(f"gemm_wide_plan: unsupported shape N={N} M={M} K={K}")
+    return a.value, b.value, c.value
+
+
+def gemm_wide(X, W, Y=None, P=None, splits=1, gated=False, rg=None, ng=None):
+    """Prefill GEMM on the tiled W: Y[N,M] = X[N,K] . W[M,K]^T (bf16 Y; gated:
+    Y = act[N, M/2]) or fp32 partials P[splits][N][M]. rg/ng default to the
+    planner's tile for this shape and split count."""
+    N, K = X.shape[0], W.shape[1]
+    M = W.shape[0]
+    if rg is None or ng is None:
+        rg, ng, _ = gemm_wide_plan(N, M, K, gated, 1)
+        if splits > 1:
+            rg, ng, s = gemm_wide_plan(N, M, K, gated, splits)
+            if s != splits:
+                rg, ng = 2, 8
+    _call("cujev_op_gemm_wide", _ptr(X), X.stride(0), _ptr(W), int(N), int(M), int(K),
+          int(bool(gated)), int(rg), int(ng), int(splits), _ptr(Y),
+          Y.stride(0) if Y is not None else 0, _ptr(P), _stream())
 
 
 def add_rmsnorm(x, w, out, eps, y=None, yp=None, splits=0, rows=None):

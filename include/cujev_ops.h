@@ -71,6 +71,21 @@ int cujev_op_gemm_small_tile(const void *W, int M, int K, void *Wt, void *stream
 /* Split count the engine uses for an (M, K) few-token GEMM; 0 = unsupported shape. */
 int cujev_ops_gemm_small_splits(int M, int K);
 
+/* Replaces reference src/kernels/kernels.h:50-53 (k_gemm_bf16) at prefill
+ * token counts (any N >= 1): the operands and outputs of
+ * cujev_op_gemm_small (tiled W from cujev_op_gemm_small_tile; bf16 Y, gated
+ * act[N][M/2], or fp32 partials P[splits][N][M] to be summed in split order)
+ * through a hand-tiled MFMA kernel. M % 16 == 0 (gated: M % 32 == 0),
+ * K % 128 == 0, (K/128) % splits == 0, X and W under 4 GiB each. The tile is
+ * 64 rg weight rows (gated: 32 rg gate rows and the same up rows) x 32 ng
+ * tokens; (rg, ng) must be a pair cujev_ops_gemm_wide_plan can return. */
+int cujev_op_gemm_wide(const void *X, int ldx, const void *W, int N, int M, int K, int gated,
+                       int rg, int ng, int splits, void *Y, int ldy, float *P, void *stream);
+/* The tile (rg, ng) and split count (<= max_splits) the engine uses for a
+ * shape; 0 on success, -1 for an unsupported shape. */
+int cujev_ops_gemm_wide_plan(int N, int M, int K, int gated, int max_splits, int *rg, int *ng,
+                             int *splits);
+
 /* Replaces reference src/kernels/kernels.h:40-43 (k_rmsnorm, k_add) fused:
  * row r reads source row src = rows ? rows[r] : r (R rows, else N);
  * v = x[src] + (y ? y[src] : yp ? bf16(sum_s yp[s][src]) : 0), written back
