@@ -265,19 +265,21 @@ def kernel_rooflines():
                        "frac": round(att["tflops"] / PEAK_BF16_TFLOPS, 4),
                        "traffic": kernel_bench.measured_traffic("attention"),
                        "traffic_source": "rocprofv3 --pmc FETCH_SIZE x2 + WRITE_SIZE x1 "
-                                         "(copy-calibrated), bytes per launch",
+                                         "(copy-calibrated), bytes per launch, measured at "
+                                         + kernel_bench.MEASURED_AT,
                        "us_per_launch": round(att["us"], 2),
                        "flop_per_launch": att["flop"]}
     gdn = gdn_roofline()
     log(f"gdn config 2 prefill: {gdn['us']:.1f} us, {gdn['gbs']:.1f} GB/s")
-    res["gdn_roofline"] = {"kernel": "gdn layer call: conv_tail + chunk_a (conv and gates "
-                                     "inside) + chunk_b + norm_gate, config 2 T=2048 "
-                                     "prefill", "bound": "hbm",
+    res["gdn_roofline"] = {"kernel": "gdn layer call: chunk_a (conv and gates inside) + "
+                                     "chunk_b (conv tail copied by extra workgroups) + "
+                                     "norm_gate, config 2 T=2048 prefill", "bound": "hbm",
                            "achieved": round(gdn["gbs"], 1), "peak": PEAK_HBM_GBS,
                            "unit": "GB/s", "frac": round(gdn["gbs"] / PEAK_HBM_GBS, 4),
                            "us_per_layer": round(gdn["us"], 2),
                            "compulsory_bytes": gdn["bytes"],
-                           "traffic": kernel_bench.measured_traffic("gdn")}
+                           "traffic": kernel_bench.measured_traffic("gdn"),
+                           "traffic_measured_at": kernel_bench.MEASURED_AT}
     gbr = gdn_roofline(case="gdn_branch")
     log(f"gdn config 2 branches: {gbr['us']:.1f} us, {gbr['gbs']:.1f} GB/s")
     res["gdn_branch_roofline"] = {"kernel": "gdn layer call: chunk_a (conv and gates inside, "
@@ -287,7 +289,8 @@ def kernel_rooflines():
                                   "unit": "GB/s", "frac": round(gbr["gbs"] / PEAK_HBM_GBS, 4),
                                   "us_per_layer": round(gbr["us"], 2),
                                   "compulsory_bytes": gbr["bytes"],
-                                  "traffic": kernel_bench.measured_traffic("gdn_branch")}
+                                  "traffic": kernel_bench.measured_traffic("gdn_branch"),
+                                  "traffic_measured_at": kernel_bench.MEASURED_AT}
     return res
 
 

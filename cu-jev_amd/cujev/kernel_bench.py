@@ -23,15 +23,19 @@ import sys
 # HBM traffic per launch, measured with rocprofv3 --pmc on MI355X (one
 # counter group per run): FETCH_SIZE and WRITE_SIZE in KiB per dispatch,
 # summed over the kernels of the case. A plain 256 MiB device copy reads
-# 131084 KiB of FETCH_SIZE and 262144 KiB of WRITE_SIZE, so FETCH_SIZE is
-# scaled by 2 and WRITE_SIZE by 1. The figures belong to the kernels of this
-# tree; re-measure after changing a kernel.
+# 131085 KiB of FETCH_SIZE and 262144 KiB of WRITE_SIZE, so FETCH_SIZE is
+# scaled by 2 and WRITE_SIZE by 1. Measured at commit fa3acd9 (GDN kernels as
+# of 59420b9, attention unchanged since its counters were first taken);
+# re-measure after changing a kernel.
 COPY_SCALE = {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0}
+MEASURED_AT = "fa3acd9"
 MEASURED_KIB = {
-    "attention": {"FETCH_SIZE": 115080.8, "WRITE_SIZE": 32930.9},
-    "gdn": {"FETCH_SIZE": 36.7 + 18148.3 + 37049.2 + 16398.7,
-            "WRITE_SIZE": 96.0 + 73984.0 + 18432.0 + 16384.0},
-    "gdn_branch": {"FETCH_SIZE": 9842.7 + 26690.0, "WRITE_SIZE": 36992.0 + 8192.0},
+    "attention": {"FETCH_SIZE": 115091.8, "WRITE_SIZE": 32967.1},
+    # chunk_a<1>, chunk_b (with the conv-tail workgroups), norm_gate
+    "gdn": {"FETCH_SIZE": 18182.7 + 57551.8 + 24595.3,
+            "WRITE_SIZE": 115233.0 + 34912.0 + 16384.0},
+    # chunk_a<2>, short_b
+    "gdn_branch": {"FETCH_SIZE": 9844.7 + 32824.4, "WRITE_SIZE": 57540.9 + 8192.0},
 }
 
 
