@@ -64,3 +64,36 @@ def test_request_oracle_catches_a_short_state(tiny):
     out = rq.request_logits(path, state[:-1], branches[:1], modes=("f64",), full=True)
     ref = q35.model_last_logits(cfg, W, state + branches[0][0])
     assert np.abs(out["f64"]["full"][0] - ref).max() / np.abs(ref).max() > 1e-3
+
+
+def _scan_inputs(seed=3, T=150, H=2, d=32):
+    rng = np.random.default_rng(seed)
+    rb = lambda x: q35.bf16_round(np.asarray(x, np.float32)).astype(np.float64)
+    q = rb(rng.normal(size=(T, H, d)) / np.sqrt(d))
+    k = rng.normal(size=(T, H, d))
+    k = rb(k / np.linalg.norm(k, axis=-1, keepdims=True))
+    v = rb(rng.normal(size=(T, H, d)))
+    g = -np.log1p(np.exp(rng.normal(size=(T, H))))
+    beta = 1.0 / (1.0 + np.exp(-rng.normal(size=(T, H))))
+    S0 = rng.normal(size=(H, d, d)) * 0.1
+    return q, k, v, g, beta, S0
+
+
+OPS = ("S", "Vp", "T", "W", "U", "Qg", "QK", "KgT", "O")
+
+
+def test_emulated_kernel_scan_is_pinned_to_the_chunked_form():
+    """oracle.request.gdn_chunk_emulated (the kernel's rounding points, used
+    for attribution statistics): with every operand carried as a split pair
+    it is the float64 chunked scan to split-bf16 precision; leaving any one
+    operand as plain bf16 moves it by about a bf16 rounding."""
+    q, k, v, g, beta, S0 = _scan_inputs()
+    o_ref, S_ref = q35.gdn_chunked(q, k, v, g, beta, S0)
+    rel = lambda a, b: float(np.abs(a - b).max() / np.abs(b).max())
+    o_all, S_all = rq.gdn_chunk_emulated(q, k, v, g, beta, S0, split=OPS)
+    assert rel(o_all, o_ref) <= 1e-4 and rel(S_all, S_ref) <= 1e-4
+    for op in OPS:
+        o1, S1 = rq.gdn_chunk_emulated(q, k, v, g, beta, S0, split=tuple(x for x in OPS if x != op))
+        e = max(rel(o1, o_ref), rel(S1, S_ref))
+        print(f"{op} as plain bf16: {e:.2e}")
+        assert 2e-5 < e <= 3e-2, op
