@@ -259,10 +259,13 @@ static cujev_status run_eval(cujev_model *m, cujev_state *st, const fwd_launch *
     /* a packed and an unpacked table can have the same chunk count, but
      * their metadata sits at other offsets of the uploaded block */
     const int packed = a->chunks.chunk_starts != NULL;
+    /* same shape, other GDN kernels: the segment lengths pick the path */
+    const int recur = cujev_gdn_recur_chosen(&a->chunks, m->Hv, 0, 0);
     for (int i = 0; i < CUJEV_GRAPH_SLOTS; i++) {
         cujev_graph_slot *x = &m->graphs[i];
         if (x->st == st && x->P == a->P && x->N == a->N && x->B == a->B && x->nc == a->nc &&
-            x->maxc == a->maxc && x->has_cand == has_cand && x->packed == packed) {
+            x->maxc == a->maxc && x->has_cand == has_cand && x->packed == packed &&
+            x->recur == recur) {
             g = x;
             break;
         }
@@ -282,6 +285,7 @@ static cujev_status run_eval(cujev_model *m, cujev_state *st, const fwd_launch *
         g->maxc = a->maxc;
         g->has_cand = has_cand;
         g->packed = packed;
+        g->recur = recur;
     }
     g->stamp = ++m->graph_clock;
     if (g->exec) {
@@ -441,11 +445,13 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
     a.rows = d + o_rows;
     a.cand = cand ? d + o_cand : NULL;
     a.ncand = cand ? d + o_ncand : NULL;
-    int max_snc = 0;
-    for (int b = 0; b < B; b++)
+    int max_snc = 0, max_len = 0;
+    for (int b = 0; b < B; b++) {
         max_snc = h[o_snc + b] > max_snc ? h[o_snc + b] : max_snc;
+        max_len = seg_len[b] > max_len ? seg_len[b] : max_len;
+    }
     const cujev_chunks chunks = {d + o_ctok, d + o_clen, d + o_sc0, d + o_snc, nc, B, max_snc,
-                                 NULL};
+                                 NULL, max_len};
     a.chunks = chunks;
     if (npk) {
         a.nc = a.chunks.num_chunks = npk;

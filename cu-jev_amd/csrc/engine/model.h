@@ -49,6 +49,7 @@ typedef struct cujev_graph_slot {
     const struct cujev_state *st;
     int P, N, B, nc, maxc, has_cand;
     int packed; /* GDN chunk table packed (its metadata offsets differ) */
+    int recur;  /* GDN layers run the token-by-token branch path */
     int seen; /* eager runs so far; -1: capture failed, this key stays eager */
     hipGraphExec_t exec;
     unsigned long long stamp;

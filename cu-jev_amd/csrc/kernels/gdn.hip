@@ -33,6 +33,8 @@
  * 8(r/4) + 4(l/32) + r%4. An accumulator used again as a B operand supplies
  * its k values in that row order, so the matching A operand is read as two
  * 4-element pieces at k offsets 4h and 8+4h of each 16-wide step. */
+#include <stdlib.h>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -1316,6 +1318,180 @@ __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
 /* y = bf16( w * bf16(o * rsqrt(mean o^2 + eps)) * silu(z) ) from the fp32
  * output o: 16 lanes per (token, v-head) row, 8 columns a lane.
  * REF src/kernels/gdn.cu:193-216. */
+/* ---------------------------------------------------------------------- */
+/* few-token branches: the recurrence token by token, fp32                 */
+/* ---------------------------------------------------------------------- */
+/* For an eval of a few short branches the chunked scan is one round of
+ * workgroups whose serial chains (conv, products, inverse, operand stores,
+ * then phase B) set the time. Here each workgroup owns one (segment, v-head,
+ * block of RC_COLS state columns), so a handful of branches still fills the
+ * chip, and runs the reference's recurrence (src/kernels/gdn.cu:140-176) in
+ * fp32 registers:
+ *   kS = S^T k;  v' = beta (v - e^g kS);  S = e^g S + k v'^T;  o = S^T q
+ * Wave w owns state columns 8w..8w+7 of the block whole: lane (c = l%8,
+ * r = l/8) holds rows 16r..16r+15 of column c, so k.S and q.S finish inside
+ * the wave (one DPP rotate and two permlane swaps) and the token loop has no
+ * barrier and no LDS traffic but the broadcast reads of k and q.
+ * Before it, the workgroup stages the segment's pre-conv rows (its k-head's
+ * q and k slices, its v columns) in LDS with every load in flight at once;
+ * thread t then runs channel t's causal conv + SiLU over the tokens with
+ * its weights and the state's tail in registers (gdn_conv_prep's
+ * arithmetic), and 8 lanes per (token, q|k) row apply the l2-norm and q's
+ * scale. o (fp32) goes to the gated norm kernel. */
+constexpr int RC_THREADS = 256;
+constexpr int RC_COLS = 32;
+constexpr int RC_MAXL = CUJEV_GDN_RECUR_MAX_LEN;
+constexpr int RC_CH = 2 * DK + RC_COLS; /* q, k and this block's v channels */
+
+struct RecurSmem {
+    float q[RC_MAXL][DK];
+    float k[RC_MAXL][DK];
+    float v[RC_MAXL][RC_COLS];
+    bf16 x[RC_MAXL][RC_CH]; /* pre-conv rows of the segment's tokens */
+    float g[RC_MAXL], beta[RC_MAXL];
+};
+
+/* sum over the 8 lanes l, l^8, ..., l^56 (lane bits 3..5) */
+DEV float sum_lanes8(float v) {
+    v += dpp<0x128>(v); /* row_ror:8 = lane ^ 8 inside a row of 16 */
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]); /* + lane ^ 16 */
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]); /* + lane ^ 32 */
+}
+
+template <bool TAIL>
+__global__ __launch_bounds__(RC_THREADS, 2) void gdn_recur_kernel(
+    ConvSrc cv, const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
+    const int32_t *__restrict__ seg_chunk0, int Hk, int Hv, int units,
+    const float *__restrict__ S_in, float *__restrict__ o) {
+    __shared__ __attribute__((aligned(16))) RecurSmem sm;
+    const int cb = blockIdx.x & 3, unit = blockIdx.x >> 2;
+    if (unit >= units)
+        return;
+    const int seg = unit / Hv, hv = unit - seg * Hv, hk = hv / (Hv / Hk);
+    const int c0 = seg_chunk0[seg];
+    const int t0 = chunk_tok0[c0], L = min(chunk_len[c0], RC_MAXL);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int C = (2 * Hk + Hv) * DK;
+    /* channel slot -> projection column: q slice, k slice, this block's v */
+    auto gch = [&](int ch) {
+        return ch < DK       ? hk * DK + ch
+               : ch < 2 * DK ? (Hk + hk) * DK + ch - DK
+                             : (2 * Hk + hv) * DK + RC_COLS * cb + ch - 2 * DK;
+    };
+
+    /* ---- stage: rows, gates; weights, tail and the state in registers ---- */
+    for (int i = tid; i < L * (RC_CH / 8); i += RC_THREADS) {
+        const int r = i / (RC_CH / 8), ch = 8 * (i - r * (RC_CH / 8));
+        *(bf16x8 *)&sm.x[r][ch] = ld8(cv.proj + (size_t)(t0 + r) * cv.ps + gch(ch));
+    }
+    if (tid < L) {
+        const bf16 *ab = cv.proj + (size_t)(t0 + tid) * cv.ps + C + Hv * DV;
+        sm.beta[tid] = sigmoid_f(bf2f(ab[hv]));
+        sm.g[tid] = cv.A_neg_exp[hv] * softplus_f(bf2f(ab[Hv + hv]) + cv.dt_bias[hv]);
+    }
+    /* thread t convolves q/k channel t, and v channel t when t < RC_COLS */
+    const int gq = gch(tid), gv = gch(2 * DK + (tid & (RC_COLS - 1)));
+    const float4 wq = *(const float4 *)(cv.conv_w + (size_t)gq * 4);
+    const float4 wv = *(const float4 *)(cv.conv_w + (size_t)gv * 4);
+    float tq[3], tv[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        tq[j] = TAIL ? cv.conv_in[(size_t)gq * 3 + j] : 0.f;
+        tv[j] = TAIL ? cv.conv_in[(size_t)gv * 3 + j] : 0.f;
+    }
+    const int c = lane & 7, r = lane >> 3, colw = 8 * wave + c;
+    float S[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        S[i] = S_in ? S_in[((size_t)hv * DK + 16 * r + i) * DV + RC_COLS * cb + colw] : 0.f;
+    lds_barrier();
+
+    /* ---- conv + SiLU, a sliding window per channel ---- */
+    {
+        float x3 = tq[0], x2 = tq[1], x1 = tq[2]; /* inputs of tokens -3, -2, -1 */
+        float *dst = tid < DK ? &sm.q[0][tid] : &sm.k[0][tid - DK];
+        for (int j = 0; j < L; j++) {
+            const float x0 = bf2f(sm.x[j][tid]);
+            float y = fmaf(wq.x, x3, 0.f);
+            y = fmaf(wq.y, x2, y);
+            y = fmaf(wq.z, x1, y);
+            y = fmaf(wq.w, x0, y);
+            dst[j * DK] = silu_f(y);
+            x3 = x2, x2 = x1, x1 = x0;
+        }
+    }
+    if (tid < RC_COLS) {
+        float x3 = tv[0], x2 = tv[1], x1 = tv[2];
+        for (int j = 0; j < L; j++) {
+            const float x0 = bf2f(sm.x[j][2 * DK + tid]);
+            float y = fmaf(wv.x, x3, 0.f);
+            y = fmaf(wv.y, x2, y);
+            y = fmaf(wv.z, x1, y);
+            y = fmaf(wv.w, x0, y);
+            sm.v[j][tid] = silu_f(y);
+            x3 = x2, x2 = x1, x1 = x0;
+        }
+    }
+    lds_barrier();
+    /* ---- l2-norm of q and k rows (q also * 128^-1/2), 8 lanes a row ---- */
+    for (int base = 0; base < 2 * L; base += RC_THREADS / 8) {
+        const int row = base + (tid >> 3), part = tid & 7;
+        if (row < 2 * L) { /* whole 8-lane groups */
+            float *rp = (row < L ? sm.q[row] : sm.k[row - L]) + 16 * part;
+            float4 a[4];
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                a[e] = *(const float4 *)(rp + 4 * e);
+                ss += a[e].x * a[e].x + a[e].y * a[e].y + a[e].z * a[e].z + a[e].w * a[e].w;
+            }
+            ss += dpp<0xB1>(ss);  /* lane ^ 1 */
+            ss += dpp<0x4E>(ss);  /* lane ^ 2 */
+            ss += dpp<0x141>(ss); /* the other quad of 8 */
+            const float inv = rsqrtf(ss + 1e-6f) * (row < L ? 0.08838834764831845f : 1.f);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                *(float4 *)(rp + 4 * e) =
+                    make_float4(a[e].x * inv, a[e].y * inv, a[e].z * inv, a[e].w * inv);
+        }
+    }
+    lds_barrier();
+
+    /* ---- the recurrence: no barrier, the waves run free ---- */
+    float *orow = o + (size_t)hv * DV + RC_COLS * cb + colw;
+    for (int j = 0; j < L; j++) {
+        float kq[16], qq[16];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float4 a = *(const float4 *)&sm.k[j][16 * r + 4 * e];
+            const float4 b = *(const float4 *)&sm.q[j][16 * r + 4 * e];
+            kq[4 * e] = a.x, kq[4 * e + 1] = a.y, kq[4 * e + 2] = a.z, kq[4 * e + 3] = a.w;
+            qq[4 * e] = b.x, qq[4 * e + 1] = b.y, qq[4 * e + 2] = b.z, qq[4 * e + 3] = b.w;
+        }
+        const float eg = fast_exp(sm.g[j]);
+        float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            p[i & 3] = fmaf(kq[i], S[i], p[i & 3]);
+        const float kS = sum_lanes8((p[0] + p[1]) + (p[2] + p[3]));
+        const float vn = sm.beta[j] * (sm.v[j][colw] - eg * kS);
+        float u[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            S[i] = fmaf(eg, S[i], kq[i] * vn);
+            u[i & 3] = fmaf(qq[i], S[i], u[i & 3]);
+        }
+        const float os = sum_lanes8((u[0] + u[1]) + (u[2] + u[3]));
+        if (r == 0)
+            orow[(size_t)(t0 + j) * Hv * DV] = os;
+    }
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void gdn_norm_gate_kernel(const float *__restrict__ o,
                                                             const bf16 *__restrict__ z, int zs,
@@ -1445,6 +1621,50 @@ extern "C" hipError_t k_gdn_scan(const float *q, const float *k, const float *v,
                        stream);
 }
 
+extern "C" int cujev_gdn_recur_chosen(const cujev_chunks *ck, int Hv, int has_S_out,
+                                      int has_conv_out) {
+    if (has_S_out || has_conv_out || ck->chunk_starts || ck->max_seg_chunks != 1 ||
+        ck->max_seg_len <= 0 || ck->max_seg_len > RC_MAXL || ck->num_segments <= 0)
+        return 0;
+    static int mode = -2;
+    if (mode == -2) {
+        const char *e = getenv("CUJEV_GDN_RECUR");
+        mode = e && *e == '0' ? 0 : e && *e == '1' ? 1 : -1;
+    }
+    if (mode >= 0)
+        return mode;
+    /* the token loop is latency-bound while there are at most about two
+     * workgroups per CU, each with few tokens */
+    return (long)ck->num_segments * Hv <= 256 && ck->max_seg_len <= RC_MAXL;
+}
+
+extern "C" hipError_t k_gdn_recur(const bf16_t *proj, int proj_stride, const float *conv_w,
+                                  const float *conv_in, const float *A_neg_exp,
+                                  const float *dt_bias, const cujev_chunks *ck, const float *S_in,
+                                  const float *norm_w, float eps, int Hk, int Hv, bf16_t *y,
+                                  const cujev_gdn_scratch *ws, int N, hipStream_t stream) {
+    if (N <= 0 || ck->num_segments <= 0)
+        return hipSuccess;
+    if (Hk <= 0 || Hv % Hk != 0 || proj_stride % 8 != 0 || ((uintptr_t)proj & 15) != 0 ||
+        ck->chunk_starts || ck->max_seg_chunks != 1 || ck->max_seg_len <= 0 ||
+        ck->max_seg_len > RC_MAXL)
+        return hipErrorInvalidValue;
+    const ConvSrc cv{(const bf16 *)proj, proj_stride, conv_w, conv_in, nullptr,
+                     A_neg_exp,          dt_bias,     N};
+    const int units = ck->num_segments * Hv;
+    hipLaunchKernelGGL(conv_in ? gdn_recur_kernel<true> : gdn_recur_kernel<false>,
+                       dim3((unsigned)(4 * units)), dim3(RC_THREADS), 0, stream, cv,
+                       ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, Hk, Hv, units, S_in, ws->O);
+    const int C = (2 * Hk + Hv) * DK;
+    const bf16_t *z = proj + C;
+    const int rows = N * Hv;
+    const bool zvec = proj_stride % 8 == 0 && ((uintptr_t)z & 15) == 0;
+    hipLaunchKernelGGL(zvec ? gdn_norm_gate_kernel<true> : gdn_norm_gate_kernel<false>,
+                       dim3((unsigned)CEIL_DIV(rows, 16)), dim3(256), 0, stream, ws->O,
+                       (const bf16 *)z, proj_stride, norm_w, eps, rows, Hv, (bf16 *)y);
+    return hipGetLastError();
+}
+
 extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const float *conv_w,
                                   const float *conv_in, float *conv_out, int seg0_len,
                                   const int32_t *own_base, const float *A_neg_exp,
@@ -1465,6 +1685,9 @@ extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const flo
                                seg0_len, C);
         return hipGetLastError();
     }
+    if (cujev_gdn_recur_chosen(ck, Hv, S_out != nullptr, conv_out != nullptr))
+        return k_gdn_recur(proj, proj_stride, conv_w, conv_in, A_neg_exp, dt_bias, ck, S_in,
+                           norm_w, eps, Hk, Hv, y, ws, N, stream);
     const ConvSrc cv{(const bf16 *)proj, proj_stride, conv_w, conv_in, own_base,
                      A_neg_exp,          dt_bias,     N};
     /* the conv tail rides along with phase B */

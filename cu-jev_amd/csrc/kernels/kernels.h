@@ -106,6 +106,7 @@ typedef struct cujev_chunks {
      * only for branches that all continue S_in with no final state written.
      * The segment arrays are then unused. */
     const uint64_t *chunk_starts;
+    int max_seg_len; /* longest segment in tokens (host-side); 0 = not known */
 } cujev_chunks;
 
 /* Scratch of the chunked scan. Per (chunk, v-head), written by the parallel
@@ -181,6 +182,24 @@ hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const float *conv_w,
                        const cujev_chunks *chunks, const float *S_in, float *S_out,
                        const float *norm_w, float eps, int Hk, int Hv, bf16_t *y,
                        const cujev_gdn_scratch *scratch, int N, hipStream_t stream);
+
+/* Few-token branches (eval: every segment continues S_in, none writes a
+ * final state or conv tail, no packed chunks, each at most
+ * CUJEV_GDN_RECUR_MAX_LEN tokens) can run the recurrence token by token in
+ * fp32 (the reference's own form) instead of the chunked scan: one kernel for
+ * conv, gates and recurrence, then the gated norm. Returns 1 when k_gdn_layer
+ * takes that path for these arguments (the engine keys its captured graphs
+ * on it). CUJEV_GDN_RECUR=0 never takes it, =1 whenever eligible; by default
+ * only while segments x heads x tokens stays within the latency-bound range. */
+#define CUJEV_GDN_RECUR_MAX_LEN 32
+int cujev_gdn_recur_chosen(const cujev_chunks *chunks, int Hv, int has_S_out, int has_conv_out);
+/* The token-by-token path on its own (the chunk table must describe one
+ * chunk per segment; max_seg_len as above). */
+hipError_t k_gdn_recur(const bf16_t *proj, int proj_stride, const float *conv_w,
+                       const float *conv_in, const float *A_neg_exp, const float *dt_bias,
+                       const cujev_chunks *chunks, const float *S_in, const float *norm_w,
+                       float eps, int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *scratch,
+                       int N, hipStream_t stream);
 
 /* ---- per-layer glue --------------------------------------------------------
  * x[N,H] fp32 residual = E[tokens] (bf16 table).  REF elementwise.cu:3-11. */

@@ -292,6 +292,26 @@ EXPORT int cujev_op_gdn_layer(const void *proj, int proj_stride, const float *co
                     "gdn_layer");
 }
 
+EXPORT int cujev_op_gdn_recur(const void *proj, int proj_stride, const float *conv_w,
+                              const float *conv_in, const float *A_neg_exp, const float *dt_bias,
+                              const int32_t *chunk_tok0, const int32_t *chunk_len,
+                              const int32_t *seg_chunk0, int num_segments, int max_seg_len,
+                              const float *S_in, const float *norm_w, float eps, int Hk, int Hv,
+                              int N, void *y, void *scratch, void *stream) {
+    if (num_segments < 0 || N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk || !scratch || !y ||
+        max_seg_len < 1 || max_seg_len > CUJEV_GDN_RECUR_MAX_LEN)
+        return fail(1, "gdn_recur: bad arguments");
+    if (proj_stride % 8 || ((uintptr_t)proj & 15))
+        return fail(1, "gdn_recur: projection rows must be 16-byte aligned");
+    cujev_chunks ck = {chunk_tok0, chunk_len, seg_chunk0, nullptr, num_segments,
+                       num_segments, 1, nullptr, max_seg_len};
+    cujev_gdn_scratch ws = cujev_gdn_scratch_carve(scratch, num_segments, Hv);
+    return launched(k_gdn_recur((const bf16_t *)proj, proj_stride, conv_w, conv_in, A_neg_exp,
+                                dt_bias, &ck, S_in, norm_w, eps, Hk, Hv, (bf16_t *)y, &ws, N,
+                                (hipStream_t)stream),
+                    "gdn_recur");
+}
+
 EXPORT size_t cujev_ops_gdn_scratch_bytes(int num_chunks, int Hv, int N) {
     return cujev_gdn_scratch_bytes(num_chunks, Hv, N);
 }

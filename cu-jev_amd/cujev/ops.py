@@ -42,6 +42,8 @@ _SIGS = {
     "cujev_op_gemm_small_tile": [_P, _I, _I, _P, _P],
     "cujev_op_gemm_wide": [_P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P],
     "cujev_op_add_rmsnorm": [_P, _P, _P, _I, _P, _P, _I, _I, _F, _P, _I, _P],
+    "cujev_op_gdn_recur": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _F, _I, _I, _I, _P,
+                           _P, _P],
     "cujev_op_gdn_layer": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P,
                            _P, _P, _F, _I, _I, _I, _P, _P, _P],
     "cujev_op_gdn_scan": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P,
@@ -242,6 +244,17 @@ def gdn_layer(proj, conv_w, conv_in, conv_out, seg0_len, own_base, A_neg_exp, dt
           _ptr(chunk_tok0), _ptr(chunk_len), chunk_tok0.shape[0], _ptr(seg_chunk0),
           _ptr(seg_nchunk), nseg, int(max_seg_chunks), _ptr(chunk_starts), _ptr(S_in),
           _ptr(S_out), _ptr(norm_w), float(eps), Hk, Hv, N, _ptr(y), _ptr(scratch), _stream())
+
+
+def gdn_recur(proj, conv_w, conv_in, A_neg_exp, dt_bias, chunk_tok0, chunk_len, seg_chunk0,
+              max_seg_len, S_in, norm_w, eps, Hk, Hv, y, scratch):
+    """The token-by-token fp32 path for eval branches (each <= 32 tokens, one
+    chunk per segment): conv, gates, recurrence from S_in, gated norm."""
+    N = proj.shape[0]
+    _call("cujev_op_gdn_recur", _ptr(proj), proj.stride(0), _ptr(conv_w), _ptr(conv_in),
+          _ptr(A_neg_exp), _ptr(dt_bias), _ptr(chunk_tok0), _ptr(chunk_len), _ptr(seg_chunk0),
+          seg_chunk0.shape[0], int(max_seg_len), _ptr(S_in), _ptr(norm_w), float(eps), Hk, Hv, N,
+          _ptr(y), _ptr(scratch), _stream())
 
 
 _gemm_ws = None

@@ -209,6 +209,22 @@ int cujev_op_gdn_layer(const void *proj, int proj_stride, const float *conv_w,
                        float *S_out, const float *norm_w, float eps, int Hk, int Hv, int N,
                        void *y, void *scratch, void *stream);
 
+/* No counterpart in the reference's kernel list; its semantics are the
+ * reference's recurrent scan (src/kernels/gdn.cu:111-182) for eval branches:
+ * cujev_op_gdn_layer's result for branches that each continue S_in with no
+ * final state or conv tail written, computed token by token in fp32. The
+ * chunk table must hold one chunk per segment (chunk_tok0 / chunk_len indexed
+ * through seg_chunk0), every segment at most max_seg_len <= 32 tokens; the
+ * scratch is cujev_ops_gdn_scratch_bytes(num_segments, Hv, N) bytes.
+ * cujev_op_gdn_layer itself never takes this path; the engine does for small
+ * evals. */
+int cujev_op_gdn_recur(const void *proj, int proj_stride, const float *conv_w,
+                       const float *conv_in, const float *A_neg_exp, const float *dt_bias,
+                       const int32_t *chunk_tok0, const int32_t *chunk_len,
+                       const int32_t *seg_chunk0, int num_segments, int max_seg_len,
+                       const float *S_in, const float *norm_w, float eps, int Hk, int Hv, int N,
+                       void *y, void *scratch, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

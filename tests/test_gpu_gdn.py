@@ -201,6 +201,57 @@ def test_gdn_one_chunk_branches(seg_lens):
         start += Ls
 
 
+def run_recur(o, L, proj, seg_lens, conv_in, S_in):
+    """The token-by-token branch path (cujev_op_gdn_recur) on one chunk per
+    segment."""
+    dev = "cuda"
+    N = proj.shape[0]
+    t = lambda a: torch.as_tensor(a).to(dev)
+    tok0, clen, seg0, _ = o.chunk_table(seg_lens)
+    assert len(tok0) == len(seg_lens)
+    scratch = torch.empty(o.gdn_scratch_bytes(len(seg_lens), L.Hv, N), dtype=torch.uint8,
+                          device=dev)
+    y = torch.full((N, L.Hv * DV), float("nan"), dtype=torch.bfloat16, device=dev)
+    o.gdn_recur(bf(proj).to(dev), t(L.conv_w), t(conv_in.astype(np.float32)), t(L.A_neg),
+                t(L.dt_bias), t(tok0), t(clen), t(seg0), max(seg_lens),
+                t(S_in.astype(np.float32)), t(L.norm_w), L.eps, L.Hk, L.Hv, y, scratch)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("seg_lens,Hk,Hv", [([1, 2, 3, 5, 16, 17, 31, 32], 2, 4),
+                                            ([7] * 19, 1, 4), ([20] * 4, 16, 32)])
+def test_gdn_recur_branches(seg_lens, Hk, Hv):
+    """Eval branches through the token-by-token fp32 path: each matches the
+    float64 oracle over [prefix ++ branch] (the layer output's own bf16
+    rounding and the gated norm's round trip are the error), and the chunked
+    path within the same bar. [20] * 4 at Hk 16 / Hv 32 is the config-4
+    eval shape, with config 2's gates."""
+    o = ops()
+    print(f"recur seg_lens={seg_lens} Hk={Hk} Hv={Hv}", flush=True)
+    L = Layer(21, Hk, Hv, config2=Hk == 16)
+    prefix = L.proj(90)
+    got_p = run_gpu(o, L, prefix, [90], write_state=True, fused=True)
+    br = L.proj(sum(seg_lens))
+    got = run_recur(o, L, br, seg_lens, got_p["tail"], got_p["S"])
+    assert np.isfinite(got).all()
+    chunked = run_gpu(o, L, br, seg_lens, conv_in=got_p["tail"], S_in=got_p["S"], fused=True)
+    assert rel_err(got, chunked["y"]) <= TOL
+    _, S0, tail0 = oracle_segment(L, prefix, None, None)
+    start, worst, refs = 0, 0.0, []
+    for Ls in seg_lens:
+        y_ref, _, _ = oracle_segment(L, br[start: start + Ls], tail0, S0)
+        refs.append(y_ref)
+        e = rel_err(got[start: start + Ls], y_ref)
+        worst = max(worst, e)
+        assert e <= TOL, (Ls, e)
+        start += Ls
+    ref = np.concatenate(refs)
+    print(f"recur: worst y {worst:.3e}, RMS {rms_rel(got, ref):.3e}; chunked RMS "
+          f"{rms_rel(chunked['y'], ref):.3e}")
+    assert rms_rel(got, ref) <= RMS_TOL
+
+
 @pytest.mark.parametrize("seg_lens", [[1, 2, 3, 5, 16, 37, 64, 20, 20, 20, 63, 1],
                                       [16] * 9, [64, 64, 1], [33, 31, 32, 32, 17]])
 def test_gdn_packed_branches(seg_lens):
