@@ -1349,6 +1349,7 @@ struct RecurSmem {
     float v[RC_MAXL][RC_COLS];
     bf16 x[RC_MAXL][RC_CH]; /* pre-conv rows of the segment's tokens */
     float g[RC_MAXL], beta[RC_MAXL];
+    float kq[RC_MAXL]; /* k_j . q_j */
 };
 
 /* sum over the 8 lanes l, l^8, ..., l^56 (lane bits 3..5) */
@@ -1425,45 +1426,68 @@ __global__ __launch_bounds__(RC_THREADS, 2) void gdn_recur_kernel(
             x3 = x2, x2 = x1, x1 = x0;
         }
     }
-    if (tid < RC_COLS) {
-        float x3 = tv[0], x2 = tv[1], x1 = tv[2];
-        for (int j = 0; j < L; j++) {
-            const float x0 = bf2f(sm.x[j][2 * DK + tid]);
+    if (tid < 4 * RC_COLS) { /* v: channel tid % 32, token quarter tid / 32 */
+        const int cc = tid & (RC_COLS - 1), per = (L + 3) >> 2;
+        const int j0 = (tid >> 5) * per, j1 = min(L, j0 + per);
+        auto xin = [&](int j) { /* input of token j, the tail before 0 */
+            return j >= 0 ? bf2f(sm.x[j][2 * DK + cc]) : tv[j + 3];
+        };
+        float x3 = xin(j0 - 3), x2 = xin(j0 - 2), x1 = xin(j0 - 1);
+        for (int j = j0; j < j1; j++) {
+            const float x0 = bf2f(sm.x[j][2 * DK + cc]);
             float y = fmaf(wv.x, x3, 0.f);
             y = fmaf(wv.y, x2, y);
             y = fmaf(wv.z, x1, y);
             y = fmaf(wv.w, x0, y);
-            sm.v[j][tid] = silu_f(y);
+            sm.v[j][cc] = silu_f(y);
             x3 = x2, x2 = x1, x1 = x0;
         }
     }
     lds_barrier();
-    /* ---- l2-norm of q and k rows (q also * 128^-1/2), 8 lanes a row ---- */
-    for (int base = 0; base < 2 * L; base += RC_THREADS / 8) {
-        const int row = base + (tid >> 3), part = tid & 7;
-        if (row < 2 * L) { /* whole 8-lane groups */
-            float *rp = (row < L ? sm.q[row] : sm.k[row - L]) + 16 * part;
-            float4 a[4];
-            float ss = 0.f;
+    /* ---- per token, 8 lanes: the l2-norms of q and k (q also * 128^-1/2)
+     * and k.q from the same registers ---- */
+    for (int base = 0; base < L; base += RC_THREADS / 8) {
+        const int j = base + (tid >> 3), part = tid & 7;
+        if (j < L) { /* whole 8-lane groups */
+            float *qp = sm.q[j] + 16 * part, *kp = sm.k[j] + 16 * part;
+            float4 a[4], b[4];
+            float sq = 0.f, sk = 0.f, d = 0.f;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                a[e] = *(const float4 *)(rp + 4 * e);
-                ss += a[e].x * a[e].x + a[e].y * a[e].y + a[e].z * a[e].z + a[e].w * a[e].w;
+                a[e] = *(const float4 *)(qp + 4 * e);
+                b[e] = *(const float4 *)(kp + 4 * e);
+                sq += a[e].x * a[e].x + a[e].y * a[e].y + a[e].z * a[e].z + a[e].w * a[e].w;
+                sk += b[e].x * b[e].x + b[e].y * b[e].y + b[e].z * b[e].z + b[e].w * b[e].w;
+                d += a[e].x * b[e].x + a[e].y * b[e].y + a[e].z * b[e].z + a[e].w * b[e].w;
             }
-            ss += dpp<0xB1>(ss);  /* lane ^ 1 */
-            ss += dpp<0x4E>(ss);  /* lane ^ 2 */
-            ss += dpp<0x141>(ss); /* the other quad of 8 */
-            const float inv = rsqrtf(ss + 1e-6f) * (row < L ? 0.08838834764831845f : 1.f);
+            sq += dpp<0xB1>(sq), sk += dpp<0xB1>(sk), d += dpp<0xB1>(d);    /* lane ^ 1 */
+            sq += dpp<0x4E>(sq), sk += dpp<0x4E>(sk), d += dpp<0x4E>(d);    /* lane ^ 2 */
+            sq += dpp<0x141>(sq), sk += dpp<0x141>(sk), d += dpp<0x141>(d); /* other quad */
+            const float iq = rsqrtf(sq + 1e-6f) * 0.08838834764831845f;
+            const float ik = rsqrtf(sk + 1e-6f);
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                *(float4 *)(rp + 4 * e) =
-                    make_float4(a[e].x * inv, a[e].y * inv, a[e].z * inv, a[e].w * inv);
+            for (int e = 0; e < 4; e++) {
+                *(float4 *)(qp + 4 * e) =
+                    make_float4(a[e].x * iq, a[e].y * iq, a[e].z * iq, a[e].w * iq);
+                *(float4 *)(kp + 4 * e) =
+                    make_float4(b[e].x * ik, b[e].y * ik, b[e].z * ik, b[e].w * ik);
+            }
+            if (part == 0)
+                sm.kq[j] = d * iq * ik;
         }
     }
     lds_barrier();
 
-    /* ---- the recurrence: no barrier, the waves run free ---- */
+    /* ---- the recurrence: no barrier, the waves run free ----
+     * S is kept as sigma * St (sigma = the product of the decays so far), so
+     * a token costs three FMAs per state element: k.St and q.St in one pass,
+     * then St += k (v' / sigma). With kS = sigma k.St and qS = sigma q.St of
+     * the previous state,
+     *   v' = beta (v - e^g kS),  o = e^g qS + v' (k.q)   (= S_new^T q).
+     * When sigma would drop below 2^-40 the token applies its decay to St
+     * directly and sigma restarts at 1. */
     float *orow = o + (size_t)hv * DV + RC_COLS * cb + colw;
+    float sigma = 1.f;
     for (int j = 0; j < L; j++) {
         float kq[16], qq[16];
 #pragma unroll
@@ -1474,21 +1498,31 @@ __global__ __launch_bounds__(RC_THREADS, 2) void gdn_recur_kernel(
             qq[4 * e] = b.x, qq[4 * e + 1] = b.y, qq[4 * e + 2] = b.z, qq[4 * e + 3] = b.w;
         }
         const float eg = fast_exp(sm.g[j]);
-        float p[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < 16; i++)
-            p[i & 3] = fmaf(kq[i], S[i], p[i & 3]);
-        const float kS = sum_lanes8((p[0] + p[1]) + (p[2] + p[3]));
-        const float vn = sm.beta[j] * (sm.v[j][colw] - eg * kS);
-        float u[4] = {0.f, 0.f, 0.f, 0.f};
+        float pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            S[i] = fmaf(eg, S[i], kq[i] * vn);
-            u[i & 3] = fmaf(qq[i], S[i], u[i & 3]);
+            pk[i & 3] = fmaf(kq[i], S[i], pk[i & 3]);
+            pq[i & 3] = fmaf(qq[i], S[i], pq[i & 3]);
         }
-        const float os = sum_lanes8((u[0] + u[1]) + (u[2] + u[3]));
+        const float kS = sigma * sum_lanes8((pk[0] + pk[1]) + (pk[2] + pk[3]));
+        const float qS = sigma * sum_lanes8((pq[0] + pq[1]) + (pq[2] + pq[3]));
+        const float vn = sm.beta[j] * (sm.v[j][colw] - eg * kS);
+        const float os = fmaf(eg, qS, vn * sm.kq[j]);
         if (r == 0)
             orow[(size_t)(t0 + j) * Hv * DV] = os;
+        const float sn = sigma * eg;
+        if (sn < 0x1p-40f) { /* wave-uniform: fold the decay into St */
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                S[i] = fmaf(sn, S[i], kq[i] * vn);
+            sigma = 1.f;
+        } else {
+            const float w = vn * __builtin_amdgcn_rcpf(sn);
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                S[i] = fmaf(kq[i], w, S[i]);
+            sigma = sn;
+        }
     }
 }
 
