@@ -133,10 +133,57 @@ def run_e2e(ckpt, steps, warmup, wl="config4", seed=0, full_logits=True):
                 first_out=first_out, first_full=first_full, info=info, checks=checks)
 
 
+# The reference's own benchmark shapes for the 4B model (tools/bench.c:41-74;
+# its published RTX 5090 rows, README.md:233-234): prefill P tokens, then one
+# eval of B branches x L tokens with C candidates each, timed by the
+# library's own GPU timing (cujev_last_timing), decisions/s = B / eval time.
+REF_BENCH_SHAPES = [
+    {"P": 1024, "B": 16, "L": 40, "C": 8,
+     "rtx5090": {"prefill_ms": 60.0, "eval_ms": 37.0, "decisions_per_s": 430}},
+    {"P": 8192, "B": 64, "L": 40, "C": 8,
+     "rtx5090": {"prefill_ms": 550.0, "eval_ms": 185.0, "decisions_per_s": 350}},
+]
+
+
+def run_ref_shapes(ckpt, iters=5):
+    """tools/bench.c's method on this engine: deterministic token ids
+    1000 + (7919 i mod 50000), candidates 32..32+C-1, one warm-up, then the
+    mean of `iters` prefill and eval timings."""
+    from cujev import Branch, Engine
+    out = []
+    eng = Engine(ckpt, max_state_tokens=8192, max_branch_tokens=4096, max_branches=256,
+                 max_candidates=256)
+    try:
+        for sh in REF_BENCH_SHAPES:
+            P, B, L, C = sh["P"], sh["B"], sh["L"], sh["C"]
+            tok = [1000 + (i * 7919) % 50000 for i in range(P + B * L)]
+            cands = list(range(32, 32 + C))
+            brs = [Branch(tok[P + b * L: P + (b + 1) * L], cands) for b in range(B)]
+            eng.prefill(tok[:P])
+            eng.eval(brs)
+            pre = ev = 0.0
+            for _ in range(iters):
+                eng.prefill(tok[:P])
+                pre += eng.last_timing().prefill_ms
+                eng.eval(brs)
+                ev += eng.last_timing().eval_ms
+            pre, ev = pre / iters, ev / iters
+            out.append({"state_tokens": P, "branches": B, "branch_tokens": L, "candidates": C,
+                        "prefill_ms": round(pre, 3), "prefill_tok_per_s": round(P / pre * 1e3),
+                        "eval_ms": round(ev, 3), "decisions_per_s": round(B / ev * 1e3, 1),
+                        "iters": iters, "reference_rtx5090": sh["rtx5090"]})
+    finally:
+        eng.close()
+    return out
+
+
 def e2e_child(a):
     """--e2e-child: the request loop without torch in the process; prints one
     JSON line, the full-vocabulary logits go to a .npy file."""
     assert "torch" not in sys.modules
+    if a.workload == "ref_shapes":
+        print(json.dumps({"ref_shapes": run_ref_shapes(a.ckpt)}), flush=True)
+        return
     r = run_e2e(a.ckpt, a.steps, a.warmup, wl=a.workload)
     if r["first_full"] is not None and a.workload == "config4":
         np.save(a.full_out, np.asarray(r["first_full"], np.float32), allow_pickle=False)
@@ -307,6 +354,8 @@ def main():
     ap.add_argument("--config5-steps", type=int, default=5)
     ap.add_argument("--workload", default="config4", help=argparse.SUPPRESS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ref-shapes", action="store_true",
+                    help="skip the reference's published cujev-bench shapes")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the kernel roofline entries (no request loop, no CPU baseline)")
@@ -364,6 +413,8 @@ def main():
     res["e2e_checks"] = e2e["checks"]
     if not a.no_config5:
         res["config5"] = config5_line(a)
+    if not a.no_ref_shapes:
+        res["reference_bench_shapes"] = ref_shapes_line(ckpt)
     if not a.no_kernels:
         res.update(kernel_rooflines())
     if not a.no_cpu_baseline:
@@ -403,6 +454,26 @@ def config5_line(a):
             "weights_gib": round(r["info"]["weight_gib"], 2),
             "workspace_gib": round(r["info"]["workspace_gib"], 2),
             "cpu_baseline": None}
+
+
+def ref_shapes_line(ckpt):
+    """The reference benchmark's 4B shapes on the same synthetic checkpoint,
+    in the torch-free child; the RTX 5090 figures are the reference's
+    published numbers on other hardware, for context only."""
+    import subprocess
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--e2e-child", "--ckpt", ckpt,
+           "--workload", "ref_shapes"]
+    p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=sys.stderr, text=True)
+    if p.returncode != 0:
+        raise SystemExit(f"reference-shape child failed with status {p.returncode}")
+    rows = json.loads(p.stdout.strip().splitlines()[-1])["ref_shapes"]
+    for r in rows:
+        log(f"cujev-bench shape P={r['state_tokens']} {r['branches']}x{r['branch_tokens']}: "
+            f"prefill {r['prefill_ms']:.2f} ms, eval {r['eval_ms']:.2f} ms, "
+            f"{r['decisions_per_s']:.0f} decisions/s")
+    return {"method": "tools/bench.c:41-74 (prefill then one eval, cujev_last_timing GPU ms, "
+                      "decisions/s = branches / eval ms), 4B shapes of README.md:233-234",
+            "rows": rows}
 
 
 if __name__ == "__main__":
