@@ -253,6 +253,23 @@ def test_graph_replays_match_eager(ckpt):
         ref.close()
 
 
+def test_graph_key_tells_recurrent_from_chunked(engine):
+    """Two evals of one shape (N = 40 tokens, 2 branches, 2 chunks): branches
+    of 20 + 20 tokens take the token-by-token GDN path, 5 + 35 the chunked
+    one (35 > 32). A graph captured for one must not be replayed for the
+    other: every call equals the first, eager call of its branch set."""
+    rng = np.random.default_rng(37)
+    prefix = rand_ids(rng, 50)
+    A = [Branch(rand_ids(rng, 20), rand_ids(rng, 4)) for _ in range(2)]
+    B = [Branch(rand_ids(rng, 5), rand_ids(rng, 4)), Branch(rand_ids(rng, 35), rand_ids(rng, 4))]
+    engine.prefill(prefix)
+    first_a, first_b = engine.eval(A), engine.eval(B)
+    for _ in range(3):
+        for got, ref in ((engine.eval(A), first_a), (engine.eval(B), first_b)):
+            for x, y in zip(got, ref):
+                np.testing.assert_array_equal(x, y)
+
+
 def test_graph_key_tells_packed_from_unpacked(engine, monkeypatch):
     """Branches of 33-64 tokens fill one GDN chunk each whether or not the
     chunk table is packed, so both tables have the same chunk count but lay
