@@ -1004,30 +1004,58 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
         S[r] += 0.f;
     const int c0 = seg_chunk0[seg], nc = seg_nchunk[seg];
 
-    auto load = [&](int ch, BOps &op) {
+    /* The operand set of a chunk in four parts, so that the next chunk's
+     * loads can be issued piecewise between this chunk's MFMAs: issued as one
+     * burst, the texture unit's time for all of them (about 1.4k cycles per
+     * CU for 88 KiB) would be spent before the barrier that starts the
+     * dependent chain, and added to it. */
+    struct OpPtr {
+        const bf16x8 *w, *qg, *kg, *qk;
+        const float4 *u;
+        const float *gl;
+    };
+    auto ptrs = [&](int ch) {
         const size_t cb = (size_t)ch * Hv + hv;
-        const bf16x8 *w = Wi + cb * 1024 + wave * 256 + lane;
-        const bf16x8 *qg = Qgi + cb * 1024 + wave * 256 + lane;
-        const bf16x8 *kg = KgTi + cb * 2048 + wave * 256 + lane;
-        const bf16x8 *qk = QKi + cb * 1024 + wave * 128 + lane;
+        OpPtr p;
+        p.w = Wi + cb * 1024 + wave * 256 + lane;
+        p.qg = Qgi + cb * 1024 + wave * 256 + lane;
+        p.kg = KgTi + cb * 2048 + wave * 256 + lane;
+        p.qk = QKi + cb * 1024 + wave * 128 + lane;
+        p.u = Ui + (cb * 1024 + (cbk * 4 + wave) * 64 + lane) * 2;
+        p.gl = Gli + cb * 64 + lane;
+        return p;
+    };
+    auto load_part = [&](const OpPtr &p, BOps &op, int part) {
+        if (part == 0) {
+            op.gl = p.gl[0];
+            op.u[0] = p.u[0];
+            op.u[1] = p.u[1];
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            op.w[s] = w[64 * s];
-            op.kgh[s] = kg[64 * s];
-            op.kgl[s] = kg[1024 + 64 * s];
+            for (int s = 0; s < 4; s++)
+                op.w[s] = p.w[64 * s];
+        } else if (part == 1) {
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+                op.qg[s] = p.qg[64 * s];
+        } else if (part == 2) {
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                op.kgh[s] = p.kg[64 * s];
+                op.kgl[s] = p.kg[1024 + 64 * s];
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                op.qkh[s] = p.qk[64 * s];
+                op.qkl[s] = p.qk[512 + 64 * s];
+            }
         }
-        const float4 *up = Ui + (cb * 1024 + (cbk * 4 + wave) * 64 + lane) * 2;
-        op.u[0] = up[0];
-        op.u[1] = up[1];
-        op.gl = Gli[cb * 64 + lane];
+    };
+    auto load = [&](int ch, BOps &op) {
+        const OpPtr p = ptrs(ch);
 #pragma unroll
-        for (int s = 0; s < 4; s++)
-            op.qg[s] = qg[64 * s];
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
-            op.qkh[s] = qk[64 * s];
-            op.qkl[s] = qk[512 + 64 * s];
-        }
+        for (int part = 0; part < 4; part++)
+            load_part(p, op, part);
     };
 
     /* A segment's chunks are consecutive 64-token slices: token offsets
@@ -1036,9 +1064,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
     const int tok_seg = nc > 0 ? chunk_tok0[c0] : 0;
     const int len_last = nc > 0 ? chunk_len[c0 + nc - 1] : 0;
 
-    auto step = [&](int ch, const BOps &op) {
+    /* One chunk with operand set op; the set of chunk chn goes into nx in
+     * four parts between the MFMA groups (pinned there by scheduling
+     * barriers). */
+    auto step = [&](int ch, const BOps &op, int chn, BOps &nx) {
         const int ci = ch - c0;
         const int t0 = tok_seg + CH * ci, L = ci + 1 < nc ? CH : len_last;
+        const OpPtr np = ptrs(chn);
         const float dec = fast_exp(op.gl);
 #pragma unroll
         for (int j = 0; j < 4; j++)
@@ -1058,11 +1090,17 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
 #pragma unroll
             for (int jb = 0; jb < 2; jb++)
                 V[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.w[s], sb[s][jb], V[jb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_part(np, nx, 0);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 4; s++)
 #pragma unroll
             for (int jb = 0; jb < 2; jb++)
                 O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qg[s], sb[s][jb], O[jb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_part(np, nx, 1);
+        __builtin_amdgcn_sched_barrier(0);
         const float uf[8] = {op.u[0].x, op.u[0].y, op.u[0].z, op.u[0].w,
                              op.u[1].x, op.u[1].y, op.u[1].z, op.u[1].w};
 #pragma unroll
@@ -1095,6 +1133,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
             S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgh[s], vbl[s], S, 0, 0, 0);
             S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgl[s], vbh[s], S, 0, 0, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        load_part(np, nx, 2);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 2; s++)
 #pragma unroll
@@ -1103,6 +1144,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
                 O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qkh[s], v2l[s][jb], O[jb], 0, 0, 0);
                 O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qkl[s], v2h[s][jb], O[jb], 0, 0, 0);
             }
+        __builtin_amdgcn_sched_barrier(0);
+        load_part(np, nx, 3);
+        __builtin_amdgcn_sched_barrier(0);
         /* O (fp32) through this wave's LDS tile: 32-byte stores, 128 bytes a row */
 #pragma unroll
         for (int jb = 0; jb < 2; jb++)
@@ -1129,12 +1173,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
         BOps A, B;
         load(cl(0), A);
         for (int ci = 0; ci < nc; ci += 2) {
-            load(cl(ci + 1), B);
-            step(c0 + ci, A);
+            step(c0 + ci, A, cl(ci + 1), B);
             if (ci + 1 >= nc)
                 break;
-            load(cl(ci + 2), A);
-            step(c0 + ci + 1, B);
+            step(c0 + ci + 1, B, cl(ci + 2), A);
         }
     }
     if (S_out && seg == 0) {
