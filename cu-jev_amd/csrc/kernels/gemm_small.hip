@@ -16,8 +16,9 @@
  *    [M][K] rows (16 rows x 64 bytes per instruction) runs at two thirds of
  *    that rate.
  *  - X (tiny, L2-resident) goes to an LDS ring by buffer DMA, the same three
- *    chunks ahead, and is shared by the four waves. A fifth wave issues all
- *    of those DMAs and waits for them before each step's barrier: an LDS
+ *    chunks ahead, and is shared by the computing waves. One more wave
+ *    issues all of those DMAs and waits for them before each step's
+ *    barrier: an LDS
  *    read completes only after every buffer_load ... lds its own wave issued
  *    earlier has landed, so DMAs issued by the computing waves would hold
  *    their B-operand reads behind each prefetch.
@@ -25,15 +26,23 @@
  *    bytes of its W row (k = 64j + 16(l/16) + 0..15); the two MFMAs of the
  *    step take the halves, and the B fragments are read from LDS with the
  *    same k assignment, so the product is the plain dot product.
- *  - Short M (the 2560-wide outputs) splits K over blockIdx.y. Splits write
- *    fp32 partials P[split][N][M] that the consumer (the residual add +
- *    RMSNorm) sums in a fixed order: results are deterministic, and the sum
- *    is rounded to bf16 like a bf16-output GEMM.
+ *  - What sets the time is each CU's share of the bytes it requests: its
+ *    weight rows plus a copy of X for its K range (at N = 80, 400 KiB for a
+ *    2560-wide K, as much as the rows of a 64-row workgroup). A CU moves
+ *    about 40 GB/s of such requests, so the grid is one workgroup per CU at
+ *    most: two on one CU double its share and the kernel's time.
+ *  - Short M (the 2560-wide outputs) splits K over blockIdx.y, as many ways
+ *    as fill the CUs (the splits' chunk counts may differ by one). Splits
+ *    write fp32 partials P[split][N][M] that the consumer (the residual add
+ *    + RMSNorm) sums in a fixed order: results are deterministic, and the
+ *    sum is rounded to bf16 like a bf16-output GEMM.
  *  - GATED=true is the fused gate|up projection (W rows [gate I | up I]):
- *    a workgroup takes 32 gate rows and the same 32 up rows (waves 0-1 and
- *    2-3), the up accumulators cross to the gate waves through LDS, and the
- *    output is act = bf16(silu(bf16 gate) * bf16 up) [N][I] directly, the
- *    rounding points of a bf16 GEMM followed by the activation pass.
+ *    a workgroup takes 16 H gate rows and the same up rows (H = 2 with 4
+ *    computing waves; H = 3 with 6 when 32-row halves would need more than
+ *    256 workgroups), the up accumulators cross to the gate waves through
+ *    LDS, and the output is act = bf16(silu(bf16 gate) * bf16 up) [N][I]
+ *    directly, the rounding points of a bf16 GEMM followed by the
+ *    activation pass.
  * All loads are unconditional (indices clamped into range): a load skipped
  * on one path would make the next use wait for every load in flight. */
 #include "common.h"
@@ -42,7 +51,7 @@
 namespace CUJEV_KNS {
 namespace {
 
-constexpr int SG_BM = 64;  /* W rows per workgroup */
+constexpr int SG_BM = 64;  /* W rows per workgroup (not gated) */
 constexpr int SG_KC = 128; /* K per chunk          */
 constexpr int SG_NS = 4;   /* pipeline depth: chunk c + 3 loads while c computes */
 
@@ -79,13 +88,14 @@ DEV bf16x8 sg_lds16(const unsigned char *base, uint32_t off) {
         (__attribute__((address_space(3))) const unsigned char *)base + off);
 }
 
-constexpr int SG_THREADS = 320; /* 4 computing waves + the X loader wave */
-
-template <int NB, bool GATED, bool PART>
-__global__ __launch_bounds__(SG_THREADS, 2) void gemm_small_kernel(const bf16 *__restrict__ X, int ldx,
-                                                            const bf16 *__restrict__ W, int N,
-                                                            int K, int KS, bf16 *__restrict__ Y,
-                                                            int ldy, float *__restrict__ P, int M) {
+/* CW computing waves (4, or 6 for the gated projection's 48 + 48 rows) and
+ * the X loader wave */
+template <int NB, bool GATED, bool PART, int CW>
+__global__ __launch_bounds__((CW + 1) * 64, 2) void gemm_small_kernel(
+    const bf16 *__restrict__ X, int ldx, const bf16 *__restrict__ W, int N, int K,
+    bf16 *__restrict__ Y, int ldy, float *__restrict__ P, int M) {
+    static_assert(CW == 4 || (GATED && CW == 6), "4 computing waves, or 6 when gated");
+    constexpr int H = CW / 2; /* gated: gate (and up) row groups per workgroup */
     /* X ring: SG_NS stages of NB*16 token rows x 128 k, rows of 256 bytes
      * with the 16-byte slots XOR-swizzled by (row & 15) */
     constexpr int XSTAGE = NB * 16 * 256;
@@ -93,10 +103,12 @@ __global__ __launch_bounds__(SG_THREADS, 2) void gemm_small_kernel(const bf16 *_
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, c16 = lane & 15;
-    const int split = blockIdx.y;
-    const int kb = split * KS, nch = KS / SG_KC;
+    /* split s of S takes chunks [s C / S, (s+1) C / S) of the C = K / 128 */
+    const int split = blockIdx.y, nsplit = gridDim.y, ctot = K / SG_KC;
+    const int cb0 = split * ctot / nsplit, nch = (split + 1) * ctot / nsplit - cb0;
+    const int kb = cb0 * SG_KC;
     /* this wave's first W row (GATED: M = 2I, 32 gate rows + the same 32 up rows) */
-    const int wr0 = GATED ? blockIdx.x * 32 + 16 * (wave & 1) + (wave >> 1) * (M / 2)
+    const int wr0 = GATED ? blockIdx.x * 16 * H + 16 * (wave % H) + (wave / H) * (M / 2)
                           : blockIdx.x * SG_BM + 16 * wave;
 
     /* tiled W: block (chunk, row group wr0/16) of 2048 elements, chunk-major
@@ -112,7 +124,7 @@ __global__ __launch_bounds__(SG_THREADS, 2) void gemm_small_kernel(const bf16 *_
     };
     /* the number of steps (one barrier each), rounds of 4 */
     const int nsteps = (nch + 3) / 4 * 4;
-    if (wave == 4) {
+    if (wave == CW) {
         /* X loader. A chunk -> LDS by buffer DMA: instruction i fills token
          * rows 4i + 0..3; lane l lands on slot l%16 of row 4i + l/16 and
          * fetches the chunk's 16-byte piece (l%16) ^ (row & 15). Rows >= N
@@ -197,17 +209,17 @@ __global__ __launch_bounds__(SG_THREADS, 2) void gemm_small_kernel(const bf16 *_
 
     /* acc[nb]: token 16 nb + c16, rows wr0 + 4q .. +3 */
     if constexpr (GATED) {
-        /* up waves (2, 3) hand their accumulators to the gate waves (0, 1) */
+        /* up waves (H..CW-1) hand their accumulators to the gate waves */
         lds_barrier();
-        floatx4 *xch = (floatx4 *)xs; /* [2][NB][64] */
-        if (wave >= 2) {
+        floatx4 *xch = (floatx4 *)xs; /* [H][NB][64] */
+        if (wave >= H) {
 #pragma unroll
             for (int nb = 0; nb < NB; nb++)
-                xch[((wave - 2) * NB + nb) * 64 + lane] = acc[nb];
+                xch[((wave - H) * NB + nb) * 64 + lane] = acc[nb];
         }
         lds_barrier();
-        if (wave < 2) {
-            const int m = blockIdx.x * 32 + 16 * wave + 4 * q;
+        if (wave < H) {
+            const int m = blockIdx.x * 16 * H + 16 * wave + 4 * q;
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) {
                 const int n = 16 * nb + c16;
@@ -259,13 +271,13 @@ __global__ __launch_bounds__(256) void gemm_small_tile_kernel(const bf16 *__rest
     *(bf16x8 *)(Wt + piece * 8) = ldg8(W + (size_t)row * K + k);
 }
 
-template <bool GATED, bool PART>
+template <bool GATED, bool PART, int CW>
 hipError_t launch_nb(int NB, dim3 grid, hipStream_t s, const bf16 *X, int ldx, const bf16 *W,
-                     int N, int K, int KS, bf16 *Y, int ldy, float *P, int M) {
+                     int N, int K, bf16 *Y, int ldy, float *P, int M) {
 #define CUJEV_SG_CASE(nb)                                                                    \
     case nb:                                                                                 \
-        hipLaunchKernelGGL((gemm_small_kernel<nb, GATED, PART>), grid, dim3(SG_THREADS), 0, s, X, ldx, \
-                           W, N, K, KS, Y, ldy, P, M);                                        \
+        hipLaunchKernelGGL((gemm_small_kernel<nb, GATED, PART, CW>), grid,                     \
+                           dim3((CW + 1) * 64), 0, s, X, ldx, W, N, K, Y, ldy, P, M);          \
         break;
     switch (NB) {
         CUJEV_SG_CASE(1)
@@ -289,12 +301,10 @@ extern "C" int cujev_gemm_small_splits(int M, int K) {
     if (M <= 0 || K <= 0 || M % SG_BM || K % SG_KC)
         return 0;
     const int rowblocks = M / SG_BM, chunks = K / SG_KC;
+    /* about one workgroup per CU; the splits' chunk counts may differ by one */
     int s = (256 + rowblocks / 2) / rowblocks;
     s = s < 1 ? 1 : s > chunks ? chunks : s;
-    s = s > CUJEV_GEMM_SMALL_MAX_SPLITS ? CUJEV_GEMM_SMALL_MAX_SPLITS : s;
-    while (chunks % s)
-        s--;
-    return s;
+    return s > CUJEV_GEMM_SMALL_MAX_SPLITS ? CUJEV_GEMM_SMALL_MAX_SPLITS : s;
 }
 
 extern "C" hipError_t k_gemm_small_tile(const bf16_t *W, int M, int K, bf16_t *Wt,
@@ -313,16 +323,24 @@ extern "C" hipError_t k_gemm_small(const bf16_t *X, int ldx, const bf16_t *W, in
     if (N <= 0)
         return hipSuccess;
     if (N > CUJEV_GEMM_SMALL_MAX_N || M % SG_BM || K % SG_KC || splits < 1 ||
-        (K / SG_KC) % splits || (splits > 1 && (!P || gated)) || (splits == 1 && !Y))
+        splits > K / SG_KC || (splits > 1 && (!P || gated)) || (splits == 1 && !Y))
         return hipErrorInvalidValue;
-    const int NB = (N + 15) / 16, KS = K / splits;
-    const dim3 grid((unsigned)(M / SG_BM), (unsigned)splits);
+    const int NB = (N + 15) / 16;
     const bf16 *x = (const bf16 *)X, *w = (const bf16 *)W;
     if (splits > 1)
-        return launch_nb<false, true>(NB, grid, stream, x, ldx, w, N, K, KS, nullptr, 0, P, M);
-    if (gated)
-        return launch_nb<true, false>(NB, grid, stream, x, ldx, w, N, K, KS, (bf16 *)Y, ldy,
-                                      nullptr, M);
-    return launch_nb<false, false>(NB, grid, stream, x, ldx, w, N, K, KS, (bf16 *)Y, ldy, nullptr,
-                                   M);
+        return launch_nb<false, true, 4>(NB, dim3((unsigned)(M / SG_BM), (unsigned)splits), stream,
+                                         x, ldx, w, N, K, nullptr, 0, P, M);
+    if (gated) {
+        /* More than one workgroup per CU (each streams its own copy of X as
+         * well as its rows) would double some CUs' share: past 256
+         * workgroups of 32 + 32 rows, take 48 + 48 when that divides. */
+        const int I = M / 2;
+        if (I / 32 > 256 && I % 48 == 0)
+            return launch_nb<true, false, 6>(NB, dim3((unsigned)(I / 48)), stream, x, ldx, w, N, K,
+                                             (bf16 *)Y, ldy, nullptr, M);
+        return launch_nb<true, false, 4>(NB, dim3((unsigned)(I / 32)), stream, x, ldx, w, N, K,
+                                         (bf16 *)Y, ldy, nullptr, M);
+    }
+    return launch_nb<false, false, 4>(NB, dim3((unsigned)(M / SG_BM)), stream, x, ldx, w, N, K,
+                                      (bf16 *)Y, ldy, nullptr, M);
 }

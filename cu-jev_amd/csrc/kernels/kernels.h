@@ -229,8 +229,9 @@ hipError_t k_readout(const bf16_t *h, const bf16_t *E, const int32_t *cand, cons
  * Y[N, M] = X[N, K] . W[M, K]^T for N <= CUJEV_GEMM_SMALL_MAX_N, M % 64 == 0,
  * K % 128 == 0, X rows of stride ldx, W given in the tiled layout that
  * k_gemm_small_tile writes (same size as W). splits == 1 writes bf16 Y (row stride
- * ldy); splits > 1 (K / 128 divisible by splits) writes fp32 partial sums
- * P[splits][N][M] instead, to be summed by the consumer in split order.
+ * ldy); 1 < splits <= K / 128 writes fp32 partial sums P[splits][N][M]
+ * instead (split s sums the 128-wide chunks [s C / splits, (s+1) C /
+ * splits) of the C = K / 128), to be summed by the consumer in split order.
  * gated (splits == 1): W is the fused [gate I | up I] (M = 2I) and Y gets
  * act[N][I] = bf16(silu(bf16 gate) * bf16 up). */
 #define CUJEV_GEMM_SMALL_MAX_N 96 /* 6 token blocks of 16: register budget without spills */

@@ -54,8 +54,9 @@ int cujev_op_gemm_tune(const void *X, const void *W, void *Y, int f32out, int N,
  * M % 64 == 0, K % 128 == 0, X rows of stride ldx, bf16 in, fp32
  * accumulation, weights streamed once by a hand-written kernel.
  *   splits == 1: bf16 Y, row stride ldy.
- *   splits > 1 (K/128 divisible by splits, at most 8): fp32 partial sums
- *     P[splits][N][M] (no Y); sum them in split order (cujev_op_add_rmsnorm).
+ *   1 < splits <= min(8, K/128): fp32 partial sums P[splits][N][M] (no Y); split
+ *     s sums the 128-wide K chunks [s C / splits, (s+1) C / splits) of the
+ *     C = K/128; sum them in split order (cujev_op_add_rmsnorm).
  *   gated (splits == 1): W is the fused [gate I | up I] weight (M = 2I) and
  *     Y receives act[N][I] = bf16(silu(bf16 gate) * bf16 up), which is the
  *     reference's GEMM + silu_mul pair (src/kernels/elementwise.cu:42-54). */

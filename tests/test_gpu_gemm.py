@@ -50,7 +50,10 @@ def test_gemm_small_matches_fp32(N, M, K):
     assert e <= TOL
 
 
-@pytest.mark.parametrize("N,I,H", [(80, 9216, 2560), (5, 128, 256), (96, 512, 640)])
+# 9216 and 12288 (the 4B and 9B widths) take the 48 + 48-row workgroups;
+# 8224 would need 257 workgroups of 32 + 32 rows but does not divide by 48
+@pytest.mark.parametrize("N,I,H", [(80, 9216, 2560), (5, 128, 256), (96, 512, 640),
+                                   (80, 12288, 4096), (7, 8224, 256)])
 def test_gemm_small_gated_is_silu_mul(N, I, H):
     o = ops()
     print(f"gated N={N} I={I} H={H}", flush=True)
@@ -105,6 +108,28 @@ def test_split_partials_feed_add_rmsnorm(N, H, K):
         o.add_rmsnorm(x2, w, out2, 1e-6, yp=P, splits=sp)
         torch.cuda.synchronize()
         assert torch.equal(out, out2) and torch.equal(x, x2)
+
+
+@pytest.mark.parametrize("N,M,K,splits", [(80, 2560, 4096, 6), (33, 640, 1024, 3),
+                                          (80, 2560, 2560, 7)])
+def test_split_ranges(N, M, K, splits):
+    """Split s holds the product over the 128-wide K chunks [s C / S,
+    (s+1) C / S) of the C = K / 128, so ranges may differ by one chunk."""
+    o = ops()
+    print(f"split ranges N={N} M={M} K={K} splits={splits}", flush=True)
+    X = rand_bf16(N, K, seed=12)
+    W = rand_bf16(M, K, seed=13, scale=0.02)
+    P = torch.full((splits, N, M), float("nan"), dtype=torch.float32, device="cuda")
+    o.gemm_small(X, o.gemm_small_tile(W), P=P, splits=splits)
+    torch.cuda.synchronize()
+    C = K // 128
+    worst = 0.0
+    for s in range(splits):
+        k0, k1 = 128 * (s * C // splits), 128 * ((s + 1) * C // splits)
+        ref = X[:, k0:k1].float() @ W[:, k0:k1].float().t()
+        worst = max(worst, rel(P[s], ref))
+    print(f"worst split rel err {worst:.3e}")
+    assert worst <= 1e-4
 
 
 def tile_reference(W):
