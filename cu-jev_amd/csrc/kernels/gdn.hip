@@ -928,30 +928,44 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
 /* phase B: the state recurrence over chunks                                */
 /* ---------------------------------------------------------------------- */
 /* The columns of S evolve independently, so a (segment, v-head) is spread
- * over NCB workgroups of 32 state columns each, and inside a workgroup the
- * four waves split rows: wave w holds S rows 32w..32w+31 (fp32, one 32x32
- * accumulator) and chunk tokens 16w..16w+15. Per chunk:
- *   S (bf16) -> LDS as S^T; barrier
- *   V'_w = U_w - W_w S,  O_w = (Q e^G)_w S          (16x16x32, 16 MFMAs)
- *   V'_w as hi + lo (bf16) -> LDS as V'^T; barrier
- *   S_w = e^{G_last} S_w + (K e^{G_last-G})^T_w V'  (32x32x16; hi.hi,
- *                                                    hi.lo, lo.hi: 12 MFMAs)
- *   O_w += QKm_w V'                                  (16x16x32, likewise 12)
- *   O (fp32) out through a per-wave LDS tile.
+ * over NCB workgroups of 32 state columns each. A workgroup has two sets of
+ * four waves, one of each per SIMD, which meet at two barriers per chunk:
+ *   chain wave w (S rows 32w..32w+31 in one fp32 32x32 accumulator, chunk
+ *   tokens 16w..16w+15):
+ *     S (bf16) -> LDS as S^T;                                   barrier 1
+ *     V'_w = U_w - W_w S (16x16x32, 8 MFMAs), as hi + lo (bf16)
+ *       -> LDS as V'^T;                                         barrier 2
+ *     S_w = e^{G_last} S_w + (K e^{G_last-G})^T_w V' (32x32x16; hi.hi,
+ *       hi.lo, lo.hi: 12 MFMAs)
+ *   output wave w (chunk tokens 16w..16w+15):
+ *                                                               barrier 1
+ *     O_w = (Q e^G)_w S (8 MFMAs) from the same S^T;            barrier 2
+ *     O_w += QKm_w V' (12 MFMAs), O (fp32) out through a per-wave LDS tile.
+ * The output waves keep their products off the recurrence's critical path:
+ * each LDS buffer is written by the chain waves only after the barrier
+ * that follows the output waves' last read of it (S^T(c+1) after barrier 2
+ * of chunk c, V'^T(c+1) after barrier 1 of chunk c+1), so one copy of each
+ * suffices.
  * Phase A stored every operand in fragment order, so each lane loads its
- * fragments with 16-byte reads straight into registers, one chunk ahead.
- * The NCB workgroups of one unit share those operands; block numbering puts
- * them on one XCD (blockIdx % 8 picks the XCD), so their L2 serves the
- * repeats. */
+ * fragments with 16-byte reads straight into registers, one chunk ahead, in
+ * parts between its MFMA groups: issued as one burst, the texture unit's
+ * time for all of them would be spent before a barrier and added to the
+ * chain. The NCB workgroups of one unit share those operands; block
+ * numbering puts them on one XCD (blockIdx % 8 picks the XCD), so their L2
+ * serves the repeats. */
 constexpr int NCB = DV / 32;
+constexpr int CB_THREADS = 512;
 
-struct BOps {
-    bf16x8 w[4], qg[4], qkh[2], qkl[2], kgh[4], kgl[4];
+struct ChainOps {
+    bf16x8 w[4], kgh[4], kgl[4];
     float4 u[2];
     float gl;
 };
+struct OutOps {
+    bf16x8 qg[4], qkh[2], qkl[2];
+};
 
-__global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
+__global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
     const bf16x8 *__restrict__ Wi, const bf16x8 *__restrict__ Qgi, const bf16x8 *__restrict__ QKi,
     const bf16x8 *__restrict__ KgTi, const float4 *__restrict__ Ui, const float *__restrict__ Gli,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
@@ -961,12 +975,12 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
     __shared__ __attribute__((aligned(16))) bf16 sT[32][DK + 8];   /* S^T [column][dk]        */
     __shared__ __attribute__((aligned(16))) bf16 vTh[32][CH + 8];  /* V'^T hi [column][token] */
     __shared__ __attribute__((aligned(16))) bf16 vTl[32][CH + 8];  /* V'^T lo                 */
-    __shared__ __attribute__((aligned(16))) float ost[4][16][36];  /* per-wave O tile         */
+    __shared__ __attribute__((aligned(16))) float ost[4][16][36];  /* per output wave O tile  */
 
     const int bid = blockIdx.x;
     const int nmain = NCB * ((units + 7) / 8) * 8;
-    if (bid >= nmain) { /* conv tail: 256 channels per workgroup */
-        const int c = (bid - nmain) * 256 + threadIdx.x;
+    if (bid >= nmain) { /* conv tail: CB_THREADS channels per workgroup */
+        const int c = (bid - nmain) * CB_THREADS + threadIdx.x;
         if (c < tail.C) {
             float tv[3];
 #pragma unroll
@@ -987,62 +1001,164 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
     const int seg = un / Hv, hv = un - seg * Hv;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int w4 = wave & 3;
     const int h = lane >> 5, c32 = lane & 31, q4 = lane >> 4, c16 = lane & 15;
     const int col0 = 32 * cbk;
-
-    floatx16 S; /* rows 32 wave + 8(r/4) + 4h + r%4, column col0 + c32 */
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int dk = 32 * wave + 8 * (r >> 2) + 4 * h + (r & 3);
-        S[r] = S_in ? S_in[((size_t)hv * DK + dk) * DV + col0 + c32] : 0.f;
-    }
-    /* consume S here, before any operand prefetch is in flight: S then enters
-     * the chunk loop as a VALU result, and the loop's waits only cover the
-     * operand set a step uses */
-#pragma unroll
-    for (int r = 0; r < 16; r++)
-        S[r] += 0.f;
     const int c0 = seg_chunk0[seg], nc = seg_nchunk[seg];
+    /* A segment's chunks are consecutive 64-token slices: token offsets
+     * follow from the first chunk, the length from the last. The loads are
+     * unconditional (past the end they repeat the last chunk) so the
+     * compiler's wait counts stay exact: a load skipped on one path makes
+     * the next use wait for every load in flight. */
+    const int tok_seg = nc > 0 ? chunk_tok0[c0] : 0;
+    const int len_last = nc > 0 ? chunk_len[c0 + nc - 1] : 0;
+    auto cl = [&](int ci) { return c0 + min(ci, nc - 1); };
+    /* S^T as the 16x16x32 B operand: k step s, column block jb */
+    auto read_sb = [&](bf16x8 (&sb)[4][2]) {
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int jb = 0; jb < 2; jb++)
+                sb[s][jb] = *(const bf16x8 *)&sT[16 * jb + c16][32 * s + 8 * q4];
+    };
 
-    /* The operand set of a chunk in four parts, so that the next chunk's
-     * loads can be issued piecewise between this chunk's MFMAs: issued as one
-     * burst, the texture unit's time for all of them (about 1.4k cycles per
-     * CU for 88 KiB) would be spent before the barrier that starts the
-     * dependent chain, and added to it. */
-    struct OpPtr {
-        const bf16x8 *w, *qg, *kg, *qk;
-        const float4 *u;
-        const float *gl;
+    if (wave < 4) {
+        /* ---- chain waves: the recurrence ---- */
+        floatx16 S; /* rows 32 w4 + 8(r/4) + 4h + r%4, column col0 + c32 */
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int dk = 32 * w4 + 8 * (r >> 2) + 4 * h + (r & 3);
+            S[r] = S_in ? S_in[((size_t)hv * DK + dk) * DV + col0 + c32] : 0.f;
+        }
+        /* consume S here, before any operand prefetch is in flight: S then
+         * enters the chunk loop as a VALU result, and the loop's waits only
+         * cover the operand set a step uses */
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            S[r] += 0.f;
+        struct Ptr {
+            const bf16x8 *w, *kg;
+            const float4 *u;
+            const float *gl;
+        };
+        auto ptrs = [&](int ch) {
+            const size_t cb = (size_t)ch * Hv + hv;
+            Ptr p;
+            p.w = Wi + cb * 1024 + w4 * 256 + lane;
+            p.kg = KgTi + cb * 2048 + w4 * 256 + lane;
+            p.u = Ui + (cb * 1024 + (cbk * 4 + w4) * 64 + lane) * 2;
+            p.gl = Gli + cb * 64 + lane;
+            return p;
+        };
+        auto load_part = [&](const Ptr &p, ChainOps &op, int part) {
+            if (part == 0) {
+#pragma unroll
+                for (int s = 0; s < 4; s++)
+                    op.w[s] = p.w[64 * s];
+            } else if (part == 1) {
+                op.u[0] = p.u[0];
+                op.u[1] = p.u[1];
+                op.gl = p.gl[0];
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    op.kgh[s] = p.kg[64 * s];
+                    op.kgl[s] = p.kg[1024 + 64 * s];
+                }
+            }
+        };
+        auto step = [&](const ChainOps &op, int chn, ChainOps &nx) {
+            const Ptr np = ptrs(chn);
+            const float dec = fast_exp(op.gl);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                *(bf16x4 *)&sT[c32][32 * w4 + 8 * j + 4 * h] = bf16x4{
+                    f2bf(S[4 * j]), f2bf(S[4 * j + 1]), f2bf(S[4 * j + 2]), f2bf(S[4 * j + 3])};
+            lds_barrier(); /* 1: S^T of this chunk */
+            bf16x8 sb[4][2];
+            read_sb(sb);
+            floatx4 V[2] = {};
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int jb = 0; jb < 2; jb++)
+                    V[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.w[s], sb[s][jb], V[jb], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            load_part(np, nx, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            const float uf[8] = {op.u[0].x, op.u[0].y, op.u[0].z, op.u[0].w,
+                                 op.u[1].x, op.u[1].y, op.u[1].z, op.u[1].w};
+#pragma unroll
+            for (int jb = 0; jb < 2; jb++) {
+                bf16x4 ph, pl;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const bfpair sp_ = split2(uf[4 * jb + i] - V[jb][i]);
+                    ph[i] = sp_.hi;
+                    pl[i] = sp_.lo;
+                }
+                *(bf16x4 *)&vTh[16 * jb + c16][16 * w4 + 4 * q4] = ph;
+                *(bf16x4 *)&vTl[16 * jb + c16][16 * w4 + 4 * q4] = pl;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_part(np, nx, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            lds_barrier(); /* 2: V'^T of this chunk */
+            bf16x8 vbh[4], vbl[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                vbh[s] = *(const bf16x8 *)&vTh[c32][16 * s + 8 * h];
+                vbl[s] = *(const bf16x8 *)&vTl[c32][16 * s + 8 * h];
+            }
+            S = S * dec;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgh[s], vbh[s], S, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgh[s], vbl[s], S, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgl[s], vbh[s], S, 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_part(np, nx, 2);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        if (nc > 0) {
+            ChainOps A, B;
+#pragma unroll
+            for (int part = 0; part < 3; part++)
+                load_part(ptrs(cl(0)), A, part);
+            for (int ci = 0; ci < nc; ci += 2) {
+                step(A, cl(ci + 1), B);
+                if (ci + 1 >= nc)
+                    break;
+                step(B, cl(ci + 2), A);
+            }
+        }
+        if (S_out && seg == 0) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int dk = 32 * w4 + 8 * (r >> 2) + 4 * h + (r & 3);
+                S_out[((size_t)hv * DK + dk) * DV + col0 + c32] = S[r];
+            }
+        }
+        return;
+    }
+
+    /* ---- output waves: O of chunk tokens 16 w4 .. +15 ---- */
+    struct Ptr {
+        const bf16x8 *qg, *qk;
     };
     auto ptrs = [&](int ch) {
         const size_t cb = (size_t)ch * Hv + hv;
-        OpPtr p;
-        p.w = Wi + cb * 1024 + wave * 256 + lane;
-        p.qg = Qgi + cb * 1024 + wave * 256 + lane;
-        p.kg = KgTi + cb * 2048 + wave * 256 + lane;
-        p.qk = QKi + cb * 1024 + wave * 128 + lane;
-        p.u = Ui + (cb * 1024 + (cbk * 4 + wave) * 64 + lane) * 2;
-        p.gl = Gli + cb * 64 + lane;
+        Ptr p;
+        p.qg = Qgi + cb * 1024 + w4 * 256 + lane;
+        p.qk = QKi + cb * 1024 + w4 * 128 + lane;
         return p;
     };
-    auto load_part = [&](const OpPtr &p, BOps &op, int part) {
+    auto load_part = [&](const Ptr &p, OutOps &op, int part) {
         if (part == 0) {
-            op.gl = p.gl[0];
-            op.u[0] = p.u[0];
-            op.u[1] = p.u[1];
-#pragma unroll
-            for (int s = 0; s < 4; s++)
-                op.w[s] = p.w[64 * s];
-        } else if (part == 1) {
 #pragma unroll
             for (int s = 0; s < 4; s++)
                 op.qg[s] = p.qg[64 * s];
-        } else if (part == 2) {
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                op.kgh[s] = p.kg[64 * s];
-                op.kgl[s] = p.kg[1024 + 64 * s];
-            }
         } else {
 #pragma unroll
             for (int s = 0; s < 2; s++) {
@@ -1051,74 +1167,24 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
             }
         }
     };
-    auto load = [&](int ch, BOps &op) {
-        const OpPtr p = ptrs(ch);
-#pragma unroll
-        for (int part = 0; part < 4; part++)
-            load_part(p, op, part);
-    };
-
-    /* A segment's chunks are consecutive 64-token slices: token offsets
-     * follow from the first chunk, the length from the last. The log-decay
-     * travels with the operand set (phase A stores it once per lane). */
-    const int tok_seg = nc > 0 ? chunk_tok0[c0] : 0;
-    const int len_last = nc > 0 ? chunk_len[c0 + nc - 1] : 0;
-
-    /* One chunk with operand set op; the set of chunk chn goes into nx in
-     * four parts between the MFMA groups (pinned there by scheduling
-     * barriers). */
-    auto step = [&](int ch, const BOps &op, int chn, BOps &nx) {
+    auto step = [&](int ch, const OutOps &op, int chn, OutOps &nx) {
         const int ci = ch - c0;
         const int t0 = tok_seg + CH * ci, L = ci + 1 < nc ? CH : len_last;
-        const OpPtr np = ptrs(chn);
-        const float dec = fast_exp(op.gl);
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            *(bf16x4 *)&sT[c32][32 * wave + 8 * j + 4 * h] =
-                bf16x4{f2bf(S[4 * j]), f2bf(S[4 * j + 1]), f2bf(S[4 * j + 2]), f2bf(S[4 * j + 3])};
-        lds_barrier();
-        /* every LDS operand of a stage is read before its MFMAs: one wait */
+        const Ptr np = ptrs(chn);
+        lds_barrier(); /* 1 */
         bf16x8 sb[4][2];
-#pragma unroll
-        for (int s = 0; s < 4; s++)
-#pragma unroll
-            for (int jb = 0; jb < 2; jb++)
-                sb[s][jb] = *(const bf16x8 *)&sT[16 * jb + c16][32 * s + 8 * q4];
-        floatx4 V[2] = {}, O[2] = {};
-#pragma unroll
-        for (int s = 0; s < 4; s++)
-#pragma unroll
-            for (int jb = 0; jb < 2; jb++)
-                V[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.w[s], sb[s][jb], V[jb], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        load_part(np, nx, 0);
-        __builtin_amdgcn_sched_barrier(0);
+        read_sb(sb);
+        floatx4 O[2] = {};
 #pragma unroll
         for (int s = 0; s < 4; s++)
 #pragma unroll
             for (int jb = 0; jb < 2; jb++)
                 O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qg[s], sb[s][jb], O[jb], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        load_part(np, nx, 1);
+        load_part(np, nx, 0);
         __builtin_amdgcn_sched_barrier(0);
-        const float uf[8] = {op.u[0].x, op.u[0].y, op.u[0].z, op.u[0].w,
-                             op.u[1].x, op.u[1].y, op.u[1].z, op.u[1].w};
-#pragma unroll
-        for (int jb = 0; jb < 2; jb++) {
-            bf16x4 ph, pl;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                { const bfpair sp_ = split2(uf[4 * jb + i] - V[jb][i]); ph[i] = sp_.hi; pl[i] = sp_.lo; }
-            *(bf16x4 *)&vTh[16 * jb + c16][16 * wave + 4 * q4] = ph;
-            *(bf16x4 *)&vTl[16 * jb + c16][16 * wave + 4 * q4] = pl;
-        }
-        lds_barrier();
-        bf16x8 vbh[4], vbl[4], v2h[2][2], v2l[2][2];
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            vbh[s] = *(const bf16x8 *)&vTh[c32][16 * s + 8 * h];
-            vbl[s] = *(const bf16x8 *)&vTl[c32][16 * s + 8 * h];
-        }
+        lds_barrier(); /* 2 */
+        bf16x8 v2h[2][2], v2l[2][2];
 #pragma unroll
         for (int s = 0; s < 2; s++)
 #pragma unroll
@@ -1126,16 +1192,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
                 v2h[s][jb] = *(const bf16x8 *)&vTh[16 * jb + c16][32 * s + 8 * q4];
                 v2l[s][jb] = *(const bf16x8 *)&vTl[16 * jb + c16][32 * s + 8 * q4];
             }
-        S = S * dec;
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgh[s], vbh[s], S, 0, 0, 0);
-            S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgh[s], vbl[s], S, 0, 0, 0);
-            S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.kgl[s], vbh[s], S, 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        load_part(np, nx, 2);
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 2; s++)
 #pragma unroll
@@ -1145,45 +1201,33 @@ __global__ __launch_bounds__(256) void gdn_chunk_b_kernel(
                 O[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op.qkl[s], v2h[s][jb], O[jb], 0, 0, 0);
             }
         __builtin_amdgcn_sched_barrier(0);
-        load_part(np, nx, 3);
+        load_part(np, nx, 1);
         __builtin_amdgcn_sched_barrier(0);
         /* O (fp32) through this wave's LDS tile: 32-byte stores, 128 bytes a row */
 #pragma unroll
         for (int jb = 0; jb < 2; jb++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                ost[wave][4 * q4 + i][16 * jb + c16] = O[jb][i];
+                ost[w4][4 * q4 + i][16 * jb + c16] = O[jb][i];
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int r = lane >> 2, c8 = 8 * (lane & 3);
-        const float4 o0 = *(const float4 *)&ost[wave][r][c8];
-        const float4 o1 = *(const float4 *)&ost[wave][r][c8 + 4];
-        if (16 * wave + r < L) {
-            float *dst = o + ((size_t)(t0 + 16 * wave + r) * Hv + hv) * DV + col0 + c8;
+        const float4 o0 = *(const float4 *)&ost[w4][r][c8];
+        const float4 o1 = *(const float4 *)&ost[w4][r][c8 + 4];
+        if (16 * w4 + r < L) {
+            float *dst = o + ((size_t)(t0 + 16 * w4 + r) * Hv + hv) * DV + col0 + c8;
             *(float4 *)dst = o0;
             *(float4 *)(dst + 4) = o1;
         }
     };
-
-    /* two operand sets in rotation: chunk ci + 1 loads while ci runs. The
-     * loads are unconditional (past the end they repeat the last chunk) so
-     * the compiler's wait counts stay exact: a load skipped on one path makes
-     * the next use wait for every load in flight. */
     if (nc > 0) {
-        auto cl = [&](int ci) { return c0 + min(ci, nc - 1); };
-        BOps A, B;
-        load(cl(0), A);
+        OutOps A, B;
+        load_part(ptrs(cl(0)), A, 0);
+        load_part(ptrs(cl(0)), A, 1);
         for (int ci = 0; ci < nc; ci += 2) {
             step(c0 + ci, A, cl(ci + 1), B);
             if (ci + 1 >= nc)
                 break;
             step(c0 + ci + 1, B, cl(ci + 2), A);
-        }
-    }
-    if (S_out && seg == 0) {
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int dk = 32 * wave + 8 * (r >> 2) + 4 * h + (r & 3);
-            S_out[((size_t)hv * DK + dk) * DV + col0 + c32] = S[r];
         }
     }
 }
@@ -1665,9 +1709,9 @@ static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *
     if (packed)
         return hipErrorInvalidValue; /* packed segments write no final state */
     const int units = ck->num_segments * Hv;
-    const int ntail = tail.conv_out ? CEIL_DIV(tail.C, 256) : 0;
+    const int ntail = tail.conv_out ? CEIL_DIV(tail.C, CB_THREADS) : 0;
     hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)(NCB * CEIL_DIV(units, 8) * 8 + ntail)),
-                       dim3(256), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
+                       dim3(CB_THREADS), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
                        (const bf16x8 *)ws->QK, (const bf16x8 *)ws->KgT, (const float4 *)ws->U,
                        ws->Glast, ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk,
                        S_in, S_out, Hv, units, ws->O, tail);
