@@ -10,7 +10,8 @@
  * residual projections split K into fp32 partials that the residual add +
  * RMSNorm sums, and the grid is one round of workgroups:
  *
- *  - 4 waves stacked along M, one per SIMD. A wave owns RG row groups of
+ *  - 4 waves stacked along M, one per SIMD (or 8, two per SIMD, each with
+ *    half the row groups: gw_eight_waves). A wave owns RG row groups of
  *    16 weight rows and all NG token groups of 16 of the tile: RG x NG
  *    accumulators of v_mfma_f32_16x16x32_bf16 (W as the A operand). Tile
  *    64 RG x 16 NG. A wave's weight rows are its own (no fragment is loaded
@@ -47,9 +48,19 @@ namespace CUJEV_KNS {
 namespace {
 
 constexpr int GW_THREADS = 256;
+
 constexpr int GW_KC = 128;
 
 enum { GW_PLAIN = 0, GW_GATED = 1, GW_PART = 2 };
+
+/* A tile of 64 RG rows runs as 8 waves of RG/2 row groups (two per SIMD,
+ * which hides part of each other's wait for late weight loads: 2-3 % at the
+ * prefill shapes) where the halves are whole (gated: whole gate/up pairs)
+ * and the wave's registers fit without scratch; else as 4 waves of RG. Each
+ * output is summed by one wave in the same k order either way. */
+constexpr bool gw_eight_waves(int rg, int ng, int mode) {
+    return rg % 2 == 0 && (mode != GW_GATED || rg % 4 == 0) && ng % 2 == 0 && !(rg == 4 && ng == 12);
+}
 
 DEV __amdgpu_buffer_rsrc_t gw_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
@@ -66,13 +77,16 @@ DEV void gw_lds_write(unsigned char *base, uint32_t off, bf16x8 v) {
     *(__attribute__((address_space(3))) bf16x8 *)((lds_u8 *)base + off) = v;
 }
 
-template <int RG, int NG, int MODE>
-__global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
+template <int RG, int NG, int MODE, int WV>
+__global__ __launch_bounds__(64 * WV, 1) void gemm_wide_kernel(
     const bf16 *__restrict__ X, int ldx, const bf16 *__restrict__ Wt, int N, int M, int K,
     int nch, int mblocks, int nblocks, int splits, int per_xcd, bf16 *__restrict__ Y, int ldy,
     float *__restrict__ P) {
     static_assert(MODE != GW_GATED || RG % 2 == 0, "gated tiles pair gate and up row groups");
+    static_assert(WV == 4 || WV == 8, "4 or 8 waves stacked along M");
+    static_assert((4 * NG) % WV == 0, "whole X pieces per thread");
     constexpr int BN = 16 * NG;       /* tokens per tile */
+    constexpr int SPT = 4 * NG / WV;  /* X pieces a thread stages per chunk */
     constexpr int XBUF = BN * 256;    /* bytes of one X chunk: BN tokens x 128 k */
     __shared__ __attribute__((aligned(1024))) unsigned char xl[2 * XBUF];
 
@@ -97,7 +111,7 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
         const int GI = G >> 1;
 #pragma unroll
         for (int r = 0; r < H; r++) {
-            gidx[r] = (mb * 4 + wave) * H + r;
+            gidx[r] = (mb * WV + wave) * H + r;
             const int gc = min(gidx[r], GI - 1);
             wofs[r] = (uint32_t)gc * 4096u;
             gidx[r + H] = gidx[r];
@@ -106,7 +120,7 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
     } else {
 #pragma unroll
         for (int r = 0; r < RG; r++) {
-            gidx[r] = (mb * 4 + wave) * RG + r;
+            gidx[r] = (mb * WV + wave) * RG + r;
             wofs[r] = (uint32_t)min(gidx[r], G - 1) * 4096u;
         }
     }
@@ -118,25 +132,26 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
         return gw_load(wr, wlane, c * wchunk + wofs[r] + (uint32_t)i * 1024u);
     };
 
-    /* X staging: thread (wave w, lane l) owns, for s < NG, the piece of token
-     * group s, step w, lane l: token nb BN + 16 s + l%16, 16-byte piece
-     * 8 (w/2) + 2 (l/16) + w%2 of the chunk; it lands at LDS byte
-     * 16 (tid + 256 s). */
+    /* X staging: piece p = tid + 64 WV s (s < SPT) of a chunk is token group
+     * p / 256, step i = (p / 64) % 4 (= wave % 4), lane l: token nb BN +
+     * 16 (p / 256) + l%16, 16-byte piece 8 (i/2) + 2 (l/16) + i%2 of the
+     * chunk; it lands at LDS byte 16 p. */
     const __amdgpu_buffer_rsrc_t xr = gw_rsrc(X, (uint32_t)((size_t)N * ldx * 2));
-    const int kpiece = 8 * (wave >> 1) + 2 * q + (wave & 1);
-    const uint32_t xrow0 =
-        (uint32_t)(nb * BN + c16) * (uint32_t)ldx * 2u + (uint32_t)kpiece * 16u;
-    const uint32_t xstride = 16u * (uint32_t)ldx * 2u; /* one token group */
-    auto ldx_chunk = [&](int cl, bf16x8 (&xs)[NG]) {
+    const int xi = wave & 3;
+    const int kpiece = 8 * (xi >> 1) + 2 * q + (xi & 1);
+    const uint32_t xrow0 = (uint32_t)(nb * BN + 16 * (wave >> 2) + c16) * (uint32_t)ldx * 2u +
+                           (uint32_t)kpiece * 16u;
+    const uint32_t xstride = (uint32_t)(16 * WV / 4) * (uint32_t)ldx * 2u; /* between pieces */
+    auto ldx_chunk = [&](int cl, bf16x8 (&xs)[SPT]) {
         const uint32_t kb = (uint32_t)(c0 + min(cl, nch - 1)) * (GW_KC * 2);
 #pragma unroll
-        for (int s = 0; s < NG; s++)
+        for (int s = 0; s < SPT; s++)
             xs[s] = gw_load(xr, xrow0 + (uint32_t)s * xstride, kb);
     };
-    auto stx_chunk = [&](int buf, const bf16x8 (&xs)[NG]) {
+    auto stx_chunk = [&](int buf, const bf16x8 (&xs)[SPT]) {
 #pragma unroll
-        for (int s = 0; s < NG; s++)
-            gw_lds_write(xl, (uint32_t)(buf * XBUF + (tid + 256 * s) * 16), xs[s]);
+        for (int s = 0; s < SPT; s++)
+            gw_lds_write(xl, (uint32_t)(buf * XBUF + (tid + 64 * WV * s) * 16), xs[s]);
     };
     /* B fragment (token group j, step i) of buffer b: 1 KiB at
      * b XBUF + (4 j + i) 1024, lane l at + 16 l */
@@ -157,7 +172,7 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
      * chunk the 12 newest loads in flight are the W prefetches issued after
      * the staged X */
     bf16x8 w[4][RG];
-    bf16x8 xs[NG];
+    bf16x8 xs[SPT];
     ldx_chunk(0, xs);
     stx_chunk(0, xs);
     ldx_chunk(1, xs);
@@ -250,8 +265,14 @@ hipError_t launch_mode(int RG, int NG, dim3 grid, hipStream_t s, const bf16 *X, 
                        int splits, int per_xcd, bf16 *Y, int ldy, float *P) {
 #define CUJEV_GW_CASE(rg, ng)                                                                \
     if (RG == rg && NG == ng) {                                                              \
-        hipLaunchKernelGGL((gemm_wide_kernel<rg, ng, MODE>), grid, dim3(GW_THREADS), 0, s, X, \
-                           ldx, W, N, M, K, nch, mblocks, nblocks, splits, per_xcd, Y, ldy, P); \
+        if constexpr (gw_eight_waves(rg, ng, MODE))                                         \
+            hipLaunchKernelGGL((gemm_wide_kernel<rg / 2, ng, MODE, 8>), grid, dim3(512), 0, s, \
+                               X, ldx, W, N, M, K, nch, mblocks, nblocks, splits, per_xcd, Y,  \
+                               ldy, P);                                                      \
+        else                                                                                 \
+            hipLaunchKernelGGL((gemm_wide_kernel<rg, ng, MODE, 4>), grid, dim3(GW_THREADS), 0, \
+                               s, X, ldx, W, N, M, K, nch, mblocks, nblocks, splits, per_xcd, \
+                               Y, ldy, P);                                                   \
         return hipGetLastError();                                                            \
     }
     CUJEV_GW_CASE(2, 8)
