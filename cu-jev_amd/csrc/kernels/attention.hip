@@ -26,7 +26,9 @@
  *    XOR-swizzled for conflict-free ds_read_b128. K and V^T have separate
  *    double buffers: while a wave runs the softmax of tile i interleaved with
  *    the S^T MFMAs of tile i+1 and then the PV MFMAs of tile i, the V^T of
- *    tile i+1 and the K of tile i+2 are in flight. One barrier per tile.
+ *    tile i+1 and the K of tile i+2 are in flight. One barrier per tile;
+ *    the last two PV MFMAs of a tile run after it, while the next tile's
+ *    first K reads come back (their operands are read before it).
  *  - The softmax shift mu stays 0 while the running max is within 2^+-64
  *    of it, so S accumulators start at the MFMA's inline zero and scores need
  *    no per-tile shift; only rows whose scores leave that range pay for a
@@ -258,6 +260,15 @@ __global__ __launch_bounds__(256) void attention_kernel(
 
     constexpr int QD = 3; /* S^T A-operand reads in flight, in k-steps */
     constexpr int VD = 4; /* V^T A-operand reads in flight, in MFMAs   */
+#ifndef ATT_HB
+#define ATT_HB 2
+#endif
+    constexpr int HB = ATT_HB; /* PV MFMAs held back past the barrier */
+    static_assert(HB <= VD && HB <= 8, "held-back operands are read before the barrier, in P block 3");
+    bf16x8 vd[HB], pd = {};
+#pragma unroll
+    for (int t = 0; t < HB; t++)
+        vd[t] = bf16x8{};
     auto kaddr = [&](int ks, int buf) { return ka[ks & 7] + (ks >> 3) * 256 + buf * K_BYTES; };
     auto vaddr = [&](int t, int buf) { return va[t >> 3] + (t & 7) * 4096 + buf * V_BYTES; };
 
@@ -322,6 +333,16 @@ __global__ __launch_bounds__(256) void attention_kernel(
                 r1[ks] = lds_read16(lds, kaddr(ks, kbuf_next) + 16384);
             }
         }
+        /* The previous tile's last HB PV MFMAs, held back past the barrier
+         * (their V^T operands were read before it) so the matrix core works
+         * while the reads above come back. Zero operands before the first
+         * tile. */
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < HB; t++)
+            o[(32 - HB + t) & 7] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(vd[t], pd, o[(32 - HB + t) & 7], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
         /* Softmax of tile i with the exponentials taken for the shift 0 (the
          * common case): score pairs 0-7 (P blocks 0 and 1) between the S^T
          * MFMAs of tile i+1, pairs 8-15 (blocks 2 and 3) between the PV MFMAs
@@ -398,13 +419,15 @@ __global__ __launch_bounds__(256) void attention_kernel(
             mu_run = mu_new;
         }
 
-        /* O^T += V^T P^T */
+        /* O^T += V^T P^T; with a next tile the last HB MFMAs wait for the
+         * next step (their operands in vd, pd) */
+        constexpr int TPV = NEXT ? 32 - HB : 32;
         bf16x8 vr[VD];
 #pragma unroll
         for (int t = 0; t < VD; t++)
             vr[t] = lds_read16(lds, vaddr(t, vbuf));
 #pragma unroll
-        for (int t = 0; t < 32; t++) {
+        for (int t = 0; t < TPV; t++) {
             const bf16x8 a = vr[t % VD];
             if (t + VD < 32)
                 vr[t % VD] = lds_read16(lds, vaddr(t + VD, vbuf));
@@ -414,6 +437,12 @@ __global__ __launch_bounds__(256) void attention_kernel(
             if (t < 16 && (t & 1) == 0)
                 pair(8 + (t >> 1));
             __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (NEXT) {
+#pragma unroll
+            for (int t = 0; t < HB; t++)
+                vd[t] = vr[(32 - HB + t) % VD]; /* the reads of MFMAs 32 - HB .. 31 */
+            pd = pf[3];
         }
         l_run += lsum;
         wait_tile_loads();
