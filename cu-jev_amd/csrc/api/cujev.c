@@ -106,6 +106,16 @@ API cujev_status cujev_model_open(const char *dir, const cujev_options *opts, cu
     m->max_tokens = m->opts.max_state_tokens > m->opts.max_branch_tokens
                         ? m->opts.max_state_tokens
                         : m->opts.max_branch_tokens;
+    /* CUJEV_DEFER_PREFILL=1: a prefill only stages its tokens and runs inside
+     * the state's next eval, as one pass over state and branch tokens (each
+     * layer's weights streamed once for both); the workspace then holds both.
+     * =2 stages too, but the eval runs the prefill on its own first. */
+    {
+        const char *e = getenv("CUJEV_DEFER_PREFILL");
+        m->defer_prefill = e && (*e == '1' || *e == '2') ? *e - '0' : 0;
+    }
+    if (m->defer_prefill)
+        m->max_tokens = m->opts.max_state_tokens + m->opts.max_branch_tokens;
     m->state_stride = cujev_kv_stride(m->opts.max_state_tokens);
     m->branch_stride = cujev_kv_stride(m->opts.max_branch_tokens);
     m->rope_positions = m->opts.max_state_tokens + m->opts.max_branch_tokens;
@@ -163,6 +173,7 @@ API void cujev_state_destroy(cujev_state *st) {
         cujev_graphs_forget(st->model, st);
     }
     cujev_slab_release(&st->mem);
+    free(st->pending);
     free(st->kv_k);
     free(st->kv_vt);
     free(st->S);
@@ -232,6 +243,21 @@ API cujev_status cujev_state_prefill(cujev_model *m, cujev_state *st, const int3
     for (int i = 0; i < N; i++)
         if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size)
             return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "token id %d out of range", tokens[i]);
+    st->pending_n = 0;
+    if (m->defer_prefill) { /* staged; the next eval runs it */
+        if (!st->pending) {
+            st->pending = (int32_t *)malloc((size_t)m->opts.max_state_tokens * 4);
+            if (!st->pending)
+                return cujev_raise(CUJEV_ERR_OOM, "deferred prefill staging");
+        }
+        memcpy(st->pending, tokens, (size_t)N * 4);
+        st->pending_n = N;
+        st->num_tokens = N;
+        m->timing.prefill_ms = 0.f;
+        m->timing.prefill_tokens = N;
+        cujev_error_reset();
+        return CUJEV_OK;
+    }
     const int32_t ss = 0, sl = N;
     st->num_tokens = 0;
     HIP_CHECK(hipEventRecord(m->ev0, m->stream));

@@ -41,12 +41,18 @@ static cujev_status check(cujev_model *m, hipError_t launch, const char *what, i
 
 #define K_TRY(call, what, layer) CJ_CHECK(check(m, (call), (what), (layer)))
 
-/* Everything the launch sequence needs besides the model and the state. */
+/* Everything the launch sequence needs besides the model and the state.
+ * Tokens come in up to two groups: the state's (PREFILL, and the first Ns of
+ * a FUSED call) and the branches' (EVAL, and the rest of a FUSED call).
+ * `chunks` is the GDN chunk table of the PREFILL or EVAL group; a FUSED call
+ * has the branches' there and the state's in `schunks`. Token indices in a
+ * table, and own-key bases, count from the start of their group. */
 typedef struct {
     cujev_fwd_mode mode;
     int N, B, P, nc, maxc;
+    int Ns, nc_s; /* FUSED: state tokens (first in the call) and their chunks */
     const int32_t *tok, *pos, *base, *rows, *cand, *ncand; /* device metadata */
-    cujev_chunks chunks;
+    cujev_chunks chunks, schunks;
 } fwd_launch;
 
 /* Projection GEMMs Y[N,M] = X[N,K] W^T. For few tokens (the eval, N <= 96)
@@ -144,8 +150,15 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
     const cujev_fwd_mode mode = a->mode;
     const float eps = c->rms_norm_eps;
     hipStream_t s = m->stream;
-    const cujev_gdn_scratch gws = cujev_gdn_scratch_carve(m->gdn_scratch, a->nc, m->Hv);
     const float q_scale = (1.0f / sqrtf((float)m->D)) * 1.4426950408889634f;
+    /* the groups: ns state tokens (rows [0, ns)), then nb branch tokens */
+    const int ns = mode == CUJEV_FWD_PREFILL ? N : mode == CUJEV_FWD_FUSED ? a->Ns : 0;
+    const int nb = N - ns;
+    const cujev_chunks *sch = mode == CUJEV_FWD_FUSED ? &a->schunks : &a->chunks;
+    const cujev_gdn_scratch gws_s =
+        cujev_gdn_scratch_carve(m->gdn_scratch, mode == CUJEV_FWD_FUSED ? a->nc_s : a->nc, m->Hv);
+    const cujev_gdn_scratch gws_b = cujev_gdn_scratch_carve(m->gdn_scratch, a->nc, m->Hv);
+    const size_t qrow = (size_t)m->Hq * m->D; /* q and attention-output row width */
 
     K_TRY(k_embed(a->tok, m->embed, m->x, N, H, s), "embed", -1);
     K_TRY(k_add_rmsnorm(m->x, NULL, NULL, 0, m->layers[0].in_norm, m->xb, N, H, eps, NULL, 0, s),
@@ -159,38 +172,52 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
         if (ly->type == CUJEV_LAYER_FULL) {
             K_TRY(proj_gemm(m, m->xb, ly->w_qkv, ly->wt_qkv, m->proj, N, m->w_attn, H), "gemm qkv",
                   l);
-            bf16_t *kdst, *vdst;
-            int kstride;
-            if (mode == CUJEV_FWD_PREFILL) {
-                kdst = st->kv_k[l];
-                vdst = st->kv_vt[l];
-                kstride = m->state_stride;
-            } else {
-                kdst = m->br_k;
-                vdst = m->br_vt;
-                kstride = m->branch_stride;
-            }
-            K_TRY(k_attn_prep(m->proj, m->w_attn, ly->q_norm, ly->k_norm, a->pos, N, m->Hq,
-                              m->Hkv, c->rotary_dim, m->rope, eps, q_scale, m->q, kdst, vdst,
-                              kstride, s),
-                  "attn_prep", l);
-            K_TRY(k_attention(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l], st->kv_vt[l],
-                              P, m->state_stride, kdst, vdst, kstride, a->base, N, m->Hq,
-                              m->Hkv, m->mix_out, m->attn_ws, m->attn_ws_bytes, s),
-                  "attention", l);
+            /* state tokens: K and V^T into the state's cache, causal over it;
+             * branch tokens: into the branch scratch, over the state's P keys
+             * and their own */
+            const bf16_t *bproj = m->proj + (size_t)ns * m->w_attn;
+            if (ns)
+                K_TRY(k_attn_prep(m->proj, m->w_attn, ly->q_norm, ly->k_norm, a->pos, ns, m->Hq,
+                                  m->Hkv, c->rotary_dim, m->rope, eps, q_scale, m->q, st->kv_k[l],
+                                  st->kv_vt[l], m->state_stride, s),
+                      "attn_prep", l);
+            if (nb)
+                K_TRY(k_attn_prep(bproj, m->w_attn, ly->q_norm, ly->k_norm, a->pos + ns, nb, m->Hq,
+                                  m->Hkv, c->rotary_dim, m->rope, eps, q_scale,
+                                  m->q + (size_t)ns * qrow, m->br_k, m->br_vt, m->branch_stride,
+                                  s),
+                      "attn_prep", l);
+            if (ns)
+                K_TRY(k_attention(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l],
+                                  st->kv_vt[l], 0, m->state_stride, st->kv_k[l], st->kv_vt[l],
+                                  m->state_stride, a->base, ns, m->Hq, m->Hkv, m->mix_out,
+                                  m->attn_ws, m->attn_ws_bytes, s),
+                      "attention", l);
+            if (nb)
+                K_TRY(k_attention(m->q + (size_t)ns * qrow, bproj + m->D, m->w_attn, 2 * m->D,
+                                  st->kv_k[l], st->kv_vt[l], P, m->state_stride, m->br_k,
+                                  m->br_vt, m->branch_stride, a->base + ns, nb, m->Hq, m->Hkv,
+                                  m->mix_out + (size_t)ns * qrow, m->attn_ws, m->attn_ws_bytes,
+                                  s),
+                      "attention", l);
             K_TRY(resid_gemm(m, m->mix_out, ly->w_o, ly->wt_o, N, H, m->Hq * m->D, 0, &ry, &ryp,
                              &rsp),
                   "gemm o", l);
         } else {
             K_TRY(proj_gemm(m, m->xb, ly->w_in, ly->wt_in, m->proj, N, m->w_gdn, H), "gemm in", l);
-            const float *conv_in = mode == CUJEV_FWD_EVAL ? st->conv[l] : NULL;
-            float *conv_out = mode == CUJEV_FWD_PREFILL ? st->conv[l] : NULL;
-            const float *S_in = mode == CUJEV_FWD_EVAL ? st->S[l] : NULL;
-            float *S_out = mode == CUJEV_FWD_PREFILL ? st->S[l] : NULL;
-            K_TRY(k_gdn_layer(m->proj, m->w_gdn, ly->conv_w, conv_in, conv_out, N, a->base,
-                              ly->A_neg_exp, ly->dt_bias, &a->chunks, S_in, S_out, ly->g_norm,
-                              eps, m->Hk, m->Hv, m->mix_out, &gws, N, s),
-                  "gdn_layer", l);
+            /* state tokens write the state's final S and conv tail; branch
+             * tokens continue from them (read-only) */
+            if (ns)
+                K_TRY(k_gdn_layer(m->proj, m->w_gdn, ly->conv_w, NULL, st->conv[l], ns, a->base,
+                                  ly->A_neg_exp, ly->dt_bias, sch, NULL, st->S[l], ly->g_norm, eps,
+                                  m->Hk, m->Hv, m->mix_out, &gws_s, ns, s),
+                      "gdn_layer", l);
+            if (nb)
+                K_TRY(k_gdn_layer(m->proj + (size_t)ns * m->w_gdn, m->w_gdn, ly->conv_w,
+                                  st->conv[l], NULL, nb, a->base + ns, ly->A_neg_exp, ly->dt_bias,
+                                  &a->chunks, st->S[l], NULL, ly->g_norm, eps, m->Hk, m->Hv,
+                                  m->mix_out + (size_t)ns * m->V, &gws_b, nb, s),
+                      "gdn_layer", l);
             K_TRY(resid_gemm(m, m->mix_out, ly->w_out, ly->wt_out, N, H, m->V, 0, &ry, &ryp,
                              &rsp),
                   "gemm out", l);
@@ -331,19 +358,41 @@ static cujev_status run_eval(cujev_model *m, cujev_state *st, const fwd_launch *
                            : cujev_raise(CUJEV_ERR_CUDA, "hipGraphLaunch: %s", hipGetErrorString(e));
 }
 
-cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
-                                           const int32_t *tokens, int N, const int32_t *seg_start,
-                                           const int32_t *seg_len, int B, const int32_t *cand,
-                                           const int32_t *ncand, int maxc, int32_t **d_cand,
-                                           int32_t **d_ncand) {
-    const int P = mode == CUJEV_FWD_EVAL ? st->num_tokens : 0;
+/* GDN chunk rows of B segments (starts counted within their group): each
+ * segment's 64-token chunks in order. Returns the number of chunks. */
+static int fill_chunk_table(int32_t *h, size_t o_ctok, size_t o_clen, size_t o_sc0, size_t o_snc,
+                            const int32_t *seg_start, const int32_t *seg_len, int B) {
+    int ci = 0;
+    for (int b = 0; b < B; b++) {
+        h[o_sc0 + b] = ci;
+        for (int t = 0; t < seg_len[b]; t += 64) {
+            h[o_ctok + ci] = seg_start[b] + t;
+            h[o_clen + ci] = seg_len[b] - t < 64 ? seg_len[b] - t : 64;
+            ci++;
+        }
+        h[o_snc + b] = ci - h[o_sc0 + b];
+    }
+    return ci;
+}
+
+/* One forward over Ns state tokens (FUSED only, stok) followed by Nt tokens
+ * in B segments (the prefill's one segment, or the branches). */
+static cujev_status forward_call(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
+                                 const int32_t *stok, int Ns, const int32_t *tokens, int Nt,
+                                 const int32_t *seg_start, const int32_t *seg_len, int B,
+                                 const int32_t *cand, const int32_t *ncand, int maxc,
+                                 int32_t **d_cand, int32_t **d_ncand) {
+    const int N = Ns + Nt;
+    const int P = mode == CUJEV_FWD_EVAL ? st->num_tokens : Ns;
 
     /* ---- metadata: one packed block, one upload ---- */
     int nc = 0;
     for (int b = 0; b < B; b++)
         nc += (seg_len[b] + 63) / 64;
-    if (nc > m->max_chunks)
-        return cujev_raise(CUJEV_ERR_CAPACITY, "%d GDN chunks exceed %d", nc, m->max_chunks);
+    const int nc_s = (Ns + 63) / 64;
+    if (nc + nc_s > m->max_chunks)
+        return cujev_raise(CUJEV_ERR_CAPACITY, "%d GDN chunks exceed %d", nc + nc_s,
+                          m->max_chunks);
     /* Eval branches that each fit a 64-token chunk: consecutive whole
      * segments share a chunk (they all continue the stored state and write
      * none back), so a scan chunk holds up to 64 tokens however short the
@@ -353,7 +402,7 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
      * packed chunks, 0 when not packing. */
     int npk = 0;
     const int pack_min = gdn_pack_min_units();
-    if (mode == CUJEV_FWD_EVAL && pack_min >= 0 && B * m->Hv > pack_min) {
+    if (mode != CUJEV_FWD_PREFILL && pack_min >= 0 && B * m->Hv > pack_min) {
         int fill = 64, end = -1;
         for (int b = 0; b < B; b++) {
             if (seg_len[b] > 64) {
@@ -370,6 +419,7 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
             end = seg_start[b] + seg_len[b];
         }
     }
+    const int fused = mode == CUJEV_FWD_FUSED;
     int32_t *h = m->h_meta;
     size_t o = 0;
     const size_t o_cst = o; o += 2 * (size_t)npk; /* uint64 segment-start masks, 8-byte aligned */
@@ -381,27 +431,33 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
     const size_t o_clen = o; o += (size_t)nc;
     const size_t o_sc0 = o; o += (size_t)B;
     const size_t o_snc = o; o += (size_t)B;
+    const size_t o_sctok = o; o += (size_t)nc_s; /* FUSED: the state's one-segment table */
+    const size_t o_sclen = o; o += (size_t)nc_s;
+    const size_t o_ssc0 = o; o += fused;
+    const size_t o_ssnc = o; o += fused;
     const size_t o_cand = o; o += cand ? (size_t)B * maxc : 0;
     const size_t o_ncand = o; o += cand ? (size_t)B : 0;
     if (o > m->meta_ints)
         return cujev_raise(CUJEV_ERR_CAPACITY, "per-call metadata exceeds its buffer");
-    memcpy(h + o_tok, tokens, (size_t)N * 4);
-    int ci = 0;
+    if (Ns) { /* state tokens: positions 0.., one causal segment from 0 */
+        memcpy(h + o_tok, stok, (size_t)Ns * 4);
+        for (int t = 0; t < Ns; t++) {
+            h[o_pos + t] = t;
+            h[o_base + t] = 0;
+        }
+        const int32_t s0 = 0, sl = Ns;
+        fill_chunk_table(h, o_sctok, o_sclen, o_ssc0, o_ssnc, &s0, &sl, 1);
+    }
+    memcpy(h + o_tok + Ns, tokens, (size_t)Nt * 4);
     for (int b = 0; b < B; b++) {
         for (int t = 0; t < seg_len[b]; t++) {
-            const int n = seg_start[b] + t;
+            const int n = Ns + seg_start[b] + t;
             h[o_pos + n] = P + t;
             h[o_base + n] = seg_start[b];
         }
-        h[o_rows + b] = seg_start[b] + seg_len[b] - 1;
-        h[o_sc0 + b] = ci;
-        for (int t = 0; t < seg_len[b]; t += 64) {
-            h[o_ctok + ci] = seg_start[b] + t;
-            h[o_clen + ci] = seg_len[b] - t < 64 ? seg_len[b] - t : 64;
-            ci++;
-        }
-        h[o_snc + b] = ci - h[o_sc0 + b];
+        h[o_rows + b] = Ns + seg_start[b] + seg_len[b] - 1;
     }
+    fill_chunk_table(h, o_ctok, o_clen, o_sc0, o_snc, seg_start, seg_len, B);
     if (npk) { /* the chunk rows now describe packed chunks */
         int pc = -1, end = -1;
         uint64_t mask = 0;
@@ -433,11 +489,14 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
         *d_ncand = cand ? m->d_meta + o_ncand : NULL;
     }
     fwd_launch a;
+    memset(&a, 0, sizeof a);
     a.mode = mode;
     a.N = N;
     a.B = B;
     a.P = P;
     a.nc = nc;
+    a.Ns = Ns;
+    a.nc_s = nc_s;
     a.maxc = cand ? maxc : 0;
     a.tok = d + o_tok;
     a.pos = d + o_pos;
@@ -457,7 +516,51 @@ cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cuje
         a.nc = a.chunks.num_chunks = npk;
         a.chunks.chunk_starts = (const uint64_t *)(d + o_cst);
     }
+    if (fused) {
+        const cujev_chunks sc = {d + o_sctok, d + o_sclen, d + o_ssc0, d + o_ssnc, nc_s, 1, nc_s,
+                                 NULL, Ns};
+        a.schunks = sc;
+    }
     return mode == CUJEV_FWD_EVAL ? run_eval(m, st, &a) : launch_all(m, st, &a);
+}
+
+cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
+                                           const int32_t *tokens, int N, const int32_t *seg_start,
+                                           const int32_t *seg_len, int B, const int32_t *cand,
+                                           const int32_t *ncand, int maxc, int32_t **d_cand,
+                                           int32_t **d_ncand) {
+    if (mode == CUJEV_FWD_FUSED)
+        return cujev_raise(CUJEV_ERR_INVALID_ARGUMENT, "FUSED comes from a pending prefill");
+    if (mode == CUJEV_FWD_EVAL && st->pending_n > 0) {
+        /* a deferred prefill: one pass over both when they fit the
+         * workspace, else the prefill on its own first */
+        const int Ns = st->pending_n;
+        int nc = 0;
+        for (int b = 0; b < B; b++)
+            nc += (seg_len[b] + 63) / 64;
+        st->pending_n = 0;
+        cujev_status s;
+        if (m->defer_prefill == 1 && Ns + N <= m->max_tokens &&
+            nc + (Ns + 63) / 64 <= m->max_chunks) {
+            s = forward_call(m, st, CUJEV_FWD_FUSED, st->pending, Ns, tokens, N, seg_start,
+                             seg_len, B, cand, ncand, maxc, d_cand, d_ncand);
+            if (s != CUJEV_OK)
+                st->num_tokens = 0; /* the state is not usable */
+            return s;
+        }
+        const int32_t s0 = 0, sl = Ns;
+        s = forward_call(m, st, CUJEV_FWD_PREFILL, NULL, 0, st->pending, Ns, &s0, &sl, 1, NULL,
+                         NULL, 0, NULL, NULL);
+        /* the eval rewrites the pinned metadata block the prefill's upload reads */
+        if (s == CUJEV_OK && hipStreamSynchronize(m->stream) != hipSuccess)
+            s = cujev_raise(CUJEV_ERR_CUDA, "deferred prefill failed");
+        if (s != CUJEV_OK) {
+            st->num_tokens = 0;
+            return s;
+        }
+    }
+    return forward_call(m, st, mode, NULL, 0, tokens, N, seg_start, seg_len, B, cand, ncand, maxc,
+                        d_cand, d_ncand);
 }
 
 cujev_status cujev_forward(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,

@@ -296,7 +296,8 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
     const size_t mix = N * (size_t)((m->Hq * m->D > m->V) ? m->Hq * m->D : m->V);
     const size_t br_kv = (size_t)m->Hkv * m->branch_stride * m->D * 2;
     m->max_chunks = m->max_tokens / 64 + (int)B + 1;
-    m->meta_ints = 3 * N + 3 * B + 4 * (size_t)m->max_chunks + B * (size_t)m->opts.max_candidates + B;
+    /* + 8: a FUSED call's second (one-segment) chunk table heads */
+    m->meta_ints = 3 * N + 3 * B + 4 * (size_t)m->max_chunks + B * (size_t)m->opts.max_candidates + B + 8;
     m->gemm_ws_bytes = (size_t)64 << 20;
     m->attn_ws_bytes = cujev_attention_ws_max(m->max_tokens, m->Hq, m->Hkv);
     /* split-K partials: the few-token GEMM's at most 8 splits of 96 tokens,

@@ -73,7 +73,11 @@ struct cujev_model {
     /* derived widths */
     int D, Hq, Hkv, Hk, Hv, K, V, C;
     int w_attn, w_gdn, w_proj;
-    int max_tokens;     /* workspace rows: max(max_state, max_branch) */
+    int max_tokens;     /* workspace rows: max(max_state, max_branch), or their
+                         * sum when prefills are deferred */
+    int defer_prefill;  /* CUJEV_DEFER_PREFILL at open: 1 = a prefill runs
+                         * inside the state's next eval (one pass over both),
+                         * 2 = it runs first in that eval, on its own */
     int max_chunks;     /* GDN chunks of one forward */
     int state_stride;   /* kv stride of the state caches */
     int branch_stride;  /* kv stride of the branch scratch */
@@ -111,6 +115,10 @@ struct cujev_state {
     cujev_model *model;
     cujev_slab mem; /* K / V^T caches, S, conv tails */
     int num_tokens;
+    /* a deferred prefill not yet run: its tokens (host, max_state_tokens
+     * ints) and count; 0 when the device state is current */
+    int32_t *pending;
+    int pending_n;
     bf16_t **kv_k, **kv_vt; /* per layer, NULL for GDN layers */
     float **S;              /* per layer, NULL for full layers */
     float **conv;           /* per layer, NULL for full layers */
@@ -119,7 +127,12 @@ struct cujev_state {
 cujev_status cujev_model_load_weights(cujev_model *m, const char *dir);
 cujev_status cujev_model_alloc_workspace(cujev_model *m);
 
-typedef enum { CUJEV_FWD_PREFILL = 0, CUJEV_FWD_EVAL = 1 } cujev_fwd_mode;
+/* FUSED: one pass over [pending prefill tokens ++ branch tokens]. The
+ * token-parallel kernels (embedding, projections, norms) run once over all
+ * of them, so each layer's weights are streamed once; the mixers run per
+ * group, the state's first (writing the state), then the branches' (reading
+ * it), as PREFILL and EVAL would. */
+typedef enum { CUJEV_FWD_PREFILL = 0, CUJEV_FWD_EVAL = 1, CUJEV_FWD_FUSED = 2 } cujev_fwd_mode;
 
 /* Run the network over N tokens in B segments (host arrays). PREFILL: one
  * segment, side outputs go to the state. EVAL: every segment sees the state's
@@ -132,7 +145,10 @@ cujev_status cujev_forward(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
  * with the metadata; their device copies are returned in d_cand / d_ncand.
  * With candidates the readout runs too: d_logits[B][maxc] holds the
  * candidate logits. EVAL forwards are replayed from captured HIP graphs
- * once a launch shape repeats (CUJEV_GRAPHS=0 keeps them eager). */
+ * once a launch shape repeats (CUJEV_GRAPHS=0 keeps them eager). An EVAL on
+ * a state with a pending prefill runs FUSED when both fit the workspace (no
+ * graph), else the prefill first and then the EVAL; either way the state is
+ * current afterwards. */
 cujev_status cujev_forward_with_candidates(cujev_model *m, cujev_state *st, cujev_fwd_mode mode,
                                            const int32_t *tokens, int N, const int32_t *seg_start,
                                            const int32_t *seg_len, int B, const int32_t *cand,
