@@ -187,13 +187,19 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
                                   m->q + (size_t)ns * qrow, m->br_k, m->br_vt, m->branch_stride,
                                   s),
                       "attn_prep", l);
-            if (ns)
+            if (ns && nb) /* FUSED: both groups in one launch, side by side */
+                K_TRY(k_attention_pair(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l],
+                                       st->kv_vt[l], m->state_stride, a->base, m->mix_out, m->Hq,
+                                       m->Hkv, ns, 0, st->kv_k[l], st->kv_vt[l], m->state_stride,
+                                       nb, P, m->br_k, m->br_vt, m->branch_stride, s),
+                      "attention", l);
+            else if (ns)
                 K_TRY(k_attention(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l],
                                   st->kv_vt[l], 0, m->state_stride, st->kv_k[l], st->kv_vt[l],
                                   m->state_stride, a->base, ns, m->Hq, m->Hkv, m->mix_out,
                                   m->attn_ws, m->attn_ws_bytes, s),
                       "attention", l);
-            if (nb)
+            else
                 K_TRY(k_attention(m->q + (size_t)ns * qrow, bproj + m->D, m->w_attn, 2 * m->D,
                                   st->kv_k[l], st->kv_vt[l], P, m->state_stride, m->br_k,
                                   m->br_vt, m->branch_stride, a->base + ns, nb, m->Hq, m->Hkv,

@@ -150,19 +150,39 @@ struct AttnPart {
     int nsplit;
 };
 
-template <bool SPLIT>
+/* The second problem of a paired launch: N packed tokens starting row0
+ * rows after the first problem's, over the shared state cache's first P
+ * keys and their own keys in (ok, ovt) (see k_attention). */
+struct AttnJob {
+    const bf16 *ok, *ovt;
+    int row0, P, o_stride, N;
+};
+
+/* PAIR (attention_pair): workgroups [0, nblk_a) serve the problem of the
+ * leading arguments, the rest a second one over the same state cache, given
+ * by jb (its rows start jb.row0 rows further into q, gate, own_base and
+ * out; nblk_a is a multiple of 8 where Hkv divides 8, so both keep the XCD
+ * mapping). Without PAIR, jb and nblk_a are unused. */
+template <bool SPLIT, bool PAIR>
 __global__ __launch_bounds__(256) void attention_kernel(
     const bf16 *__restrict__ q, const bf16 *__restrict__ gate, int gts, int ghs,
     const bf16 *__restrict__ pk, const bf16 *__restrict__ pvt, int P, int p_stride,
     const bf16 *__restrict__ ok, const bf16 *__restrict__ ovt, int o_stride,
     const int32_t *__restrict__ own_base, int N, int Hq, int Hkv, int ntile, bf16 *__restrict__ out,
-    AttnPart part) {
+    AttnPart part, AttnJob jb, int nblk_a) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[LDS_BYTES];
+    int bid = blockIdx.x;
+    if (PAIR && bid >= nblk_a) {
+        bid -= nblk_a;
+        q += (size_t)jb.row0 * Hq * D, gate += (size_t)jb.row0 * gts;
+        own_base += jb.row0, out += (size_t)jb.row0 * Hq * D;
+        P = jb.P, ok = jb.ok, ovt = jb.ovt, o_stride = jb.o_stride, N = jb.N;
+        ntile = (N + QW - 1) / QW;
+    }
 
     /* ---- XCD-aware work mapping ---- */
     int kh, tile;
     {
-        const int bid = blockIdx.x;
         if (8 % Hkv == 0) {
             const int G = 8 / Hkv, xcd = bid & 7, slot = bid >> 3;
             kh = xcd / G;
@@ -734,6 +754,17 @@ extern "C" size_t cujev_attention_ws_max(int max_tokens, int Hq, int Hkv) {
     return best;
 }
 
+/* Workgroups of one job: ntile token tiles x Hkv kv-heads, rounded up so
+ * that every XCD group of the mapping is whole (a multiple of 8 when Hkv
+ * divides 8). */
+static int attention_blocks(int ntile, int Hkv) {
+    if (8 % Hkv == 0) {
+        const int G = 8 / Hkv;
+        return CEIL_DIV(ntile, G) * G * Hkv;
+    }
+    return ntile * Hkv;
+}
+
 extern "C" hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_tok_stride,
                                   int gate_head_stride, const bf16_t *pk, const bf16_t *pvt, int P,
                                   int p_stride, const bf16_t *ok, const bf16_t *ovt, int o_stride,
@@ -744,13 +775,7 @@ extern "C" hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_
     if (Hq != 4 * Hkv || P < 0 || p_stride % 64 != 0 || o_stride % 64 != 0)
         return hipErrorInvalidValue;
     const int ntile = CEIL_DIV(N, QW);
-    int nblk;
-    if (8 % Hkv == 0) {
-        const int G = 8 / Hkv;
-        nblk = CEIL_DIV(ntile, G) * G * Hkv;
-    } else {
-        nblk = ntile * Hkv;
-    }
+    const int nblk = attention_blocks(ntile, Hkv);
     /* Few workgroups (an eval of a few branches: 4 kv-heads x 3 token tiles
      * at 80 tokens): split the key tiles over blockIdx.y so that about 256
      * workgroups run, when the workspace holds the partials. */
@@ -758,20 +783,47 @@ extern "C" hipError_t k_attention(const bf16_t *q, const bf16_t *gate, int gate_
     if (nsplit > 1 && ws && ws_bytes >= cujev_attention_ws_bytes(N, Hq, nsplit)) {
         const size_t rows = (size_t)nsplit * N * Hq;
         AttnPart part{(float *)ws, (float *)ws + rows * D, (float *)ws + rows * (D + 1), nsplit};
-        hipLaunchKernelGGL(attention_kernel<true>, dim3((unsigned)nblk, (unsigned)nsplit),
+        hipLaunchKernelGGL((attention_kernel<true, false>), dim3((unsigned)nblk, (unsigned)nsplit),
                            dim3(256), 0, stream, (const bf16 *)q, (const bf16 *)gate,
                            gate_tok_stride, gate_head_stride, (const bf16 *)pk, (const bf16 *)pvt,
                            P, p_stride, (const bf16 *)ok, (const bf16 *)ovt, o_stride, own_base, N,
-                           Hq, Hkv, ntile, (bf16 *)out, part);
+                           Hq, Hkv, ntile, (bf16 *)out, part, AttnJob{}, 0);
         hipLaunchKernelGGL(attention_merge_kernel, dim3((unsigned)CEIL_DIV(N * Hq, 4)), dim3(256),
                            0, stream, part, (const bf16 *)gate, gate_tok_stride, gate_head_stride,
                            N, Hq, (bf16 *)out);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(attention_kernel<false>, dim3((unsigned)nblk), dim3(256), 0, stream,
+    hipLaunchKernelGGL((attention_kernel<false, false>), dim3((unsigned)nblk), dim3(256), 0, stream,
                        (const bf16 *)q, (const bf16 *)gate, gate_tok_stride, gate_head_stride,
                        (const bf16 *)pk, (const bf16 *)pvt, P, p_stride, (const bf16 *)ok,
                        (const bf16 *)ovt, o_stride, own_base, N, Hq, Hkv, ntile, (bf16 *)out,
-                       AttnPart{});
+                       AttnPart{}, AttnJob{}, 0);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t k_attention_pair(const bf16_t *q, const bf16_t *gate, int gate_tok_stride,
+                                       int gate_head_stride, const bf16_t *pk, const bf16_t *pvt,
+                                       int p_stride, const int32_t *own_base, bf16_t *out, int Hq,
+                                       int Hkv, int Na, int Pa, const bf16_t *oka,
+                                       const bf16_t *ovta, int oa_stride, int Nb, int Pb,
+                                       const bf16_t *okb, const bf16_t *ovtb, int ob_stride,
+                                       hipStream_t stream) {
+    if (Na <= 0 || Nb <= 0)
+        return Na > 0 ? k_attention(q, gate, gate_tok_stride, gate_head_stride, pk, pvt, Pa,
+                                    p_stride, oka, ovta, oa_stride, own_base, Na, Hq, Hkv, out,
+                                    nullptr, 0, stream)
+                      : k_attention(q, gate, gate_tok_stride, gate_head_stride, pk, pvt, Pb,
+                                    p_stride, okb, ovtb, ob_stride, own_base, Nb, Hq, Hkv, out,
+                                    nullptr, 0, stream);
+    if (Hq != 4 * Hkv || Pa < 0 || Pb < 0 || p_stride % 64 || oa_stride % 64 || ob_stride % 64)
+        return hipErrorInvalidValue;
+    const int ta = CEIL_DIV(Na, QW), tb = CEIL_DIV(Nb, QW);
+    const AttnJob jb{(const bf16 *)okb, (const bf16 *)ovtb, Na, Pb, ob_stride, Nb};
+    const int na = attention_blocks(ta, Hkv), nb = attention_blocks(tb, Hkv);
+    hipLaunchKernelGGL((attention_kernel<false, true>), dim3((unsigned)(na + nb)), dim3(256), 0,
+                       stream, (const bf16 *)q, (const bf16 *)gate, gate_tok_stride,
+                       gate_head_stride, (const bf16 *)pk, (const bf16 *)pvt, Pa, p_stride,
+                       (const bf16 *)oka, (const bf16 *)ovta, oa_stride, own_base, Na, Hq, Hkv, ta,
+                       (bf16 *)out, AttnPart{}, jb, na);
     return hipGetLastError();
 }

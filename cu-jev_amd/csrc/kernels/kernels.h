@@ -76,6 +76,19 @@ int cujev_attention_splits(int N, int Hkv, int P);
 size_t cujev_attention_ws_bytes(int N, int Hq, int nsplit);
 /* the largest workspace any N <= max_tokens can use */
 size_t cujev_attention_ws_max(int max_tokens, int Hq, int Hkv);
+/* Two k_attention problems over one state cache (pk, pvt) in one launch,
+ * one pass each (no key split): rows [0, Na) of q, gate, own_base and out
+ * are problem a (the cache's first Pa keys, own keys in oka / ovta), rows
+ * [Na, Na + Nb) problem b (Pb keys, own keys in okb / ovtb; own_base
+ * counted from its own first row). The workgroups of one run beside the
+ * other's, so the launch takes about as long as the longer of the two. Same
+ * results as two k_attention calls with ws NULL. */
+hipError_t k_attention_pair(const bf16_t *q, const bf16_t *gate, int gate_tok_stride,
+                            int gate_head_stride, const bf16_t *pk, const bf16_t *pvt,
+                            int p_stride, const int32_t *own_base, bf16_t *out, int Hq, int Hkv,
+                            int Na, int Pa, const bf16_t *oka, const bf16_t *ovta, int oa_stride,
+                            int Nb, int Pb, const bf16_t *okb, const bf16_t *ovtb, int ob_stride,
+                            hipStream_t stream);
 
 /* ---- Gated DeltaNet -------------------------------------------------------
  * proj[N, proj_stride] bf16 is the fused row [q Hk*128 | k Hk*128 | v Hv*128 |

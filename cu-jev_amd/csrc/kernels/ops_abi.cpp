@@ -173,6 +173,23 @@ EXPORT int cujev_op_attention(const void *q, const void *gate, int gate_tok_stri
                     "attention");
 }
 
+EXPORT int cujev_op_attention_pair(const void *q, const void *gate, int gate_tok_stride,
+                                   int gate_head_stride, const void *pk, const void *pvt,
+                                   int p_stride, const int32_t *own_base, void *out, int Hq,
+                                   int Hkv, int Na, int Pa, const void *oka, const void *ovta,
+                                   int oa_stride, int Nb, int Pb, const void *okb,
+                                   const void *ovtb, int ob_stride, void *stream) {
+    if (Na < 0 || Nb < 0 || Pa < 0 || Pb < 0 || Hkv <= 0)
+        return fail(1, "attention_pair: bad arguments");
+    return launched(k_attention_pair((const bf16_t *)q, (const bf16_t *)gate, gate_tok_stride,
+                                     gate_head_stride, (const bf16_t *)pk, (const bf16_t *)pvt,
+                                     p_stride, own_base, (bf16_t *)out, Hq, Hkv, Na, Pa,
+                                     (const bf16_t *)oka, (const bf16_t *)ovta, oa_stride, Nb, Pb,
+                                     (const bf16_t *)okb, (const bf16_t *)ovtb, ob_stride,
+                                     (hipStream_t)stream),
+                    "attention_pair");
+}
+
 EXPORT size_t cujev_ops_attention_ws_bytes(int N, int Hq, int Hkv, int P) {
     return cujev_attention_ws_bytes(N, Hq, cujev_attention_splits(N, Hkv, P));
 }

@@ -36,6 +36,10 @@ _SIGS = {
                               C.c_size_t, _P],
     "cujev_op_attention_noalloc": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I,
                                    _P, _P],
+    # q, gate, gts, ghs, pk, pvt, p_stride, own_base, out, Hq, Hkv,
+    # Na, Pa, oka, ovta, oa_stride, Nb, Pb, okb, ovtb, ob_stride, stream
+    "cujev_op_attention_pair": [_P, _P, _I, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I,
+                                _I, _I, _P, _P, _I, _P],
     "cujev_op_gdn_conv_prep": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P,
                                _P, _P],
     "cujev_op_gemm_small": [_P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _P],
@@ -152,6 +156,18 @@ def attention(q, gate, gate_tok_stride, gate_head_stride, pk, pvt, P, p_stride, 
     _call("cujev_op_attention", _ptr(q), _ptr(gate), gate_tok_stride, gate_head_stride,
           _ptr(pk), _ptr(pvt), int(P), p_stride, _ptr(ok), _ptr(ovt), o_stride, _ptr(own_base),
           N, Hq, Hkv, _ptr(out), _stream())
+
+
+def attention_pair(q, gate, gate_tok_stride, gate_head_stride, pk, pvt, p_stride, own_base, Hq,
+                   Hkv, out, Na, Pa, oka, ovta, oa_stride, Pb, okb, ovtb, ob_stride):
+    """Two problems in one launch: rows [0, Na) of q / gate / own_base / out
+    over the state's first Pa keys and own keys (oka, ovta), the remaining
+    rows over Pb keys and (okb, ovtb)."""
+    Nb = q.shape[0] - Na
+    _call("cujev_op_attention_pair", _ptr(q), _ptr(gate), gate_tok_stride, gate_head_stride,
+          _ptr(pk), _ptr(pvt), p_stride, _ptr(own_base), _ptr(out), Hq, Hkv, int(Na), int(Pa),
+          _ptr(oka), _ptr(ovta), oa_stride, int(Nb), int(Pb), _ptr(okb), _ptr(ovtb), ob_stride,
+          _stream())
 
 
 def attention_noalloc(q, gate, gate_tok_stride, gate_head_stride, pk, pvt, P, p_stride, ok, ovt,

@@ -122,6 +122,18 @@ int cujev_op_attention(const void *q, const void *gate, int gate_tok_stride, int
                        const void *pk, const void *pvt, int P, int p_stride, const void *ok,
                        const void *ovt, int o_stride, const int32_t *own_base, int N, int Hq,
                        int Hkv, void *out, void *stream);
+/* Two such problems over one state cache in one launch (no counterpart in
+ * the reference; the engine's deferred-prefill pass uses it for the state's
+ * tokens and the branches' side by side). Rows [0, Na) of q, gate, own_base
+ * and out are problem a (state keys [0, Pa), own keys in oka / ovta), rows
+ * [Na, Na + Nb) problem b (state keys [0, Pb), own keys in okb / ovtb,
+ * own_base counted from its first row). One pass each: the same bits as two
+ * cujev_op_attention calls. */
+int cujev_op_attention_pair(const void *q, const void *gate, int gate_tok_stride,
+                            int gate_head_stride, const void *pk, const void *pvt, int p_stride,
+                            const int32_t *own_base, void *out, int Hq, int Hkv, int Na, int Pa,
+                            const void *oka, const void *ovta, int oa_stride, int Nb, int Pb,
+                            const void *okb, const void *ovtb, int ob_stride, void *stream);
 /* The same with a device workspace (no counterpart in the reference, whose
  * kernel has one pass): with few workgroups (N <= 256 tokens giving under
  * 128 of them) the key tiles are split over up to 16 workgroups

@@ -141,6 +141,53 @@ def test_attention_key_split_matches_oracle(seed, Hq, Hkv, P, seg_lens):
     assert e <= TOL and e1 <= 1e-2
 
 
+@pytest.mark.parametrize("Hq,Hkv,Na,branches", [
+    (16, 4, 530, [20] * 4),        # the deferred config-4 pass
+    (8, 2, 17, [33, 1, 5]),
+    (12, 3, 100, [64, 70]),        # Hkv not dividing 8: plain block mapping
+])
+def test_attention_pair_equals_two_launches(Hq, Hkv, Na, branches):
+    """The paired launch of the deferred-prefill pass: rows [0, Na) are a
+    prefill over the state cache's own rows (P = 0), the rest branches over
+    those Na keys and their own; the same bits as two one-pass launches."""
+    o = ops()
+    dev = "cuda"
+    rng = np.random.default_rng(Na + len(branches))
+    Nb = int(sum(branches))
+    N = Na + Nb
+    print(f"case Hq={Hq} Hkv={Hkv} Na={Na} branches={branches}", flush=True)
+    ps, bs = o.kv_stride(Na), o.kv_stride(Nb)
+    pk = torch.zeros(Hkv, ps, D, dtype=torch.bfloat16, device=dev)
+    pvt = torch.zeros(Hkv, D, ps, dtype=torch.bfloat16, device=dev)
+    pk[:, :Na] = bf(rng.standard_normal((Hkv, Na, D))).to(dev)
+    pvt[:, :, :Na] = bf(rng.standard_normal((Hkv, D, Na))).to(dev)
+    bk = torch.zeros(Hkv, bs, D, dtype=torch.bfloat16, device=dev)
+    bvt = torch.zeros(Hkv, D, bs, dtype=torch.bfloat16, device=dev)
+    bk[:, :Nb] = bf(rng.standard_normal((Hkv, Nb, D))).to(dev)
+    bvt[:, :, :Nb] = bf(rng.standard_normal((Hkv, D, Nb))).to(dev)
+    qd = bf(rng.standard_normal((N, Hq, D)) * 0.6 * orc.LOG2E / 16.0).to(dev)
+    qg = torch.zeros(N, Hq, 2 * D, dtype=torch.bfloat16, device=dev)
+    qg[:, :, D:] = bf(rng.standard_normal((N, Hq, D))).to(dev)
+    base = np.zeros(N, np.int32)
+    s0 = 0
+    for L in branches:
+        base[Na + s0: Na + s0 + L] = s0
+        s0 += L
+    ob = torch.as_tensor(base).to(dev)
+    gate = qg[:, :, D:]
+    pair = torch.empty(N, Hq * D, dtype=torch.bfloat16, device=dev)
+    o.attention_pair(qd, gate, Hq * 2 * D, 2 * D, pk, pvt, ps, ob, Hq, Hkv, pair, Na, 0, pk, pvt,
+                     ps, Na, bk, bvt, bs)
+    two = torch.empty_like(pair)
+    o.attention(qd[:Na], gate[:Na], Hq * 2 * D, 2 * D, pk, pvt, 0, ps, pk, pvt, ps, ob[:Na], Hq,
+                Hkv, two[:Na])
+    o.attention(qd[Na:], gate[Na:], Hq * 2 * D, 2 * D, pk, pvt, Na, ps, bk, bvt, bs, ob[Na:], Hq,
+                Hkv, two[Na:])
+    torch.cuda.synchronize()
+    assert torch.isfinite(pair.float()).all()
+    assert torch.equal(pair, two)
+
+
 def test_attention_branch_isolation():
     """A branch's output does not depend on its siblings. Not bit for bit:
     alone, the branch's rows sit at other positions of the 32-token tiles and
