@@ -155,9 +155,17 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
     const int ns = mode == CUJEV_FWD_PREFILL ? N : mode == CUJEV_FWD_FUSED ? a->Ns : 0;
     const int nb = N - ns;
     const cujev_chunks *sch = mode == CUJEV_FWD_FUSED ? &a->schunks : &a->chunks;
+    /* GDN scratch. FUSED: the state group's chunk arrays, then o for all N
+     * rows (the branch group's rows after the state's, so one gated norm
+     * covers both), then the branch group's chunk arrays. */
     const cujev_gdn_scratch gws_s =
         cujev_gdn_scratch_carve(m->gdn_scratch, mode == CUJEV_FWD_FUSED ? a->nc_s : a->nc, m->Hv);
-    const cujev_gdn_scratch gws_b = cujev_gdn_scratch_carve(m->gdn_scratch, a->nc, m->Hv);
+    cujev_gdn_scratch gws_b = gws_s;
+    if (mode == CUJEV_FWD_FUSED) {
+        gws_b = cujev_gdn_scratch_carve((char *)gws_s.O + cujev_align256((size_t)N * m->Hv * 128 * 4),
+                                        a->nc, m->Hv);
+        gws_b.O = gws_s.O + (size_t)ns * m->Hv * 128;
+    }
     const size_t qrow = (size_t)m->Hq * m->D; /* q and attention-output row width */
 
     K_TRY(k_embed(a->tok, m->embed, m->x, N, H, s), "embed", -1);
@@ -213,17 +221,35 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
             K_TRY(proj_gemm(m, m->xb, ly->w_in, ly->wt_in, m->proj, N, m->w_gdn, H), "gemm in", l);
             /* state tokens write the state's final S and conv tail; branch
              * tokens continue from them (read-only) */
+            /* o of both groups is left in scratch and normed by one launch
+             * where neither group's scan applied the norm itself */
+            int pend_s = 0, pend_b = 0;
             if (ns)
-                K_TRY(k_gdn_layer(m->proj, m->w_gdn, ly->conv_w, NULL, st->conv[l], ns, a->base,
-                                  ly->A_neg_exp, ly->dt_bias, sch, NULL, st->S[l], ly->g_norm, eps,
-                                  m->Hk, m->Hv, m->mix_out, &gws_s, ns, s),
+                K_TRY(k_gdn_layer_o(m->proj, m->w_gdn, ly->conv_w, NULL, st->conv[l], ns, a->base,
+                                    ly->A_neg_exp, ly->dt_bias, sch, NULL, st->S[l], ly->g_norm,
+                                    eps, m->Hk, m->Hv, m->mix_out, &gws_s, ns, s, &pend_s),
                       "gdn_layer", l);
             if (nb)
-                K_TRY(k_gdn_layer(m->proj + (size_t)ns * m->w_gdn, m->w_gdn, ly->conv_w,
-                                  st->conv[l], NULL, nb, a->base + ns, ly->A_neg_exp, ly->dt_bias,
-                                  &a->chunks, st->S[l], NULL, ly->g_norm, eps, m->Hk, m->Hv,
-                                  m->mix_out + (size_t)ns * m->V, &gws_b, nb, s),
+                K_TRY(k_gdn_layer_o(m->proj + (size_t)ns * m->w_gdn, m->w_gdn, ly->conv_w,
+                                    st->conv[l], NULL, nb, a->base + ns, ly->A_neg_exp,
+                                    ly->dt_bias, &a->chunks, st->S[l], NULL, ly->g_norm, eps,
+                                    m->Hk, m->Hv, m->mix_out + (size_t)ns * m->V, &gws_b, nb, s,
+                                    &pend_b),
                       "gdn_layer", l);
+            const bf16_t *z = m->proj + m->C; /* the gate z, after the conv channels */
+            const int zs = m->w_gdn;
+            if (pend_s && pend_b)
+                K_TRY(k_gdn_norm_gate(gws_s.O, z, zs, ly->g_norm, eps, N * m->Hv, m->Hv,
+                                      m->mix_out, s),
+                      "gdn_norm", l);
+            else if (pend_s)
+                K_TRY(k_gdn_norm_gate(gws_s.O, z, zs, ly->g_norm, eps, ns * m->Hv, m->Hv,
+                                      m->mix_out, s),
+                      "gdn_norm", l);
+            else if (pend_b)
+                K_TRY(k_gdn_norm_gate(gws_b.O, z + (size_t)ns * zs, zs, ly->g_norm, eps,
+                                      nb * m->Hv, m->Hv, m->mix_out + (size_t)ns * m->V, s),
+                      "gdn_norm", l);
             K_TRY(resid_gemm(m, m->mix_out, ly->w_out, ly->wt_out, N, H, m->V, 0, &ry, &ryp,
                              &rsp),
                   "gemm out", l);

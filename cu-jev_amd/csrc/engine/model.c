@@ -324,7 +324,10 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
         {(void **)&m->mix_out, mix * 2},
         {(void **)&m->br_k, br_kv},
         {(void **)&m->br_vt, br_kv},
-        {(void **)&m->gdn_scratch, cujev_gdn_scratch_bytes(m->max_chunks, m->Hv, m->max_tokens)},
+        /* + 4 KiB: a FUSED call carves the chunk arrays of its two token
+         * groups apart, each rounded up on its own */
+        {(void **)&m->gdn_scratch,
+         cujev_gdn_scratch_bytes(m->max_chunks, m->Hv, m->max_tokens) + 4096},
         {(void **)&m->act, N * I * 2},
         {(void **)&m->hsel, B * H * 2},
         {(void **)&m->full_logits, B * (size_t)c->vocab_size * 4},

@@ -1685,10 +1685,16 @@ extern "C" hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const
 }
 
 /* Phase B and the gated norm after phase A (either front end). */
+/* norm == false leaves o in ws->O for k_gdn_norm_gate (*o_pending = 1)
+ * where a separate norm launch would follow; the short-segment kernel
+ * applies the norm itself either way (*o_pending = 0). */
 static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *S_out,
                               const bf16_t *z, int z_stride, const float *norm_w, float eps,
                               int Hv, bf16_t *y, const cujev_gdn_scratch *ws, int N,
-                              const TailJob &tail, hipStream_t stream) {
+                              const TailJob &tail, hipStream_t stream, bool norm = true,
+                              int *o_pending = nullptr) {
+    if (o_pending)
+        *o_pending = 0;
     const bool packed = ck->chunk_starts != nullptr;
     if (!S_out && (packed || ck->max_seg_chunks == 1)) {
         /* packed: the units are the chunks, each scanned from S_in */
@@ -1715,12 +1721,12 @@ static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *
                        (const bf16x8 *)ws->QK, (const bf16x8 *)ws->KgT, (const float4 *)ws->U,
                        ws->Glast, ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk,
                        S_in, S_out, Hv, units, ws->O, tail);
-    const int rows = N * Hv;
-    const bool zvec = z_stride % 8 == 0 && ((uintptr_t)z & 15) == 0;
-    hipLaunchKernelGGL(zvec ? gdn_norm_gate_kernel<true> : gdn_norm_gate_kernel<false>,
-                       dim3((unsigned)CEIL_DIV(rows, 16)), dim3(256), 0, stream, ws->O,
-                       (const bf16 *)z, z_stride, norm_w, eps, rows, Hv, (bf16 *)y);
-    return hipGetLastError();
+    if (!norm) {
+        if (o_pending)
+            *o_pending = 1;
+        return hipGetLastError();
+    }
+    return k_gdn_norm_gate(ws->O, z, z_stride, norm_w, eps, N * Hv, Hv, y, stream);
 }
 
 extern "C" hipError_t k_gdn_scan(const float *q, const float *k, const float *v, const float *g,
@@ -1758,11 +1764,11 @@ extern "C" int cujev_gdn_recur_chosen(const cujev_chunks *ck, int Hv, int has_S_
     return (long)ck->num_segments * Hv <= 256 && ck->max_seg_len <= RC_MAXL;
 }
 
-extern "C" hipError_t k_gdn_recur(const bf16_t *proj, int proj_stride, const float *conv_w,
-                                  const float *conv_in, const float *A_neg_exp,
-                                  const float *dt_bias, const cujev_chunks *ck, const float *S_in,
-                                  const float *norm_w, float eps, int Hk, int Hv, bf16_t *y,
-                                  const cujev_gdn_scratch *ws, int N, hipStream_t stream) {
+static hipError_t gdn_recur(const bf16_t *proj, int proj_stride, const float *conv_w,
+                            const float *conv_in, const float *A_neg_exp, const float *dt_bias,
+                            const cujev_chunks *ck, const float *S_in, const float *norm_w,
+                            float eps, int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *ws,
+                            int N, hipStream_t stream, bool norm) {
     if (N <= 0 || ck->num_segments <= 0)
         return hipSuccess;
     if (Hk <= 0 || Hv % Hk != 0 || proj_stride % 8 != 0 || ((uintptr_t)proj & 15) != 0 ||
@@ -1775,23 +1781,30 @@ extern "C" hipError_t k_gdn_recur(const bf16_t *proj, int proj_stride, const flo
     hipLaunchKernelGGL(conv_in ? gdn_recur_kernel<true> : gdn_recur_kernel<false>,
                        dim3((unsigned)(4 * units)), dim3(RC_THREADS), 0, stream, cv,
                        ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, Hk, Hv, units, S_in, ws->O);
+    if (!norm)
+        return hipGetLastError();
     const int C = (2 * Hk + Hv) * DK;
-    const bf16_t *z = proj + C;
-    const int rows = N * Hv;
-    const bool zvec = proj_stride % 8 == 0 && ((uintptr_t)z & 15) == 0;
-    hipLaunchKernelGGL(zvec ? gdn_norm_gate_kernel<true> : gdn_norm_gate_kernel<false>,
-                       dim3((unsigned)CEIL_DIV(rows, 16)), dim3(256), 0, stream, ws->O,
-                       (const bf16 *)z, proj_stride, norm_w, eps, rows, Hv, (bf16 *)y);
-    return hipGetLastError();
+    return k_gdn_norm_gate(ws->O, proj + C, proj_stride, norm_w, eps, N * Hv, Hv, y, stream);
 }
 
-extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const float *conv_w,
-                                  const float *conv_in, float *conv_out, int seg0_len,
-                                  const int32_t *own_base, const float *A_neg_exp,
+extern "C" hipError_t k_gdn_recur(const bf16_t *proj, int proj_stride, const float *conv_w,
+                                  const float *conv_in, const float *A_neg_exp,
                                   const float *dt_bias, const cujev_chunks *ck, const float *S_in,
-                                  float *S_out, const float *norm_w, float eps, int Hk, int Hv,
-                                  bf16_t *y, const cujev_gdn_scratch *ws, int N,
-                                  hipStream_t stream) {
+                                  const float *norm_w, float eps, int Hk, int Hv, bf16_t *y,
+                                  const cujev_gdn_scratch *ws, int N, hipStream_t stream) {
+    return gdn_recur(proj, proj_stride, conv_w, conv_in, A_neg_exp, dt_bias, ck, S_in, norm_w,
+                     eps, Hk, Hv, y, ws, N, stream, true);
+}
+
+static hipError_t gdn_layer(const bf16_t *proj, int proj_stride, const float *conv_w,
+                            const float *conv_in, float *conv_out, int seg0_len,
+                            const int32_t *own_base, const float *A_neg_exp, const float *dt_bias,
+                            const cujev_chunks *ck, const float *S_in, float *S_out,
+                            const float *norm_w, float eps, int Hk, int Hv, bf16_t *y,
+                            const cujev_gdn_scratch *ws, int N, hipStream_t stream, bool norm,
+                            int *o_pending) {
+    if (o_pending)
+        *o_pending = 0;
     if (N <= 0)
         return hipSuccess;
     if (Hk <= 0 || Hv % Hk != 0 || (ck->chunk_starts && S_out) || proj_stride % 8 != 0 ||
@@ -1805,9 +1818,12 @@ extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const flo
                                seg0_len, C);
         return hipGetLastError();
     }
-    if (cujev_gdn_recur_chosen(ck, Hv, S_out != nullptr, conv_out != nullptr))
-        return k_gdn_recur(proj, proj_stride, conv_w, conv_in, A_neg_exp, dt_bias, ck, S_in,
-                           norm_w, eps, Hk, Hv, y, ws, N, stream);
+    if (cujev_gdn_recur_chosen(ck, Hv, S_out != nullptr, conv_out != nullptr)) {
+        if (o_pending)
+            *o_pending = !norm;
+        return gdn_recur(proj, proj_stride, conv_w, conv_in, A_neg_exp, dt_bias, ck, S_in,
+                         norm_w, eps, Hk, Hv, y, ws, N, stream, norm);
+    }
     const ConvSrc cv{(const bf16 *)proj, proj_stride, conv_w, conv_in, own_base,
                      A_neg_exp,          dt_bias,     N};
     /* the conv tail rides along with phase B */
@@ -1821,5 +1837,42 @@ extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const flo
                        ck->chunk_len, ck->chunk_starts, Hk, Hv, npairs, (bf16 *)ws->W,
                        (bf16 *)ws->Qg, (bf16 *)ws->QK, (bf16 *)ws->KgT, ws->U, ws->Glast);
     return gdn_phase_b(ck, S_in, S_out, proj + C, proj_stride, norm_w, eps, Hv, y, ws, N, tail,
-                       stream);
+                       stream, norm, o_pending);
+}
+
+extern "C" hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const float *conv_w,
+                                  const float *conv_in, float *conv_out, int seg0_len,
+                                  const int32_t *own_base, const float *A_neg_exp,
+                                  const float *dt_bias, const cujev_chunks *ck, const float *S_in,
+                                  float *S_out, const float *norm_w, float eps, int Hk, int Hv,
+                                  bf16_t *y, const cujev_gdn_scratch *ws, int N,
+                                  hipStream_t stream) {
+    return gdn_layer(proj, proj_stride, conv_w, conv_in, conv_out, seg0_len, own_base, A_neg_exp,
+                     dt_bias, ck, S_in, S_out, norm_w, eps, Hk, Hv, y, ws, N, stream, true,
+                     nullptr);
+}
+
+extern "C" hipError_t k_gdn_layer_o(const bf16_t *proj, int proj_stride, const float *conv_w,
+                                    const float *conv_in, float *conv_out, int seg0_len,
+                                    const int32_t *own_base, const float *A_neg_exp,
+                                    const float *dt_bias, const cujev_chunks *ck,
+                                    const float *S_in, float *S_out, const float *norm_w,
+                                    float eps, int Hk, int Hv, bf16_t *y,
+                                    const cujev_gdn_scratch *ws, int N, hipStream_t stream,
+                                    int *o_pending) {
+    return gdn_layer(proj, proj_stride, conv_w, conv_in, conv_out, seg0_len, own_base, A_neg_exp,
+                     dt_bias, ck, S_in, S_out, norm_w, eps, Hk, Hv, y, ws, N, stream, false,
+                     o_pending);
+}
+
+extern "C" hipError_t k_gdn_norm_gate(const float *o, const bf16_t *z, int z_stride,
+                                      const float *norm_w, float eps, int rows, int Hv, bf16_t *y,
+                                      hipStream_t stream) {
+    if (rows <= 0)
+        return hipSuccess;
+    const bool zvec = z_stride % 8 == 0 && ((uintptr_t)z & 15) == 0;
+    hipLaunchKernelGGL(zvec ? gdn_norm_gate_kernel<true> : gdn_norm_gate_kernel<false>,
+                       dim3((unsigned)CEIL_DIV(rows, 16)), dim3(256), 0, stream, o,
+                       (const bf16 *)z, z_stride, norm_w, eps, rows, Hv, (bf16 *)y);
+    return hipGetLastError();
 }

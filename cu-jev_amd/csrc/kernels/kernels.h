@@ -195,6 +195,21 @@ hipError_t k_gdn_layer(const bf16_t *proj, int proj_stride, const float *conv_w,
                        const cujev_chunks *chunks, const float *S_in, float *S_out,
                        const float *norm_w, float eps, int Hk, int Hv, bf16_t *y,
                        const cujev_gdn_scratch *scratch, int N, hipStream_t stream);
+/* k_gdn_layer up to its gated norm: where that norm would be a launch of its
+ * own, o (fp32 [N][Hv][128]) is left in scratch->O and *o_pending = 1, for
+ * one k_gdn_norm_gate over several calls' rows; where the scan kernel
+ * applies the norm itself, y is written and *o_pending = 0. */
+hipError_t k_gdn_layer_o(const bf16_t *proj, int proj_stride, const float *conv_w,
+                         const float *conv_in, float *conv_out, int seg0_len,
+                         const int32_t *own_base, const float *A_neg_exp, const float *dt_bias,
+                         const cujev_chunks *chunks, const float *S_in, float *S_out,
+                         const float *norm_w, float eps, int Hk, int Hv, bf16_t *y,
+                         const cujev_gdn_scratch *scratch, int N, hipStream_t stream,
+                         int *o_pending);
+/* The gated RMSNorm of k_gdn_scan over `rows` = tokens x Hv rows of o (fp32,
+ * 128 each): y[n, hv*128 + c] from o[n][hv] and z[n*z_stride + hv*128 + c]. */
+hipError_t k_gdn_norm_gate(const float *o, const bf16_t *z, int z_stride, const float *norm_w,
+                           float eps, int rows, int Hv, bf16_t *y, hipStream_t stream);
 
 /* Few-token branches (eval: every segment continues S_in, none writes a
  * final state or conv tail, no packed chunks, each at most
