@@ -184,12 +184,18 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
              * branch tokens: into the branch scratch, over the state's P keys
              * and their own */
             const bf16_t *bproj = m->proj + (size_t)ns * m->w_attn;
-            if (ns)
+            if (ns && nb) /* FUSED: one launch, each group into its cache */
+                K_TRY(k_attn_prep_pair(m->proj, m->w_attn, ly->q_norm, ly->k_norm, a->pos, ns, nb,
+                                       m->Hq, m->Hkv, c->rotary_dim, m->rope, eps, q_scale, m->q,
+                                       st->kv_k[l], st->kv_vt[l], m->state_stride, m->br_k,
+                                       m->br_vt, m->branch_stride, s),
+                      "attn_prep", l);
+            else if (ns)
                 K_TRY(k_attn_prep(m->proj, m->w_attn, ly->q_norm, ly->k_norm, a->pos, ns, m->Hq,
                                   m->Hkv, c->rotary_dim, m->rope, eps, q_scale, m->q, st->kv_k[l],
                                   st->kv_vt[l], m->state_stride, s),
                       "attn_prep", l);
-            if (nb)
+            else
                 K_TRY(k_attn_prep(bproj, m->w_attn, ly->q_norm, ly->k_norm, a->pos + ns, nb, m->Hq,
                                   m->Hkv, c->rotary_dim, m->rope, eps, q_scale,
                                   m->q + (size_t)ns * qrow, m->br_k, m->br_vt, m->branch_stride,

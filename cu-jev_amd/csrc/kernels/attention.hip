@@ -587,15 +587,24 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnPart part,
  * not the data, sets the time; 4 tokens keep it short and the grid wide. */
 constexpr int PREP_TOK = 4;
 
+/* Tokens [0, Na) write K / V^T to (kc, vtc, cs) columns n, the rest (from
+ * workgroup nblk_a on) to (kc2, vtc2, cs2) columns n - Na; a one-cache
+ * launch passes Na = N and nblk_a = gridDim.x. */
 __global__ __launch_bounds__(320) void attn_prep_kernel(
     const bf16 *__restrict__ proj, int ps, const float *__restrict__ qw, const float *__restrict__ kw,
     const int32_t *__restrict__ pos, int N, int Hq, int Hkv, int rot,
     const float2 *__restrict__ rope, float eps, float q_scale, bf16 *__restrict__ q_out,
-    bf16 *__restrict__ kc, bf16 *__restrict__ vtc, int cs) {
+    bf16 *__restrict__ kc, bf16 *__restrict__ vtc, int cs, int Na, int nblk_a,
+    bf16 *__restrict__ kc2, bf16 *__restrict__ vtc2, int cs2) {
     __shared__ bf16 vs[256][PREP_TOK + 8]; /* V^T staging [d][token] */
-    const int n0 = blockIdx.x * PREP_TOK, kh = blockIdx.y;
+    int blk = blockIdx.x, nend = Na, col0 = 0;
+    if (blk >= nblk_a) {
+        blk -= nblk_a, nend = N, col0 = Na;
+        kc = kc2, vtc = vtc2, cs = cs2;
+    }
+    const int n0 = col0 + blk * PREP_TOK, kh = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nt = min(PREP_TOK, N - n0);
+    const int nt = min(PREP_TOK, nend - n0);
     const int half_lanes = rot / 8; /* lanes holding the first rot/2 dims */
     const int hr = rot / 2;
 
@@ -675,7 +684,7 @@ __global__ __launch_bounds__(320) void attn_prep_kernel(
 #pragma unroll
             for (int e = 0; e < 4; e++)
                 o[e] = f2bf(x[e]);
-            *(bf16x4 *)(kc + ((size_t)kh * cs + nn) * 256 + 4 * lane) = o;
+            *(bf16x4 *)(kc + ((size_t)kh * cs + nn - col0) * 256 + 4 * lane) = o;
         }
     }
 
@@ -697,7 +706,7 @@ __global__ __launch_bounds__(320) void attn_prep_kernel(
     typedef __bf16 bf16xVP __attribute__((ext_vector_type(VP)));
     for (int idx = threadIdx.x; idx < 256 * NPC; idx += 320) {
         const int d = idx / NPC, c = idx % NPC;
-        bf16 *dst = vtc + ((size_t)kh * 256 + d) * cs + n0 + VP * c;
+        bf16 *dst = vtc + ((size_t)kh * 256 + d) * cs + (n0 - col0) + VP * c;
         if (VP * c + VP <= nt) {
             *(bf16xVP *)dst = *(const bf16xVP *)&vs[d][VP * c];
         } else {
@@ -720,11 +729,34 @@ extern "C" hipError_t k_attn_prep(const bf16_t *proj, int proj_stride, const flo
         return hipSuccess;
     if (Hq != 4 * Hkv || rot > 64 || rot % 8 != 0)
         return hipErrorInvalidValue;
-    dim3 grid((unsigned)CEIL_DIV(N, PREP_TOK), (unsigned)Hkv);
-    hipLaunchKernelGGL(attn_prep_kernel, grid, dim3(320), 0, stream, (const bf16 *)proj,
-                       proj_stride, q_norm_w, k_norm_w, pos, N, Hq, Hkv, rot,
+    const int nblk = CEIL_DIV(N, PREP_TOK);
+    hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)nblk, (unsigned)Hkv), dim3(320), 0, stream,
+                       (const bf16 *)proj, proj_stride, q_norm_w, k_norm_w, pos, N, Hq, Hkv, rot,
                        (const float2 *)rope_table, eps, q_scale, (bf16 *)q_out, (bf16 *)k_cache,
+                       (bf16 *)vt_cache, cache_stride, N, nblk, (bf16 *)k_cache,
                        (bf16 *)vt_cache, cache_stride);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t k_attn_prep_pair(const bf16_t *proj, int proj_stride,
+                                       const float *q_norm_w, const float *k_norm_w,
+                                       const int32_t *pos, int Na, int Nb, int Hq, int Hkv,
+                                       int rot, const float *rope_table, float eps, float q_scale,
+                                       bf16_t *q_out, bf16_t *k_cache, bf16_t *vt_cache,
+                                       int cache_stride, bf16_t *k_cache2, bf16_t *vt_cache2,
+                                       int cache_stride2, hipStream_t stream) {
+    if (Na < 0 || Nb < 0)
+        return hipErrorInvalidValue;
+    if (Na + Nb <= 0)
+        return hipSuccess;
+    if (Hq != 4 * Hkv || rot > 64 || rot % 8 != 0)
+        return hipErrorInvalidValue;
+    const int na = CEIL_DIV(Na, PREP_TOK), nb = CEIL_DIV(Nb, PREP_TOK);
+    hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)(na + nb), (unsigned)Hkv), dim3(320), 0,
+                       stream, (const bf16 *)proj, proj_stride, q_norm_w, k_norm_w, pos, Na + Nb,
+                       Hq, Hkv, rot, (const float2 *)rope_table, eps, q_scale, (bf16 *)q_out,
+                       (bf16 *)k_cache, (bf16 *)vt_cache, cache_stride, Na, na, (bf16 *)k_cache2,
+                       (bf16 *)vt_cache2, cache_stride2);
     return hipGetLastError();
 }
 

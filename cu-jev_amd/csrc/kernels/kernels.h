@@ -53,6 +53,15 @@ hipError_t k_attn_prep(const bf16_t *proj, int proj_stride, const float *q_norm_
                        const float *k_norm_w, const int32_t *pos, int N, int Hq, int Hkv, int rot,
                        const float *rope_table, float eps, float q_scale, bf16_t *q_out,
                        bf16_t *k_cache, bf16_t *vt_cache, int cache_stride, hipStream_t stream);
+/* The same over Na + Nb tokens in one launch: K / V^T of tokens [0, Na) go
+ * to columns n of (k_cache, vt_cache), those of tokens [Na, Na + Nb) to
+ * columns n - Na of (k_cache2, vt_cache2); q_out rows are n throughout. */
+hipError_t k_attn_prep_pair(const bf16_t *proj, int proj_stride, const float *q_norm_w,
+                            const float *k_norm_w, const int32_t *pos, int Na, int Nb, int Hq,
+                            int Hkv, int rot, const float *rope_table, float eps, float q_scale,
+                            bf16_t *q_out, bf16_t *k_cache, bf16_t *vt_cache, int cache_stride,
+                            bf16_t *k_cache2, bf16_t *vt_cache2, int cache_stride2,
+                            hipStream_t stream);
 
 /* out[n, h*256 + d] = sigmoid(gate[n*gate_tok_stride + h*gate_head_stride + d])
  *                     * softmax_j(q[n,h] . k_j) v_j          (base-2 softmax)

@@ -158,6 +158,23 @@ EXPORT int cujev_op_attn_prep(const void *proj, int proj_stride, const float *q_
                     "attn_prep");
 }
 
+EXPORT int cujev_op_attn_prep_pair(const void *proj, int proj_stride, const float *q_norm_w,
+                                   const float *k_norm_w, const int32_t *pos, int Na, int Nb,
+                                   int Hq, int Hkv, int rot, const float *rope_table, float eps,
+                                   float q_scale, void *q_out, void *k_cache, void *vt_cache,
+                                   int cache_stride, void *k_cache2, void *vt_cache2,
+                                   int cache_stride2, void *stream) {
+    if (Na < 0 || Nb < 0 || Hkv <= 0 || rot <= 0 || rot > 64 || cache_stride % 64 ||
+        cache_stride2 % 64 || !rope_table)
+        return fail(1, "attn_prep_pair: bad arguments");
+    return launched(k_attn_prep_pair((const bf16_t *)proj, proj_stride, q_norm_w, k_norm_w, pos,
+                                     Na, Nb, Hq, Hkv, rot, rope_table, eps, q_scale,
+                                     (bf16_t *)q_out, (bf16_t *)k_cache, (bf16_t *)vt_cache,
+                                     cache_stride, (bf16_t *)k_cache2, (bf16_t *)vt_cache2,
+                                     cache_stride2, (hipStream_t)stream),
+                    "attn_prep_pair");
+}
+
 EXPORT int cujev_op_attention(const void *q, const void *gate, int gate_tok_stride,
                               int gate_head_stride, const void *pk, const void *pvt, int P,
                               int p_stride, const void *ok, const void *ovt, int o_stride,

@@ -31,6 +31,8 @@ _SIGS = {
     "cujev_op_gemm": [_P, _P, _P, _I, _I, _I, _I, _P, C.c_size_t, _P],
     "cujev_op_rope_table": [_D, _I, _I, _P],
     "cujev_op_attn_prep": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _F, _F, _P, _P, _P, _I, _P],
+    "cujev_op_attn_prep_pair": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _F, _P, _P, _P,
+                                _I, _P, _P, _I, _P],
     "cujev_op_attention": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P],
     "cujev_op_attention_ws": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P,
                               C.c_size_t, _P],
@@ -137,6 +139,17 @@ def attn_prep(proj, q_norm_w, k_norm_w, pos, Hq, Hkv, rot, rope, eps, q_scale,
     _call("cujev_op_attn_prep", _ptr(proj), proj.stride(0), _ptr(q_norm_w), _ptr(k_norm_w),
           _ptr(pos), N, Hq, Hkv, rot, _ptr(rope), float(eps), float(q_scale), _ptr(q_out),
           _ptr(k_cache), _ptr(vt_cache), cache_stride, _stream())
+
+
+def attn_prep_pair(proj, q_norm_w, k_norm_w, pos, Na, Hq, Hkv, rot, rope, eps, q_scale, q_out,
+                   k_cache, vt_cache, cache_stride, k_cache2, vt_cache2, cache_stride2):
+    """attn_prep of rows [0, Na) into (k_cache, vt_cache) and of the rest into
+    (k_cache2, vt_cache2), one launch."""
+    Nb = proj.shape[0] - Na
+    _call("cujev_op_attn_prep_pair", _ptr(proj), proj.stride(0), _ptr(q_norm_w), _ptr(k_norm_w),
+          _ptr(pos), int(Na), int(Nb), Hq, Hkv, rot, _ptr(rope), float(eps), float(q_scale),
+          _ptr(q_out), _ptr(k_cache), _ptr(vt_cache), cache_stride, _ptr(k_cache2),
+          _ptr(vt_cache2), cache_stride2, _stream())
 
 
 def attention_ws_bytes(N, Hq, Hkv, P) -> int:

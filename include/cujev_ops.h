@@ -114,6 +114,18 @@ int cujev_op_attn_prep(const void *proj, int proj_stride, const float *q_norm_w,
                        int rot, const float *rope_table, float eps, float q_scale, void *q_out,
                        void *k_cache, void *vt_cache, int cache_stride, void *stream);
 
+/* The same over Na + Nb tokens in one launch (no counterpart in the
+ * reference; the engine's deferred-prefill pass writes the state's tokens
+ * and the branches' this way): K rows / V^T columns of tokens [0, Na) go to
+ * column n of (k_cache, vt_cache), those of the rest to column n - Na of
+ * (k_cache2, vt_cache2); q_out rows are n throughout. The same bits as two
+ * cujev_op_attn_prep calls. */
+int cujev_op_attn_prep_pair(const void *proj, int proj_stride, const float *q_norm_w,
+                            const float *k_norm_w, const int32_t *pos, int Na, int Nb, int Hq,
+                            int Hkv, int rot, const float *rope_table, float eps, float q_scale,
+                            void *q_out, void *k_cache, void *vt_cache, int cache_stride,
+                            void *k_cache2, void *vt_cache2, int cache_stride2, void *stream);
+
 /* Replaces reference src/kernels/kernels.h:203-206 (k_attention).
  * out bf16 [N][Hq*256] = sigmoid(gate) * softmax2(q.k) v over the state keys
  * [0,P) of (pk, pvt) and own keys [own_base[n], n] of (ok, ovt).

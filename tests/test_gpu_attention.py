@@ -279,6 +279,41 @@ def test_attn_prep_matches_oracle():
     np.testing.assert_array_equal(np32(vtc)[:, :, :N].transpose(2, 0, 1), rv.astype(np.float32))
 
 
+@pytest.mark.parametrize("Na,Nb", [(530, 80), (17, 33), (4, 1)])
+def test_attn_prep_pair_equals_two_launches(Na, Nb):
+    """The deferred-prefill pass's prep: rows [0, Na) into the state cache,
+    the rest into the branch scratch at their own columns; the same bits as
+    two launches (Na not a multiple of the 4-token workgroup included)."""
+    o = ops()
+    rng = np.random.default_rng(Na * 3 + Nb)
+    Hq, Hkv, rot, theta, eps = 16, 4, 64, 1e7, 1e-6
+    N = Na + Nb
+    W = Hq * 2 * D + 2 * Hkv * D
+    dev = "cuda"
+    proj = bf(rng.standard_normal((N, W))).to(dev)
+    qn = torch.as_tensor((1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)).to(dev)
+    kn = torch.as_tensor((1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)).to(dev)
+    pos = torch.as_tensor(np.concatenate([np.arange(Na), Na + np.arange(Nb) % 7]).astype(np.int32)).to(dev)
+    rope = o.rope_table(theta, rot, N + 8)
+    qs = orc.LOG2E / 16.0
+    sa, sb = o.kv_stride(Na), o.kv_stride(Nb)
+
+    def bufs():
+        return (torch.empty(N, Hq, D, dtype=torch.bfloat16, device=dev),
+                torch.zeros(Hkv, sa, D, dtype=torch.bfloat16, device=dev),
+                torch.zeros(Hkv, D, sa, dtype=torch.bfloat16, device=dev),
+                torch.zeros(Hkv, sb, D, dtype=torch.bfloat16, device=dev),
+                torch.zeros(Hkv, D, sb, dtype=torch.bfloat16, device=dev))
+    q1, ka, va, kb, vb = bufs()
+    o.attn_prep_pair(proj, qn, kn, pos, Na, Hq, Hkv, rot, rope, eps, qs, q1, ka, va, sa, kb, vb, sb)
+    q2, ka2, va2, kb2, vb2 = bufs()
+    o.attn_prep(proj[:Na], qn, kn, pos[:Na], Hq, Hkv, rot, rope, eps, qs, q2[:Na], ka2, va2, sa)
+    o.attn_prep(proj[Na:], qn, kn, pos[Na:], Hq, Hkv, rot, rope, eps, qs, q2[Na:], kb2, vb2, sb)
+    torch.cuda.synchronize()
+    for x, y in ((q1, q2), (ka, ka2), (va, va2), (kb, kb2), (vb, vb2)):
+        assert torch.equal(x, y)
+
+
 @pytest.mark.parametrize("rows", [64])
 def test_attention_capacity_shape(rows):
     """Config 3 shape (Hq 16 / Hkv 4, state 8192, 256 branches x 16) against a
