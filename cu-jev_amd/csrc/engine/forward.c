@@ -177,6 +177,12 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
         const bf16_t *ry; /* what the residual add reads: bf16 rows or split-K partials */
         const float *ryp;
         int rsp;
+        /* Past the last layer's mixer only each segment's last token reaches
+         * the outputs: the state's rows need nothing more (a PREFILL ends
+         * there), and the branches' final rows go on alone. */
+        const int last = l + 1 == c->num_layers;
+        const bf16_t *w_res, *wt_res; /* the mixer's output projection */
+        int k_res;
         if (ly->type == CUJEV_LAYER_FULL) {
             K_TRY(proj_gemm(m, m->xb, ly->w_qkv, ly->wt_qkv, m->proj, N, m->w_attn, H), "gemm qkv",
                   l);
@@ -201,28 +207,29 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
                                   m->q + (size_t)ns * qrow, m->br_k, m->br_vt, m->branch_stride,
                                   s),
                       "attn_prep", l);
-            if (ns && nb) /* FUSED: both groups in one launch, side by side */
+            /* whose attention output is read: the state's rows only before
+             * the last layer */
+            const int att_s = ns && !last, att_b = nb > 0;
+            if (att_s && att_b) /* FUSED: both groups in one launch, side by side */
                 K_TRY(k_attention_pair(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l],
                                        st->kv_vt[l], m->state_stride, a->base, m->mix_out, m->Hq,
                                        m->Hkv, ns, 0, st->kv_k[l], st->kv_vt[l], m->state_stride,
                                        nb, P, m->br_k, m->br_vt, m->branch_stride, s),
                       "attention", l);
-            else if (ns)
+            else if (att_s)
                 K_TRY(k_attention(m->q, m->proj + m->D, m->w_attn, 2 * m->D, st->kv_k[l],
                                   st->kv_vt[l], 0, m->state_stride, st->kv_k[l], st->kv_vt[l],
                                   m->state_stride, a->base, ns, m->Hq, m->Hkv, m->mix_out,
                                   m->attn_ws, m->attn_ws_bytes, s),
                       "attention", l);
-            else
+            else if (att_b)
                 K_TRY(k_attention(m->q + (size_t)ns * qrow, bproj + m->D, m->w_attn, 2 * m->D,
                                   st->kv_k[l], st->kv_vt[l], P, m->state_stride, m->br_k,
                                   m->br_vt, m->branch_stride, a->base + ns, nb, m->Hq, m->Hkv,
                                   m->mix_out + (size_t)ns * qrow, m->attn_ws, m->attn_ws_bytes,
                                   s),
                       "attention", l);
-            K_TRY(resid_gemm(m, m->mix_out, ly->w_o, ly->wt_o, N, H, m->Hq * m->D, 0, &ry, &ryp,
-                             &rsp),
-                  "gemm o", l);
+            w_res = ly->w_o, wt_res = ly->wt_o, k_res = m->Hq * m->D;
         } else {
             K_TRY(proj_gemm(m, m->xb, ly->w_in, ly->wt_in, m->proj, N, m->w_gdn, H), "gemm in", l);
             /* state tokens write the state's final S and conv tail; branch
@@ -256,23 +263,31 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
                 K_TRY(k_gdn_norm_gate(gws_b.O, z + (size_t)ns * zs, zs, ly->g_norm, eps,
                                       nb * m->Hv, m->Hv, m->mix_out + (size_t)ns * m->V, s),
                       "gdn_norm", l);
-            K_TRY(resid_gemm(m, m->mix_out, ly->w_out, ly->wt_out, N, H, m->V, 0, &ry, &ryp,
-                             &rsp),
-                  "gemm out", l);
+            w_res = ly->w_out, wt_res = ly->wt_out, k_res = m->V;
         }
-        K_TRY(k_add_rmsnorm(m->x, ry, ryp, rsp, ly->post_norm, m->xb, N, H, eps, NULL, 0, s),
+        if (last && mode == CUJEV_FWD_PREFILL)
+            break;
+        int n = N; /* rows past the mixer */
+        const bf16_t *mix = m->mix_out;
+        float *x = m->x;
+        if (last) { /* the segments' last tokens, gathered */
+            K_TRY(k_gather_rows(m->mix_out, (size_t)k_res * 2, a->rows, B, m->mixl,
+                                (size_t)k_res * 2, (size_t)k_res * 2, s),
+                  "gather", l);
+            K_TRY(k_gather_rows(m->x, (size_t)H * 4, a->rows, B, m->xl, (size_t)H * 4,
+                                (size_t)H * 4, s),
+                  "gather", l);
+            n = B, mix = m->mixl, x = m->xl;
+        }
+        K_TRY(resid_gemm(m, mix, w_res, wt_res, n, H, k_res, 0, &ry, &ryp, &rsp), "gemm o/out", l);
+        K_TRY(k_add_rmsnorm(x, ry, ryp, rsp, ly->post_norm, m->xb, n, H, eps, NULL, 0, s),
               "add+norm", l);
-        K_TRY(gate_up_gemm(m, ly, N, I, H), "gemm gate_up", l);
-        K_TRY(resid_gemm(m, m->act, ly->w_down, ly->wt_down, N, H, I, 1, &ry, &ryp, &rsp),
+        K_TRY(gate_up_gemm(m, ly, n, I, H), "gemm gate_up", l);
+        K_TRY(resid_gemm(m, m->act, ly->w_down, ly->wt_down, n, H, I, 1, &ry, &ryp, &rsp),
               "gemm down", l);
-        if (l + 1 < c->num_layers)
-            K_TRY(k_add_rmsnorm(m->x, ry, ryp, rsp, m->layers[l + 1].in_norm, m->xb, N, H, eps,
-                                NULL, 0, s),
-                  "add+norm", l);
-        else /* final norm only at the last token of every segment */
-            K_TRY(k_add_rmsnorm(m->x, ry, ryp, rsp, m->final_norm, m->hsel, N, H, eps, a->rows, B,
-                                s),
-                  "final norm", l);
+        K_TRY(k_add_rmsnorm(x, ry, ryp, rsp, last ? m->final_norm : m->layers[l + 1].in_norm,
+                            last ? m->hsel : m->xb, n, H, eps, NULL, 0, s),
+              last ? "final norm" : "add+norm", l);
     }
     if (a->cand)
         K_TRY(k_readout(m->hsel, m->lm_head, a->cand, a->ncand, a->maxc, m->d_logits, a->maxc, B,

@@ -293,7 +293,8 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
     const size_t N = (size_t)m->max_tokens, H = (size_t)c->hidden_size,
                  I = (size_t)c->intermediate_size;
     const size_t B = (size_t)(m->opts.max_branches > 0 ? m->opts.max_branches : 1);
-    const size_t mix = N * (size_t)((m->Hq * m->D > m->V) ? m->Hq * m->D : m->V);
+    const size_t mixw = (size_t)((m->Hq * m->D > m->V) ? m->Hq * m->D : m->V);
+    const size_t mix = N * mixw;
     const size_t br_kv = (size_t)m->Hkv * m->branch_stride * m->D * 2;
     m->max_chunks = m->max_tokens / 64 + (int)B + 1;
     /* + 8: a FUSED call's second (one-segment) chunk table heads */
@@ -330,6 +331,8 @@ cujev_status cujev_model_alloc_workspace(cujev_model *m) {
          cujev_gdn_scratch_bytes(m->max_chunks, m->Hv, m->max_tokens) + 4096},
         {(void **)&m->act, N * I * 2},
         {(void **)&m->hsel, B * H * 2},
+        {(void **)&m->xl, B * H * 4},
+        {(void **)&m->mixl, B * mixw * 2},
         {(void **)&m->full_logits, B * (size_t)c->vocab_size * 4},
         {(void **)&m->gemm_ws, m->gemm_ws_bytes},
         {(void **)&m->d_meta, m->meta_ints * 4},

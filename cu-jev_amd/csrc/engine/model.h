@@ -98,6 +98,11 @@ struct cujev_model {
     void *gdn_scratch;
     bf16_t *act;  /* [N, I] */
     bf16_t *hsel; /* [B, H] */
+    /* the last layer past its mixer runs on the B rows that reach the
+     * outputs, gathered here: residual fp32 [B][H], mixer output bf16
+     * [B][max(Hq*256, V)] */
+    float *xl;
+    bf16_t *mixl;
     float *full_logits; /* [B, vocab] */
     void *gemm_ws;
     size_t gemm_ws_bytes;

@@ -25,6 +25,19 @@ __global__ __launch_bounds__(NT) void embed_kernel(const int32_t *__restrict__ t
     }
 }
 
+/* dst row r = src row rows[r], 16-byte pieces (the last layer's rows that
+ * reach the outputs) */
+__global__ __launch_bounds__(NT) void gather_rows_kernel(const unsigned char *__restrict__ src,
+                                                         size_t src_pitch,
+                                                         const int32_t *__restrict__ rows,
+                                                         unsigned char *__restrict__ dst,
+                                                         size_t dst_pitch, int pieces) {
+    const uint4 *s = (const uint4 *)(src + (size_t)rows[blockIdx.x] * src_pitch);
+    uint4 *d = (uint4 *)(dst + (size_t)blockIdx.x * dst_pitch);
+    for (int i = threadIdx.x; i < pieces; i += NT)
+        d[i] = s[i];
+}
+
 /* One block per output row r (source row rows ? rows[r] : r):
  *   v = x[src] + d (d from bf16 y, or bf16 of the split-K partial sum of yp);
  *   x[src] = v when there is a d and !rows;
@@ -194,6 +207,20 @@ extern "C" hipError_t k_add_rmsnorm(float *x, const bf16_t *y, const float *yp, 
     default: return hipErrorInvalidValue;
     }
 #undef CUJEV_RN_LAUNCH
+    return hipGetLastError();
+}
+
+extern "C" hipError_t k_gather_rows(const void *src, size_t src_pitch, const int32_t *rows, int R,
+                                    void *dst, size_t dst_pitch, size_t row_bytes,
+                                    hipStream_t s) {
+    if (R <= 0)
+        return hipSuccess;
+    if (row_bytes % 16 || src_pitch % 16 || dst_pitch % 16 || ((uintptr_t)src & 15) ||
+        ((uintptr_t)dst & 15))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)R), dim3(NT), 0, s,
+                       (const unsigned char *)src, src_pitch, rows, (unsigned char *)dst,
+                       dst_pitch, (int)(row_bytes / 16));
     return hipGetLastError();
 }
 

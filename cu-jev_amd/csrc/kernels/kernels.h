@@ -254,6 +254,11 @@ hipError_t k_add_rmsnorm(float *x, const bf16_t *y, const float *yp, int splits,
                          bf16_t *out, int N, int H, float eps, const int32_t *rows, int R,
                          hipStream_t s);
 
+/* dst row r = src row rows[r] for r < R (row_bytes each; rows, pitches and
+ * pointers 16-byte aligned). */
+hipError_t k_gather_rows(const void *src, size_t src_pitch, const int32_t *rows, int R, void *dst,
+                         size_t dst_pitch, size_t row_bytes, hipStream_t s);
+
 /* act[N,I] = bf16(silu(gu[:, :I]) * gu[:, I:])  (REF elementwise.cu:42-54). */
 hipError_t k_silu_mul(const bf16_t *gu, bf16_t *act, int N, int I, hipStream_t s);
 
