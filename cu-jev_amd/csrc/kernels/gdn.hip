@@ -1471,16 +1471,27 @@ __global__ __launch_bounds__(RC_THREADS, 2) void gdn_recur_kernel(
                              : (2 * Hk + hv) * DK + RC_COLS * cb + ch - 2 * DK;
     };
 
-    /* ---- stage: rows, gates; weights, tail and the state in registers ---- */
-    for (int i = tid; i < L * (RC_CH / 8); i += RC_THREADS) {
-        const int r = i / (RC_CH / 8), ch = 8 * (i - r * (RC_CH / 8));
-        *(bf16x8 *)&sm.x[r][ch] = ld8(cv.proj + (size_t)(t0 + r) * cv.ps + gch(ch));
+    /* ---- every global load first (one memory latency, not one per stage):
+     * the segment's rows into registers, the gates' inputs, this thread's
+     * conv weights and tail, and its slice of the state ---- */
+    constexpr int XP = CEIL_DIV(RC_MAXL * (RC_CH / 8), RC_THREADS); /* row pieces per thread */
+    const int npieces = L * (RC_CH / 8);
+    bf16x8 xr[XP];
+#pragma unroll
+    for (int k = 0; k < XP; k++) {
+        const int i = tid + k * RC_THREADS;
+        if (i < npieces) {
+            const int rr = i / (RC_CH / 8), ch = 8 * (i - rr * (RC_CH / 8));
+            xr[k] = ld8(cv.proj + (size_t)(t0 + rr) * cv.ps + gch(ch));
+        }
     }
+    float b_raw = 0.f, a_raw = 0.f;
     if (tid < L) {
         const bf16 *ab = cv.proj + (size_t)(t0 + tid) * cv.ps + C + Hv * DV;
-        sm.beta[tid] = sigmoid_f(bf2f(ab[hv]));
-        sm.g[tid] = cv.A_neg_exp[hv] * softplus_f(bf2f(ab[Hv + hv]) + cv.dt_bias[hv]);
+        b_raw = bf2f(ab[hv]);
+        a_raw = bf2f(ab[Hv + hv]);
     }
+    const float A_neg = cv.A_neg_exp[hv], dtb = cv.dt_bias[hv];
     /* thread t convolves q/k channel t, and v channel t when t < RC_COLS */
     const int gq = gch(tid), gv = gch(2 * DK + (tid & (RC_COLS - 1)));
     const float4 wq = *(const float4 *)(cv.conv_w + (size_t)gq * 4);
@@ -1496,20 +1507,41 @@ __global__ __launch_bounds__(RC_THREADS, 2) void gdn_recur_kernel(
 #pragma unroll
     for (int i = 0; i < 16; i++)
         S[i] = S_in ? S_in[((size_t)hv * DK + 16 * r + i) * DV + RC_COLS * cb + colw] : 0.f;
+#pragma unroll
+    for (int k = 0; k < XP; k++) {
+        const int i = tid + k * RC_THREADS;
+        if (i < npieces) {
+            const int rr = i / (RC_CH / 8), ch = 8 * (i - rr * (RC_CH / 8));
+            *(bf16x8 *)&sm.x[rr][ch] = xr[k];
+        }
+    }
+    if (tid < L) {
+        sm.beta[tid] = sigmoid_f(b_raw);
+        sm.g[tid] = A_neg * softplus_f(a_raw + dtb);
+    }
     lds_barrier();
 
-    /* ---- conv + SiLU, a sliding window per channel ---- */
+    /* ---- conv + SiLU, a sliding window per channel: the channel's inputs
+     * of every row slot are read first (rows past L hold no token and are
+     * not used), so the window runs on registers ---- */
     {
+        float xin[RC_MAXL];
+#pragma unroll
+        for (int j = 0; j < RC_MAXL; j++)
+            xin[j] = bf2f(sm.x[j][tid]);
         float x3 = tq[0], x2 = tq[1], x1 = tq[2]; /* inputs of tokens -3, -2, -1 */
         float *dst = tid < DK ? &sm.q[0][tid] : &sm.k[0][tid - DK];
-        for (int j = 0; j < L; j++) {
-            const float x0 = bf2f(sm.x[j][tid]);
-            float y = fmaf(wq.x, x3, 0.f);
-            y = fmaf(wq.y, x2, y);
-            y = fmaf(wq.z, x1, y);
-            y = fmaf(wq.w, x0, y);
-            dst[j * DK] = silu_f(y);
-            x3 = x2, x2 = x1, x1 = x0;
+#pragma unroll
+        for (int j = 0; j < RC_MAXL; j++) {
+            if (j < L) {
+                const float x0 = xin[j];
+                float y = fmaf(wq.x, x3, 0.f);
+                y = fmaf(wq.y, x2, y);
+                y = fmaf(wq.z, x1, y);
+                y = fmaf(wq.w, x0, y);
+                dst[j * DK] = silu_f(y);
+                x3 = x2, x2 = x1, x1 = x0;
+            }
         }
     }
     if (tid < 4 * RC_COLS) { /* v: channel tid % 32, token quarter tid / 32 */
@@ -1574,41 +1606,59 @@ __global__ __launch_bounds__(RC_THREADS, 2) void gdn_recur_kernel(
      * directly and sigma restarts at 1. */
     float *orow = o + (size_t)hv * DV + RC_COLS * cb + colw;
     float sigma = 1.f;
-    for (int j = 0; j < L; j++) {
+    /* a token's operands from LDS; read one token ahead of its use (they do
+     * not depend on the state), two buffers alternating */
+    struct StepOps {
         float kq[16], qq[16];
+        float g, beta, v, kqd;
+    };
+    auto load_ops = [&](int j, StepOps &op) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const float4 a = *(const float4 *)&sm.k[j][16 * r + 4 * e];
             const float4 b = *(const float4 *)&sm.q[j][16 * r + 4 * e];
-            kq[4 * e] = a.x, kq[4 * e + 1] = a.y, kq[4 * e + 2] = a.z, kq[4 * e + 3] = a.w;
-            qq[4 * e] = b.x, qq[4 * e + 1] = b.y, qq[4 * e + 2] = b.z, qq[4 * e + 3] = b.w;
+            op.kq[4 * e] = a.x, op.kq[4 * e + 1] = a.y, op.kq[4 * e + 2] = a.z, op.kq[4 * e + 3] = a.w;
+            op.qq[4 * e] = b.x, op.qq[4 * e + 1] = b.y, op.qq[4 * e + 2] = b.z, op.qq[4 * e + 3] = b.w;
         }
-        const float eg = fast_exp(sm.g[j]);
+        op.g = sm.g[j], op.beta = sm.beta[j], op.v = sm.v[j][colw], op.kqd = sm.kq[j];
+    };
+    auto step = [&](int j, const StepOps &op) {
+        const float eg = fast_exp(op.g);
         float pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            pk[i & 3] = fmaf(kq[i], S[i], pk[i & 3]);
-            pq[i & 3] = fmaf(qq[i], S[i], pq[i & 3]);
+            pk[i & 3] = fmaf(op.kq[i], S[i], pk[i & 3]);
+            pq[i & 3] = fmaf(op.qq[i], S[i], pq[i & 3]);
         }
         const float kS = sigma * sum_lanes8((pk[0] + pk[1]) + (pk[2] + pk[3]));
         const float qS = sigma * sum_lanes8((pq[0] + pq[1]) + (pq[2] + pq[3]));
-        const float vn = sm.beta[j] * (sm.v[j][colw] - eg * kS);
-        const float os = fmaf(eg, qS, vn * sm.kq[j]);
+        const float vn = op.beta * (op.v - eg * kS);
+        const float os = fmaf(eg, qS, vn * op.kqd);
         if (r == 0)
             orow[(size_t)(t0 + j) * Hv * DV] = os;
         const float sn = sigma * eg;
         if (sn < 0x1p-40f) { /* wave-uniform: fold the decay into St */
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                S[i] = fmaf(sn, S[i], kq[i] * vn);
+                S[i] = fmaf(sn, S[i], op.kq[i] * vn);
             sigma = 1.f;
         } else {
             const float w = vn * __builtin_amdgcn_rcpf(sn);
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                S[i] = fmaf(kq[i], w, S[i]);
+                S[i] = fmaf(op.kq[i], w, S[i]);
             sigma = sn;
         }
+    };
+    StepOps opa, opb;
+    load_ops(0, opa);
+    for (int j = 0; j < L; j += 2) { /* past the end: row L - 1 again, unused */
+        load_ops(min(j + 1, L - 1), opb);
+        step(j, opa);
+        if (j + 1 >= L)
+            break;
+        load_ops(min(j + 2, L - 1), opa);
+        step(j + 1, opb);
     }
 }
 
