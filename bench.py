@@ -137,19 +137,21 @@ def run_e2e(ckpt, steps, warmup, wl="config4", seed=0, full_logits=True):
                 first_out=first_out, first_full=first_full, info=info, checks=checks)
 
 
-# The reference's own benchmark shapes for the 4B model (tools/bench.c:41-74;
-# its published RTX 5090 rows, README.md:233-234): prefill P tokens, then one
+# The reference's own benchmark shapes (tools/bench.c:41-74; its published
+# RTX 5090 rows, README.md:233-235, 4B and 9B): prefill P tokens, then one
 # eval of B branches x L tokens with C candidates each, timed by the
 # library's own GPU timing (cujev_last_timing), decisions/s = B / eval time.
 REF_BENCH_SHAPES = [
-    {"P": 1024, "B": 16, "L": 40, "C": 8,
+    {"model": "4b", "P": 1024, "B": 16, "L": 40, "C": 8,
      "rtx5090": {"prefill_ms": 60.0, "eval_ms": 37.0, "decisions_per_s": 430}},
-    {"P": 8192, "B": 64, "L": 40, "C": 8,
+    {"model": "4b", "P": 8192, "B": 64, "L": 40, "C": 8,
      "rtx5090": {"prefill_ms": 550.0, "eval_ms": 185.0, "decisions_per_s": 350}},
+    {"model": "9b", "P": 1024, "B": 16, "L": 40, "C": 8,
+     "rtx5090": {"prefill_ms": 106.0, "eval_ms": 61.0, "decisions_per_s": 262}},
 ]
 
 
-def run_ref_shapes(ckpt, iters=5):
+def run_ref_shapes(ckpt, model="4b", iters=5):
     """tools/bench.c's method on this engine: deterministic token ids
     1000 + (7919 i mod 50000), candidates 32..32+C-1, one warm-up, then the
     mean of `iters` prefill and eval timings."""
@@ -158,7 +160,7 @@ def run_ref_shapes(ckpt, iters=5):
     eng = Engine(ckpt, max_state_tokens=8192, max_branch_tokens=4096, max_branches=256,
                  max_candidates=256)
     try:
-        for sh in REF_BENCH_SHAPES:
+        for sh in [x for x in REF_BENCH_SHAPES if x["model"] == model]:
             P, B, L, C = sh["P"], sh["B"], sh["L"], sh["C"]
             tok = [1000 + (i * 7919) % 50000 for i in range(P + B * L)]
             cands = list(range(32, 32 + C))
@@ -172,7 +174,8 @@ def run_ref_shapes(ckpt, iters=5):
                 eng.eval(brs)
                 ev += eng.last_timing().eval_ms
             pre, ev = pre / iters, ev / iters
-            out.append({"state_tokens": P, "branches": B, "branch_tokens": L, "candidates": C,
+            out.append({"model": model, "state_tokens": P, "branches": B, "branch_tokens": L,
+                        "candidates": C,
                         "prefill_ms": round(pre, 3), "prefill_tok_per_s": round(P / pre * 1e3),
                         "eval_ms": round(ev, 3), "decisions_per_s": round(B / ev * 1e3, 1),
                         "iters": iters, "reference_rtx5090": sh["rtx5090"]})
@@ -185,8 +188,9 @@ def e2e_child(a):
     """--e2e-child: the request loop without torch in the process; prints one
     JSON line, the full-vocabulary logits go to a .npy file."""
     assert "torch" not in sys.modules
-    if a.workload == "ref_shapes":
-        print(json.dumps({"ref_shapes": run_ref_shapes(a.ckpt)}), flush=True)
+    if a.workload.startswith("ref_shapes"):
+        model = a.workload.split(":")[1] if ":" in a.workload else "4b"
+        print(json.dumps({"ref_shapes": run_ref_shapes(a.ckpt, model)}), flush=True)
         return
     r = run_e2e(a.ckpt, a.steps, a.warmup, wl=a.workload)
     if r["first_full"] is not None and a.workload == "config4":
@@ -437,7 +441,8 @@ def main():
     if not a.no_config5:
         res["config5"] = config5_line(a)
     if not a.no_ref_shapes:
-        res["reference_bench_shapes"] = ref_shapes_line(ckpt)
+        res["reference_bench_shapes"] = ref_shapes_line(
+            ckpt, a.ckpt9b if os.path.isdir(a.ckpt9b) else None)
     if not a.no_kernels:
         res.update(kernel_rooflines())
     if not a.no_cpu_baseline:
@@ -488,23 +493,29 @@ def config5_line(a):
             "cpu_baseline": None}
 
 
-def ref_shapes_line(ckpt):
-    """The reference benchmark's 4B shapes on the same synthetic checkpoint,
-    in the torch-free child; the RTX 5090 figures are the reference's
-    published numbers on other hardware, for context only."""
+def ref_shapes_line(ckpt, ckpt9b=None):
+    """The reference benchmark's shapes on the same synthetic checkpoints (the
+    9B row when its checkpoint is there), each model in a torch-free child;
+    the RTX 5090 figures are the reference's published numbers on other
+    hardware, for context only."""
     import subprocess
-    cmd = [sys.executable, str(Path(__file__).resolve()), "--e2e-child", "--ckpt", ckpt,
-           "--workload", "ref_shapes"]
-    p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=sys.stderr, text=True)
-    if p.returncode != 0:
-        raise SystemExit(f"reference-shape child failed with status {p.returncode}")
-    rows = json.loads(p.stdout.strip().splitlines()[-1])["ref_shapes"]
+    rows = []
+    for model, path in (("4b", ckpt), ("9b", ckpt9b)):
+        if not path:
+            continue
+        cmd = [sys.executable, str(Path(__file__).resolve()), "--e2e-child", "--ckpt", path,
+               "--workload", f"ref_shapes:{model}"]
+        p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=sys.stderr, text=True)
+        if p.returncode != 0:
+            raise SystemExit(f"reference-shape child ({model}) failed with status {p.returncode}")
+        rows += json.loads(p.stdout.strip().splitlines()[-1])["ref_shapes"]
     for r in rows:
-        log(f"cujev-bench shape P={r['state_tokens']} {r['branches']}x{r['branch_tokens']}: "
-            f"prefill {r['prefill_ms']:.2f} ms, eval {r['eval_ms']:.2f} ms, "
+        log(f"cujev-bench shape {r['model']} P={r['state_tokens']} {r['branches']}x"
+            f"{r['branch_tokens']}: prefill {r['prefill_ms']:.2f} ms, eval {r['eval_ms']:.2f} ms, "
             f"{r['decisions_per_s']:.0f} decisions/s")
     return {"method": "tools/bench.c:41-74 (prefill then one eval, cujev_last_timing GPU ms, "
-                      "decisions/s = branches / eval ms), 4B shapes of README.md:233-234",
+                      "decisions/s = branches / eval ms), the 4B and 9B shapes of "
+                      "README.md:233-235",
             "rows": rows}
 
 
