@@ -100,3 +100,32 @@ def test_prefix_cache_and_timing(ckpt):
             e.eval([Branch([20], [21])] * 4)
         with pytest.raises(EngineError):
             e.prefill(list(range(16, 16 + 129)))
+
+
+def test_deferred_prefill_under_the_layer(ckpt, monkeypatch):
+    """The same calling sequence with CUJEV_DEFER_PREFILL=1: the first packed
+    eval after a prefill runs the fused pass (prefill + branches), later ones
+    read the state it left. Answers as the default engine's (the bar above);
+    the repeat hits the prefix cache and reproduces every packed call but the
+    first (which ran fused the first time) bit for bit; the prefill reports
+    no time of its own."""
+    rng = np.random.default_rng(13)
+    prefix = [int(x) for x in rng.integers(16, 4096, size=120)]
+    qs = questions(rng)
+    opts = dict(max_state_tokens=256, max_branch_tokens=48, max_branches=3)
+    with Engine(ckpt, **opts) as eager:
+        _, le, _, _ = Caller(eager, Branch).evaluate(prefix, qs)
+    monkeypatch.setenv("CUJEV_DEFER_PREFILL", "1")
+    with Engine(ckpt, **opts) as e:
+        c = Caller(e, Branch)
+        _, l1, hit1, _ = c.evaluate(prefix, qs)
+        assert not hit1 and e.last_timing().prefill_ms == 0
+        _, l2, hit2, _ = c.evaluate(prefix, qs)
+        assert hit2
+    worst = max(np.abs(softmax64(x) - softmax64(y)).max() for x, y in zip(l1, le))
+    first = c.calls[0][0]  # branches of the first packed call
+    for x, y in list(zip(l1, l2))[first:]:
+        assert np.array_equal(x, y)
+    print(f"deferred vs default engine: max|dp| {worst:.2e}; first packed call "
+          f"{first} branches")
+    assert worst <= PROB_TOL
