@@ -123,6 +123,27 @@ static bool table_algo(cujev_gemm *g, int N, int M, int K, int f32out, GemmPlan 
     return true;
 }
 
+/* Two timing events; false (and none left behind) when either cannot be made. */
+static bool make_events(hipEvent_t &e0, hipEvent_t &e1) {
+    e0 = e1 = nullptr;
+    if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess)
+        return true;
+    if (e0)
+        (void)hipEventDestroy(e0);
+    e0 = e1 = nullptr;
+    return false;
+}
+
+/* Records e1 on the stream, waits for it, and returns the milliseconds since
+ * e0; negative when any of those steps fails. */
+static float elapsed_ms(hipEvent_t e0, hipEvent_t e1, hipStream_t stream) {
+    float ms = 0.f;
+    if (hipEventRecord(e1, stream) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+        hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+        return -1.f;
+    return ms;
+}
+
 static bool make_plan(cujev_gemm *g, int N, int M, int K, int f32out, GemmPlan &p, const void *X,
                       const void *W, void *Y, hipStream_t stream) {
     if (!make_descs(N, M, K, f32out, p))
@@ -148,10 +169,8 @@ static bool make_plan(cujev_gemm *g, int N, int M, int K, int f32out, GemmPlan &
     if (st != HIPBLAS_STATUS_SUCCESS || count < 1)
         return false;
     int best = 0;
-    if (count > 1) {
-        hipEvent_t e0, e1;
-        hipEventCreate(&e0);
-        hipEventCreate(&e1);
+    hipEvent_t e0, e1;
+    if (count > 1 && make_events(e0, e1)) {
         const float alpha = 1.f, beta = 0.f;
         float best_ms = 1e30f;
         for (int i = 0; i < count; i++) {
@@ -160,23 +179,19 @@ static bool make_plan(cujev_gemm *g, int N, int M, int K, int f32out, GemmPlan &
             bool ok = true;
             for (int r = 0; r < 4 && ok; r++) {
                 if (r == 1)
-                    hipEventRecord(e0, stream);
-                ok = hipblasLtMatmul(g->handle, p.desc, &alpha, W, p.a, X, p.b, &beta, Y, p.c, Y,
-                                     p.c, &res[i].algo, g->workspace, res[i].workspaceSize,
-                                     stream) == HIPBLAS_STATUS_SUCCESS;
+                    ok = hipEventRecord(e0, stream) == hipSuccess;
+                ok = ok && hipblasLtMatmul(g->handle, p.desc, &alpha, W, p.a, X, p.b, &beta, Y,
+                                           p.c, Y, p.c, &res[i].algo, g->workspace,
+                                           res[i].workspaceSize, stream) == HIPBLAS_STATUS_SUCCESS;
             }
-            hipEventRecord(e1, stream);
-            if (!ok || hipEventSynchronize(e1) != hipSuccess)
-                continue;
-            float ms = 0.f;
-            hipEventElapsedTime(&ms, e0, e1);
-            if (ms < best_ms) {
+            const float ms = ok ? elapsed_ms(e0, e1, stream) : -1.f;
+            if (ms >= 0.f && ms < best_ms) {
                 best_ms = ms;
                 best = i;
             }
         }
-        hipEventDestroy(e0);
-        hipEventDestroy(e1);
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
     }
     p.algo = res[best].algo;
     p.ws = res[best].workspaceSize;
@@ -269,37 +284,36 @@ extern "C" int cujev_gemm_tune(cujev_gemm *g, const bf16_t *X, const bf16_t *W, 
         return -1;
     }
     hipEvent_t e0, e1;
-    hipEventCreate(&e0);
-    hipEventCreate(&e1);
+    if (!make_events(e0, e1)) {
+        destroy_plan(p);
+        return -1;
+    }
     const float alpha = 1.f, beta = 0.f;
     auto time_algo = [&](hipblasLtMatmulAlgo_t &algo, size_t ws) -> float {
         for (int r = 0; r < 7; r++) {
-            if (r == 2)
-                hipEventRecord(e0, stream);
+            if (r == 2 && hipEventRecord(e0, stream) != hipSuccess)
+                return -1.f;
             if (hipblasLtMatmul(g->handle, p.desc, &alpha, W, p.a, X, p.b, &beta, Y, p.c, Y, p.c,
                                 &algo, g->workspace, ws, stream) != HIPBLAS_STATUS_SUCCESS)
                 return -1.f;
         }
-        hipEventRecord(e1, stream);
-        if (hipEventSynchronize(e1) != hipSuccess)
-            return -1.f;
-        float ms = 0.f;
-        hipEventElapsedTime(&ms, e0, e1);
-        return ms * 1e3f / 5.f;
+        const float ms = elapsed_ms(e0, e1, stream);
+        return ms < 0.f ? -1.f : ms * 1e3f / 5.f;
     };
     /* the heuristic's own first choice, for reference */
-    hipblasLtMatmulPreference_t pref;
-    hipblasLtMatmulPreferenceCreate(&pref);
-    uint64_t wsb = g->ws_bytes;
-    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
-                                          sizeof wsb);
-    hipblasLtMatmulHeuristicResult_t top;
-    int cnt = 0;
     float heur = -1.f;
-    if (hipblasLtMatmulAlgoGetHeuristic(g->handle, p.desc, p.a, p.b, p.c, p.c, pref, 1, &top,
-                                        &cnt) == HIPBLAS_STATUS_SUCCESS && cnt > 0)
-        heur = time_algo(top.algo, top.workspaceSize);
-    hipblasLtMatmulPreferenceDestroy(pref);
+    hipblasLtMatmulPreference_t pref;
+    if (hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS) {
+        uint64_t wsb = g->ws_bytes;
+        hipblasLtMatmulHeuristicResult_t top;
+        int cnt = 0;
+        if (hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                  &wsb, sizeof wsb) == HIPBLAS_STATUS_SUCCESS &&
+            hipblasLtMatmulAlgoGetHeuristic(g->handle, p.desc, p.a, p.b, p.c, p.c, pref, 1, &top,
+                                            &cnt) == HIPBLAS_STATUS_SUCCESS && cnt > 0)
+            heur = time_algo(top.algo, top.workspaceSize);
+        hipblasLtMatmulPreferenceDestroy(pref);
+    }
     float best = 1e30f;
     int best_i = -1;
     for (size_t i = 0; i < all.size(); i++) {
@@ -315,8 +329,8 @@ extern "C" int cujev_gemm_tune(cujev_gemm *g, const bf16_t *X, const bf16_t *W, 
             best_i = (int)i;
         }
     }
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
     destroy_plan(p);
     if (best_i < 0)
         return -1;

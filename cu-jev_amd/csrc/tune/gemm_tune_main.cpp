@@ -78,7 +78,10 @@ int main(int argc, char **argv) {
     hipLaunchKernelGGL(fill_kernel, dim3(1024), dim3(256), 0, 0, X, maxX, 1u, 2.0f);
     hipLaunchKernelGGL(fill_kernel, dim3(1024), dim3(256), 0, 0, W, maxW, 2u, 0.05f);
     hipStream_t stream;
-    hipStreamCreate(&stream);
+    if (hipStreamCreate(&stream) != hipSuccess || hipGetLastError() != hipSuccess) {
+        fprintf(stderr, "stream creation or the operand fill failed\n");
+        return 1;
+    }
     cujev_gemm *g;
     if (cujev_gemm_create(&g, ws, WS) != 0) {
         fprintf(stderr, "hipblasLtCreate failed\n");
