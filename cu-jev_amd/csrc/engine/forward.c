@@ -60,8 +60,11 @@ typedef struct {
  * weight (its time is the HBM stream of W). Prefill token counts go to
  * hipBLASLt on the plain rows, except where the hand-tiled prefill kernel
  * (gemm_wide, same tiled copy) measured faster on MI355X: the fused
- * gate|up + silu_mul projection up to 4096 tokens and down_proj, split over
- * K into partials the residual add sums, up to 1536 tokens.
+ * gate|up + silu_mul projection up to 2048 tokens and down_proj, split over
+ * K into partials the residual add sums, up to 1536 tokens. Above 2048 tokens
+ * hipBLASLt + silu_mul measured faster for gate|up: a 4B eval of 2560 tokens
+ * 25.48 -> 25.09 ms, and the 9B request with its 4096-token eval
+ * 155.6 -> 150.9 ms (about 150 us per layer off the kernel's 781 us).
  * CUJEV_SMALL_GEMM=0 / CUJEV_WIDE_GEMM=0 send those shapes to hipBLASLt. */
 static int env_on(const char *name) {
     const char *e = getenv(name);
@@ -75,7 +78,7 @@ static int small_gemm_ok(int N, int M, int K) {
     return cached && N <= CUJEV_GEMM_SMALL_MAX_N && cujev_gemm_small_splits(M, K) > 0;
 }
 
-#define CUJEV_WIDE_GATED_MAX_N 4096
+#define CUJEV_WIDE_GATED_MAX_N 2048
 #define CUJEV_WIDE_RESID_MAX_N 1536
 static int wide_gemm_on(void) {
     static int cached = -1;
