@@ -61,9 +61,11 @@ typedef struct {
  * hipBLASLt on the plain rows, except where the hand-tiled prefill kernel
  * (gemm_wide, same tiled copy) measured faster on MI355X: the fused
  * gate|up + silu_mul projection up to 2048 tokens and down_proj, split over
- * K into partials the residual add sums, up to 1536 tokens. Above 2048 tokens
- * hipBLASLt + silu_mul measured faster for gate|up: a 4B eval of 2560 tokens
- * 25.48 -> 25.09 ms, and the 9B request with its 4096-token eval
+ * K into partials the residual add sums, up to 1000 tokens (hipBLASLt with
+ * bf16 output measured faster at 1024: 4B prefill of 1024 tokens 10.20 ->
+ * 10.02 ms, 9B 15.92 -> 15.39 ms; the kernel is faster at 530-640). Above
+ * 2048 tokens hipBLASLt + silu_mul measured faster for gate|up: a 4B eval of
+ * 2560 tokens 25.48 -> 25.09 ms, and the 9B request with its 4096-token eval
  * 155.6 -> 150.9 ms (about 150 us per layer off the kernel's 781 us).
  * CUJEV_SMALL_GEMM=0 / CUJEV_WIDE_GEMM=0 send those shapes to hipBLASLt. */
 static int env_on(const char *name) {
@@ -79,7 +81,7 @@ static int small_gemm_ok(int N, int M, int K) {
 }
 
 #define CUJEV_WIDE_GATED_MAX_N 2048
-#define CUJEV_WIDE_RESID_MAX_N 1536
+#define CUJEV_WIDE_RESID_MAX_N 1000
 static int wide_gemm_on(void) {
     static int cached = -1;
     if (cached < 0)
