@@ -97,6 +97,16 @@ static int planning(const loader *L) { return cujev_slab_planning(&L->m->weights
 static void *take(loader *L, size_t bytes) { return cujev_slab_take(&L->m->weights, bytes); }
 
 /* Row-concatenation of 2-D tensors [rows_i, K] -> one bf16 [sum rows, K]. */
+/* The output projections (o_proj, out_proj, down_proj) write the residual:
+ * their row count must be hidden_size, since the tiled copy and every GEMM on
+ * them run over exactly H rows. */
+static cujev_status need_rows(const st_tensor *t, int H, int layer) {
+    if (t->ndim != 2 || t->shape[0] != H)
+        return cujev_raise(CUJEV_ERR_FORMAT, "layer %d: tensor %s: expected [%d, *]", layer,
+                           t->name, H);
+    return CUJEV_OK;
+}
+
 static cujev_status upload_fused(loader *L, const st_tensor **parts, int nparts, int K,
                                  bf16_t **out) {
     size_t rows = 0;
@@ -223,6 +233,7 @@ static cujev_status walk(loader *L) {
             CJ_CHECK(upload_fused(L, parts, 3, H, &ly->w_qkv));
             CJ_CHECK(upload_tiled(L, ly->w_qkv, m->w_attn, H, &ly->wt_qkv));
             CJ_CHECK(need(L, "self_attn.o_proj.weight", &t));
+            CJ_CHECK(need_rows(t, H, l));
             CJ_CHECK(upload_fused(L, &t, 1, m->Hq * m->D, &ly->w_o));
             CJ_CHECK(upload_tiled(L, ly->w_o, H, m->Hq * m->D, &ly->wt_o));
             CJ_CHECK(need(L, "self_attn.q_norm.weight", &t));
@@ -240,6 +251,7 @@ static cujev_status walk(loader *L) {
             CJ_CHECK(upload_fused(L, parts, 4, H, &ly->w_in));
             CJ_CHECK(upload_tiled(L, ly->w_in, m->w_gdn, H, &ly->wt_in));
             CJ_CHECK(need(L, "linear_attn.out_proj.weight", &t));
+            CJ_CHECK(need_rows(t, H, l));
             CJ_CHECK(upload_fused(L, &t, 1, m->V, &ly->w_out));
             CJ_CHECK(upload_tiled(L, ly->w_out, H, m->V, &ly->wt_out));
             CJ_CHECK(need(L, "linear_attn.conv1d.weight", &t));
@@ -258,6 +270,7 @@ static cujev_status walk(loader *L) {
         CJ_CHECK(upload_fused(L, parts, 2, H, &ly->w_gate_up));
         CJ_CHECK(upload_tiled(L, ly->w_gate_up, 2 * c->intermediate_size, H, &ly->wt_gate_up));
         CJ_CHECK(need(L, "mlp.down_proj.weight", &t));
+        CJ_CHECK(need_rows(t, H, l));
         CJ_CHECK(upload_fused(L, &t, 1, c->intermediate_size, &ly->w_down));
         CJ_CHECK(upload_tiled(L, ly->w_down, H, c->intermediate_size, &ly->wt_down));
     }

@@ -223,8 +223,10 @@ def _write_blocks(path, cfg, *, seed, std, norm_std):
     return str(path)
 
 
-def ensure_checkpoint(path, preset="4b", *, seed=0, device="cpu", **overrides):
-    """Write the preset checkpoint once (reused when config.json already matches)."""
+def ensure_checkpoint(path, preset="4b", *, seed=0, device="cpu", generator="torch",
+                      sha256=None, **overrides):
+    """Write the preset checkpoint once (reused when config.json already
+    matches and, when `sha256` is given, the weights file hashes to it)."""
     kw = dict(PRESETS[preset])
     kw.update(overrides)
     cfg = make_config(**kw)
@@ -232,11 +234,22 @@ def ensure_checkpoint(path, preset="4b", *, seed=0, device="cpu", **overrides):
     cfg_file = path / "config.json"
     if cfg_file.exists() and (path / "model.safetensors").exists():
         try:
-            if json.loads(cfg_file.read_text()) == cfg:
+            if json.loads(cfg_file.read_text()) == cfg and (
+                    sha256 is None or file_sha256(path / "model.safetensors") == sha256):
                 return str(path)
         except ValueError:
             pass
-    return write_checkpoint(path, cfg, seed=seed, device=device)
+    return write_checkpoint(path, cfg, seed=seed, device=device, generator=generator)
+
+
+def file_sha256(file):
+    """SHA-256 hex digest of a file, read in 16 MiB pieces."""
+    import hashlib
+    h = hashlib.sha256()
+    with open(file, "rb") as f:
+        for chunk in iter(lambda: f.read(1 << 24), b""):
+            h.update(chunk)
+    return h.hexdigest()
 
 
 if __name__ == "__main__":  # python -m cujev.synthetic <dir> [preset]

@@ -139,6 +139,51 @@ def attn_prep(proj, q_norm_eff, k_norm_eff, pos, Hq, Hkv, rot, theta, eps, D=256
     return q, gate, k, v.astype(np.float64)
 
 
+KEY_TILE = 64  # keys per online-softmax step of the reference kernel (REF attention.cu:188, ATT_BC)
+
+
+def _tiled_pv(s, v, tile=KEY_TILE):
+    """Online softmax over key tiles with the probabilities rounded to bf16
+    for the PV product, as the reference kernel runs it
+    (REF src/kernels/attention.cu:188-297):
+
+      for each tile of `tile` consecutive keys (boundaries at multiples of
+      `tile` of the key index):
+        m_new = max(m, max over the tile);  sc = e^(m - m_new)
+        l = l sc + sum p;  o = o sc + bf16(p) V   with p = e^(s - m_new)
+
+    so each tile's p is rounded against the running max after that tile, not
+    against the row's final max. l sums the unrounded p. Masked keys carry
+    s = -inf (p = 0). Returns o / l.
+
+    s: [..., L] scores in the exponent's own units (the engine's log2-domain
+    scores times ln 2, so e^s = 2^(s / ln 2)); v: [..., L, D], or [H, L, D]
+    shared by every row when s is [H, T, L] (causal attention).
+    Pinned by tests/test_oracle.py::test_tiled_bf16_softmax_rounding_points
+    (one tile, or a first-tile max, gives the final-max rounding bit for bit;
+    running maxima an integer number of octaves apart give it exactly too;
+    a maximum in a later tile changes it; without rounding it is the plain
+    softmax to 1e-15).
+    """
+    L = s.shape[-1]
+    sub = "htl,hld->htd" if v.ndim == s.ndim else "...l,...ld->...d"
+    m = np.full(s.shape[:-1], -np.inf)
+    l = np.zeros(s.shape[:-1])
+    o = np.zeros(s.shape[:-1] + (v.shape[-1],))
+    for k0 in range(0, L, tile):
+        st = s[..., k0:k0 + tile]
+        mn = np.maximum(m, st.max(-1))
+        ms = np.where(np.isfinite(mn), mn, 0.0)
+        with np.errstate(invalid="ignore"):
+            sc = np.where(np.isfinite(m), np.exp(m - ms), 0.0)
+        p = np.exp(st - ms[..., None])
+        l = l * sc + p.sum(-1)
+        pb = bf16_round(p.astype(np.float32)).astype(np.float64)
+        o = o * sc[..., None] + np.einsum(sub, pb, v[..., k0:k0 + tile, :])
+        m = mn
+    return o / l[..., None]
+
+
 def shared_prefix_attention(q, gate, k_state, v_state, k_own, v_own, own_base,
                             scale=1.0 / 16.0, bf16_p=False):
     """Gated GQA attention of the engine (REF src/kernels/attention.cu:138-332).
@@ -150,8 +195,9 @@ def shared_prefix_attention(q, gate, k_state, v_state, k_own, v_own, own_base,
     q-head h reading kv-head h // (Hq // Hkv) (TF:592-601).
 
     bf16_p=True emulates the engine's rounding of the probabilities to bf16
-    before the PV product while the row sum stays in full precision
-    (REF attention.cu:270-278).
+    before the PV product, per 64-key tile of the concatenated key index
+    [state ++ own] against the running max (`_tiled_pv`), while the row sum
+    stays in full precision (REF attention.cu:188-297).
 
     Pinned by: equality with causal attention over [state ++ branch]
     (tests/test_oracle.py), the single-visible-key closed form sigma(g)*v,
@@ -164,18 +210,16 @@ def shared_prefix_attention(q, gate, k_state, v_state, k_own, v_own, own_base,
     out = np.zeros((N, Hq, D), dtype=np.float64)
     for n in range(N):
         b = int(own_base[n])
-        ks = np.concatenate([k_state, k_own[b: n + 1]], 0)  # [L, Hkv, D]
-        vs = np.concatenate([v_state, v_own[b: n + 1]], 0)
-        for h in range(Hq):
-            kh = h // grp
-            s = ks[:, kh, :].astype(np.float64) @ q[n, h].astype(np.float64) * scale
-            m = s.max()
-            p = np.exp(s - m)
-            l = p.sum()
-            if bf16_p:
-                # the engine's probabilities are exp2 of log2-scaled scores
-                p = bf16_round(p.astype(np.float32)).astype(np.float64)
-            out[n, h] = (p @ vs[:, kh, :].astype(np.float64)) / l
+        ks = np.concatenate([k_state, k_own[b: n + 1]], 0).astype(np.float64)  # [L, Hkv, D]
+        vs = np.concatenate([v_state, v_own[b: n + 1]], 0).astype(np.float64)
+        kr = np.repeat(ks.transpose(1, 0, 2), grp, axis=0)  # [Hq, L, D]
+        vr = np.repeat(vs.transpose(1, 0, 2), grp, axis=0)
+        s = np.einsum("hld,hd->hl", kr, q[n].astype(np.float64)) * scale
+        if bf16_p:
+            out[n] = _tiled_pv(s, vr)
+        else:
+            p = np.exp(s - s.max(-1, keepdims=True))
+            out[n] = np.einsum("hl,hld->hd", p, vr) / p.sum(-1)[:, None]
     return out * sigmoid(gate)
 
 
@@ -183,8 +227,9 @@ def causal_gqa_attention(q, gate, k, v, scale=1.0 / 16.0, bf16_p=False):
     """transformers-style causal attention over one sequence
     (TF:604-626 eager_attention_forward + repeat_kv TF:592-601, gate TF:697-700).
     q, gate: [T, Hq, D]; k, v: [T, Hkv, D]. bf16_p: the probabilities are
-    rounded to bf16 before the PV product, the row sum is not (engine
-    semantics, REF attention.cu:270-278)."""
+    rounded to bf16 before the PV product per 64-key tile against the
+    running max, the row sum is not (engine semantics, `_tiled_pv`,
+    REF attention.cu:188-297)."""
     T, Hq, D = q.shape
     Hkv = k.shape[1]
     grp = Hq // Hkv
@@ -193,11 +238,12 @@ def causal_gqa_attention(q, gate, k, v, scale=1.0 / 16.0, bf16_p=False):
     s = np.einsum("thd,shd->hts", q, kr) * scale
     mask = np.triu(np.ones((T, T), dtype=bool), 1)
     s = np.where(mask[None], -np.inf, s)
+    if bf16_p:
+        o = _tiled_pv(s, np.ascontiguousarray(vr.transpose(1, 0, 2), dtype=np.float64))
+        return o.transpose(1, 0, 2) * sigmoid(gate)
     s = s - s.max(-1, keepdims=True)
     p = np.exp(s)
     l = p.sum(-1, keepdims=True)
-    if bf16_p:
-        p = bf16_round(p.astype(np.float32)).astype(np.float64)
     o = np.einsum("hts,shd->thd", p / l, vr)
     return o * sigmoid(gate)
 

@@ -119,7 +119,13 @@ def main(ckpt):
         # per jitter seed vs "engine": RMS dlogit over the whole vocabulary,
         # over the sample, and max |dp| over the labels
         stat_modes=np.asarray(MODES[2:]),
-        stat_values=np.asarray([stats[m] for m in MODES[2:]]))
+        stat_values=np.asarray([stats[m] for m in MODES[2:]]),
+        # every mode's label logits (rows in MODES order, labels flattened in
+        # branch order): the jitter seeds' label deviations set the noise
+        # floor of a decision's top-2 margin
+        label_modes=np.asarray(MODES),
+        label_logits=np.stack([np.concatenate([full[m][i, c] for i, (_, c) in enumerate(brs)])
+                               for m in MODES]))
     for m, v in stats.items():
         print(f"{m} vs engine: rms dlogit {v[0]:.4f} (sample {v[1]:.4f}), max|dp| {v[2]:.2e}")
     print(f"wrote {OUT}")

@@ -8,15 +8,23 @@ a request at the engine's default capacity (REF src/api/cujev.c:11-18):
    of the reference engine's rounding points (the bar of tests/
    test_gpu_engine.py, which explains it), and candidate logits == the
    full-vocabulary logits through the same head.
-2. The config-5 request on a 4-layer model with the 9B layer dims (hidden
-   4096, intermediate 12288, 16/4 attention heads, 16/32 GDN heads, vocab
-   248320, untied head): every logit finite; candidate logits == full logits
-   of the same forward; a branch evaluated alone equals the same branch in
-   the 256-branch batch within bf16 jitter (the batch changes GEMM tile
-   choices and key splits, not the math). The oracle is not run at this size
-   (a float64 pass over 8192 tokens would take minutes); the kernels' parity
-   at these shapes is covered by the attention (config 3) and GDN (config 2)
-   tests.
+2. The config-5 request on the full 32-layer 9B-shaped model (hidden 4096,
+   intermediate 12288, 16/4 attention heads, 16/32 GDN heads, vocab 248320,
+   8 full-attention layers, untied head), written on the device from a
+   seed: every logit finite; candidate logits == full logits of the same
+   forward; a branch evaluated alone equals the same branch in the
+   256-branch batch within bf16 jitter (the batch changes GEMM tile choices,
+   GDN packing and key splits, not the math). The bar for that is 0.15
+   logits, four times the noise floor of a label logit: on the 32-layer
+   4B-shaped config-4 fixture, three other valid fp32 summation orders of
+   the reference engine's numerics (its jitter seeds) move single label
+   logits by up to 0.038 (tests/golden/request_4b.npz, label_logits); a
+   branch alone and in the batch are two such orders, each that far from
+   the reference numerics, on a model of twice the width. The oracle is not run at this size (a
+   float64 pass over 8192 tokens x 32 layers would take hours); the
+   kernels' parity at these shapes is covered by the attention (config 3)
+   and GDN (config 2) tests and the 9B-dims numerics by
+   tests/test_gpu_request_9b.py.
 """
 import numpy as np
 import pytest
@@ -66,10 +74,21 @@ def test_untied_head_tiny(tmp_path):
         assert d <= PROB_TOL and d64 <= PROB_TOL
 
 
-def test_config5_request_shape(tmp_path):
-    cfg = synthetic.make_config(**dict(synthetic.PRESETS["9b"], num_layers=4))
+ALONE_BAR = 0.15  # logits; see the module docstring
+
+
+def test_config5_request_shape():
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:  # ~19 GB, removed at the end
+        _config5_request_shape(d)
+
+
+def _config5_request_shape(tmp_path):
+    cfg = synthetic.make_config(**synthetic.PRESETS["9b"])
     assert not cfg["tie_word_embeddings"] and cfg["hidden_size"] == 4096
-    print("writing a 4-layer 9B-dims checkpoint", flush=True)
+    assert cfg["num_hidden_layers"] == 32
+    assert sum(t == "full_attention" for t in cfg["layer_types"]) == 8
+    print("writing the 32-layer 9B-shaped checkpoint", flush=True)
     synthetic.write_checkpoint(tmp_path, cfg, seed=5, device="cuda")
     torch.cuda.empty_cache()
     rng = np.random.default_rng(5)
@@ -96,4 +115,4 @@ def test_config5_request_shape(tmp_path):
     for i, a in zip((0, 77, 255), alone):
         d = np.abs(a - outs[i]).max()
         print(f"branch {i} alone vs in the batch: max |dlogit| {d:.2e}", flush=True)
-        assert d <= 5e-2
+        assert d <= ALONE_BAR

@@ -179,6 +179,25 @@ def test_capacity_errors(engine):
     assert np.all(np.isfinite(lg))
 
 
+@pytest.mark.parametrize("name", ["model.layers.0.mlp.down_proj.weight",
+                                  "model.layers.0.linear_attn.out_proj.weight",
+                                  "model.layers.3.self_attn.o_proj.weight"])
+def test_output_projection_rows_checked(ckpt, tmp_path, name):
+    """o_proj, out_proj and down_proj must have hidden_size rows: a
+    checkpoint with more is a FORMAT error at open, before any upload."""
+    import shutil
+
+    from safetensors.torch import load_file, save_file
+    t = load_file(str(ckpt) + "/model.safetensors")
+    w = t[name]
+    t[name] = torch.cat([w, w[:16]], 0).contiguous()
+    save_file(t, str(tmp_path / "model.safetensors"), metadata={"format": "pt"})
+    shutil.copy(str(ckpt) + "/config.json", tmp_path / "config.json")
+    with pytest.raises(EngineError) as ei:
+        Engine(str(tmp_path), max_state_tokens=64, max_branch_tokens=64, max_branches=4)
+    assert "expected [512, *]" in str(ei.value), str(ei.value)
+
+
 def test_timing_is_reported(engine):
     engine.prefill(list(range(16, 116)))
     engine.eval([Branch([20, 21, 22], [1, 2]), Branch([23], [3])])

@@ -7,14 +7,15 @@ transformers' math.
 
 What the bars are, and why. On this random-init 32-layer model the bf16
 rounding noise is large: the reference engine's own numerics sit at max
-|dp| ~4e-2 and RMS dlogit ~0.05 from float64, and the same numerics with
+|dp| 2.2e-2 and RMS dlogit 0.045 from float64, and the same numerics with
 another valid fp32 summation order (2^-24 jitter before every bf16 rounding,
-three seeds, stored in the fixture) drift from "engine" by max |dp| ~1.3e-2
-and RMS dlogit ~0.024 -- an order of magnitude above a 1e-3 probability bar,
-which no bf16 engine that is not bit-identical to the oracle's arithmetic can
-meet. The test therefore asserts, against "engine":
+three seeds, stored in the fixture) drift from "engine" by max |dp| up to
+1.05e-2 and RMS dlogit 0.022 -- an order of magnitude above a 1e-3
+probability bar, which no bf16 engine that is not bit-identical to the
+oracle's arithmetic can meet. The test therefore asserts, against "engine":
   * identical argmax on every branch (every top-2 label margin in the fixture
-    is >= 0.37 logits, far above the noise);
+    is >= 0.58 logits; the jitter seeds move single label logits by at most
+    0.04);
   * RMS dlogit over 4096+ vocabulary ids <= 1.5 x the largest jitter-seed
     RMS (the engine is as close to the reference numerics as another valid
     summation order is);

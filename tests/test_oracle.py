@@ -73,6 +73,71 @@ def test_shared_prefix_equals_causal_over_concatenation():
         start += L
 
 
+def test_shared_prefix_equals_causal_with_engine_rounding():
+    """The engine track's tiles follow the concatenated key index [state ++
+    own], so the shared-prefix form equals causal attention over the
+    concatenation with the rounding points included (state of 70 keys: the
+    branch rows' tiles straddle the state/own boundary)."""
+    rng = np.random.default_rng(11)
+    P, L = 70, 9
+    q, g = rng.standard_normal((L, 8, 256)), rng.standard_normal((L, 8, 256))
+    ks, vs = rng.standard_normal((P, 2, 256)), rng.standard_normal((P, 2, 256))
+    ko, vo = rng.standard_normal((L, 2, 256)), rng.standard_normal((L, 2, 256))
+    kw = dict(scale=0.05, bf16_p=True)
+    out = orc.shared_prefix_attention(q, g, ks, vs, ko, vo, np.zeros(L, int), **kw)
+    qf = np.concatenate([rng.standard_normal((P, 8, 256)), q])
+    gf = np.concatenate([rng.standard_normal((P, 8, 256)), g])
+    ref = orc.causal_gqa_attention(qf, gf, np.concatenate([ks, ko]), np.concatenate([vs, vo]),
+                                   **kw)[P:]
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-14)
+
+
+def _final_max_pv(s, v):
+    """bf16(p) against the row's final max (the rounding the tiled form must
+    reduce to when no later tile raises the max)."""
+    p = np.exp(s - s.max())
+    pb = orc.bf16_round(p.astype(np.float32)).astype(np.float64)
+    return pb @ v / p.sum()
+
+
+def test_tiled_bf16_softmax_rounding_points():
+    """Pins oracle.qwen35._tiled_pv, the reference kernel's online softmax
+    with P rounded to bf16 per 64-key tile against the running max."""
+    rng = np.random.default_rng(12)
+    L, D = 200, 16
+    v = rng.standard_normal((L, D))
+    ln2 = np.log(2.0)
+    # all scores equal: p = 1 exactly in every tile, o = mean(v)
+    np.testing.assert_allclose(orc._tiled_pv(np.zeros(L), v), v.mean(0), rtol=1e-13)
+    # one tile: the final max is the running max
+    s = rng.standard_normal(50) * 2
+    np.testing.assert_allclose(orc._tiled_pv(s, v[:50]), _final_max_pv(s, v[:50]), rtol=1e-13)
+    # the max in the first tile, at its last key (63): later tiles never move
+    # it, so every p is rounded against the final max
+    s = rng.uniform(-4, 0, L) * ln2
+    s[63] = 3.0 * ln2
+    np.testing.assert_allclose(orc._tiled_pv(s, v), _final_max_pv(s, v), rtol=1e-13)
+    # the max at key 64 (the second tile's first): tile 0 was rounded against
+    # a lower running max, which is not a whole number of octaves below, so
+    # the bf16 roundings differ
+    s2 = s.copy()
+    s2[63], s2[64] = s[64], 3.37 * ln2
+    a, b = orc._tiled_pv(s2, v), _final_max_pv(s2, v)
+    assert np.abs(a - b).max() > 1e-6 * np.abs(b).max()
+    np.testing.assert_allclose(a, b, rtol=2e-2, atol=2e-2)
+    # running maxima a whole number of octaves apart (0, then 3 in tile 1):
+    # 2^(s-0) and 2^(s-3) differ by 2^3, which bf16 rounding commutes with
+    s3 = rng.uniform(-6, -1, L) * ln2
+    s3[5], s3[100] = 0.0, 3.0 * ln2
+    np.testing.assert_allclose(orc._tiled_pv(s3, v), _final_max_pv(s3, v), rtol=1e-12)
+    # masked keys (-inf) contribute nothing, wherever they sit in a tile
+    s4 = s.copy()
+    s4[[0, 70, 150]] = -np.inf
+    keep = np.isfinite(s4)
+    np.testing.assert_allclose(orc._tiled_pv(s4, v), orc._tiled_pv(s4, np.where(keep[:, None], v, 7.0)),
+                               rtol=0, atol=0)
+
+
 def test_attention_single_key_and_gqa_mapping():
     q, g, _, _, ko, vo = _attn_inputs(4, 1, 0)
     out = orc.shared_prefix_attention(q, g, np.zeros((0, 2, 256)), np.zeros((0, 2, 256)), ko, vo,
