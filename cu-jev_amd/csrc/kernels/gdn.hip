@@ -15,13 +15,13 @@
  *                  A = tril(beta_i k_i.k_j e^{G_i-G_j}, -1),
  *                  T = (I+A)^-1 by blocked forward substitution (fp32),
  *                  W = T diag(beta e^G) K, U = T diag(beta) V,
- *                  QKm = tril(q_i.k_j e^{G_i-G_j})  -> HBM in phase B's
- *                  fragment order (bf16; U fp32; QKm and (K e^{G_last-G})^T
- *                  as bf16 hi + lo pairs).
+ *                  QKm = tril(q_i.k_j e^{G_i-G_j}), and once per k-head Q
+ *                  and K^T  -> HBM in phase B's fragment order (bf16; U
+ *                  fp32; QKm and K^T as bf16 hi + lo pairs).
  *   gdn_chunk_b    per (segment, v-head), sequential over the segment's
  *                  chunks; a workgroup owns 32 columns of S (fp32, registers):
- *                  V' = U - W S;  O = (Q e^G) S + QKm V';
- *                  S = e^{G_last} S + (K e^{G_last-G})^T V'  (bf16 MFMA, V'
+ *                  V' = U - W S;  O = e^G (Q S) + QKm V';
+ *                  S = e^{G_last} S + K^T (e^{G_last-G} V')  (bf16 MFMA, V'
  *                  and the two operands above as hi + lo products), O fp32,
  *                  then y = w * bf16(rmsnorm(O)) * silu(z) to bf16.
  * Every segment starts from S_in (the state's S, read-only) or 0 and the
@@ -207,15 +207,16 @@ __global__ void gdn_conv_tail_kernel(const bf16 *__restrict__ proj, int ps,
  *   1. q and k rows of the k-head (conv + SiLU + l2 norm and q * 128^-1/2,
  *      or read from gdn_conv_prep's fp32 output) staged in LDS as bf16
  *      pairs hi + lo (hi = bf16(x), lo = bf16(x - hi): x to ~16 bits); the
- *      gates of both v-heads: G = cumsum g (restarted at segment starts),
- *      beta e^G, beta, e^{G_last - G};
+ *      gates of both v-heads: G = cumsum g (restarted at segment starts;
+ *      leaves for phase B), beta e^G, beta;
  *   2. raw K K^T (hi parts) and Q K^T (hi.hi + hi.lo + lo.hi MFMAs) in fp32,
- *      shared by both v-heads; q e^G (bf16) of both v-heads leaves;
+ *      shared by both v-heads; q (bf16) leaves once per k-head;
  *   then waves 0-3 serve the first v-head and waves 4-7 the second, side by
  *   side:
  *   3. the masked QK^T (hi + lo) leaves; A = tril(beta_i e^{G_i-G_j}
- *      k_i.k_j, -1) (fp32); (K e^{G_last-G})^T from the exact k rows leaves
- *      as hi + lo;
+ *      k_i.k_j, -1) (fp32); K^T from the exact k rows leaves as hi + lo,
+ *      once per k-head (phase B scales V' by e^{G_last-G} instead, and
+ *      Q S by e^G, so the k-head's v-heads share Q and K^T);
  *   4. the v rows of both v-heads (hi + lo) where the q rows and the raw
  *      products were; T = (I + A)^-1 in place (fp32, blocked forward
  *      substitution);
@@ -223,11 +224,10 @@ __global__ void gdn_conv_tail_kernel(const bf16 *__restrict__ proj, int ps,
  *      MFMAs; U kept fp32), staged row-major, then stored in the fragment
  *      order phase B reads.
  * Which operands carry lo parts follows from where a bf16 rounding moves
- * the layer output: q and k in QK^T, v in U, k in (K e^{G_last-G})^T, and
- * U, QK^T, (K e^{G_last-G})^T and V' themselves each cost about as much as
- * the reference's own bf16 round trip in the gated norm; K K^T, W, T,
- * q e^G and the bf16 copy of S that the W S and q e^G S products read each
- * cost under a tenth of that.
+ * the layer output: q and k in QK^T, v in U, k in K^T, and U, QK^T, K^T
+ * and V' themselves each cost about as much as the reference's own bf16
+ * round trip in the gated norm; K K^T, W, T, Q and the bf16 copy of S that
+ * the W S and Q S products read each cost under a tenth of that.
  * A chunk may hold several whole segments (chunk_starts marks where each
  * begins): G restarts at every segment start and A and QK^T are kept
  * block-diagonal, so the segments do not see each other. This is valid for
@@ -245,7 +245,7 @@ struct __attribute__((aligned(16))) PairA_Smem {
     bf16 Yh[CH][DK + 8], Yl[CH][DK + 8];
     float AT[2][CH][CH + 4];             /* A, then T in place; then W staging    */
     float cs[2 * PA_STAGE1];             /* conv weights and tails of two slices  */
-    float G[2][CH], sK[2][CH], sKg[2][CH], sV[2][CH]; /* per v-head of the pair */
+    float G[2][CH], sK[2][CH], sV[2][CH]; /* per v-head of the pair */
     int Sid[CH]; /* segment of each token inside a packed chunk (1-based) */
 };
 static_assert(sizeof(PairA_Smem) <= 160 * 1024, "phase A fits one CU's LDS");
@@ -480,8 +480,8 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
     const float *__restrict__ g, const float *__restrict__ beta, ConvSrc cv,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
     const uint64_t *__restrict__ chunk_starts, int Hk, int Hv, int npairs,
-    bf16 *__restrict__ Wo, bf16 *__restrict__ Qgo, bf16 *__restrict__ QKo,
-    bf16 *__restrict__ KgTo, float *__restrict__ Uo, float *__restrict__ Glo) {
+    bf16 *__restrict__ Wo, bf16 *__restrict__ Qo, bf16 *__restrict__ QKo,
+    bf16 *__restrict__ KTo, float *__restrict__ Uo, float *__restrict__ Go) {
     __shared__ PairA_Smem sm;
     const int ch = blockIdx.x, hk = blockIdx.y / npairs, pr = blockIdx.y - hk * npairs;
     const int rep = Hv / Hk;
@@ -560,28 +560,28 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
         }
         /* st = first token of this lane's segment, en = its last */
         const int st = 63 - __builtin_clzll(starts & upto);
-        const uint64_t later = starts & ~upto;
-        const int en = later ? __builtin_ctzll(later) - 1 : 63;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) { /* cumulative sum restarted per segment */
             const float up = __shfl_up(gv, o, 64);
             if (lane - o >= st)
                 gv += up;
         }
-        const float gl = __shfl(gv, en, 64);
         sm.G[r][lane] = gv;
         sm.sK[r][lane] = bv * fast_exp(gv);
-        sm.sKg[r][lane] = fast_exp(gl - gv);
         sm.sV[r][lane] = bv;
-        Glo[((size_t)ch * Hv + hv) * 64 + lane] = gl; /* one copy per lane of phase B's waves */
+        /* past the chunk's end g = 0: those lanes repeat the last token's G,
+         * so G[63] is the chunk's total log-decay */
+        Go[((size_t)ch * Hv + hv) * 64 + lane] = gv;
     }
     lds_barrier();
 
     /* ---- 2. raw Q K^T (split) on waves 0-2, K K^T on waves 3, 6, 7: the
-     * lower 32x32 tiles (0,0), (1,0), (1,1) | q e^G of both v-heads (waves
-     * 4-7, 16x16x32 A-fragment order: entry i holds row 16(i/256) + i%16,
-     * columns 32((i/64)%4) + 8((i/16)%4) .. +7) | every group: the pre-conv
-     * rows of its v-conv task (slice = v-head grp/16, block grp%16) ---- */
+     * lower 32x32 tiles (0,0), (1,0), (1,1) | q of the k-head, once per
+     * k-head (waves 4-7 of its first workgroup, 16x16x32 A-fragment order:
+     * entry i holds row 16(i/256) + i%16, columns 32((i/64)%4) +
+     * 8((i/16)%4) .. +7; phase B applies each v-head's e^G to Q S) | every
+     * group: the pre-conv rows of its v-conv task (slice = v-head grp/16,
+     * block grp%16) ---- */
     constexpr bool CONV = SRC != 0;
     bf16x8 vr[7];
     int vbase[4];
@@ -619,21 +619,12 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
                 }
             }
         }
-        if (wave >= 4) {
+        if (wave >= 4 && pr == 0) { /* q rounded once: its hi part */
             const int u = tid - 256, t = u & 15, c8 = 32 * ((u >> 6) & 3) + 8 * ((u >> 4) & 3);
-            for (int r = 0; r < nh; r++) {
-                const size_t cb = (size_t)ch * Hv + hv0 + r;
+            const size_t ck = (size_t)ch * Hk + hk;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const bf16x8 a = ld8(&sm.Xh[16 * j + t][c8]), b = ld8(&sm.Xl[16 * j + t][c8]);
-                    const float eg = fast_exp(sm.G[r][16 * j + t]);
-                    bf16x8 o;
-#pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        o[e] = f2bf((bf2f(a[e]) + bf2f(b[e])) * eg);
-                    *(bf16x8 *)(Qgo + (cb * 1024 + u + 256 * j) * 8) = o;
-                }
-            }
+            for (int j = 0; j < 4; j++)
+                *(bf16x8 *)(Qo + (ck * 1024 + u + 256 * j) * 8) = ld8(&sm.Xh[16 * j + t][c8]);
         }
         /* the raw products go where the second v-head's v rows will be */
         if (job >= 0) {
@@ -653,10 +644,12 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
             eye[s][e] = f2bf(16 * s + 8 * h + e == col ? 1.f : 0.f);
     /* token of accumulator slot r of 32-row tile tb */
     auto tok = [&](int tb, int r) { return 32 * tb + 8 * (r >> 2) + 4 * h + (r & 3); };
-    const float *Gg = sm.G[hg], *sKg_g = sm.sKg[hg];
+    const float *Gg = sm.G[hg];
 
-    /* ---- 3. per group (its v-head): masked QK^T hi + lo, A, and
-     * (K e^{G_last-G})^T hi + lo for dk block 32 w4; the v-conv weights ---- */
+    /* ---- 3. per group (its v-head): masked QK^T hi + lo and A; the first
+     * group of a k-head's first workgroup: K^T hi + lo for dk block 32 w4
+     * (phase B applies each v-head's e^{G_last-G} to V'); the v-conv
+     * weights ---- */
     if (hact) {
         const int u = tid & 255;
         /* masked QK^T = tril(q_i.k_j e^{G_i-G_j}) within a segment, as hi
@@ -703,9 +696,12 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
                 wr4(&AT[ri][c16b + c4], make_float4(a[0], a[1], a[2], a[3]));
             }
         }
-        /* (K e^{G_last-G})^T as 32x32x16 A fragments (row dk = 32 w4 + l%32,
-         * tokens 16s + 8(l/32)..+7) from the exact k rows (identity
-         * products of hi and lo); the lane pair (l, l^32) trades halves */
+    }
+    if (hg == 0 && pr == 0) {
+        /* K^T as 32x32x16 A fragments (row dk = 32 w4 + l%32, tokens 16s +
+         * 8(l/32)..+7) from the exact k rows (identity products of hi and
+         * lo); the lane pair (l, l^32) trades halves */
+        const size_t ck = (size_t)ch * Hk + hk;
         floatx16 dK[2];
 #pragma unroll
         for (int tb = 0; tb < 2; tb++) {
@@ -725,7 +721,7 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
             bf16 vh_[8], vl_[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const bfpair sp = split2(dK[tb][r0 + e] * sKg_g[tok(tb, r0 + e)]);
+                const bfpair sp = split2(dK[tb][r0 + e]);
                 vh_[e] = sp.hi;
                 vl_[e] = sp.lo;
             }
@@ -746,7 +742,7 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
                     o[e] = h ? x1 : p0[e];
                     o[2 + e] = h ? p1[e] : x0;
                 }
-                *(u32x4 *)(KgTo + (cbg * 2048 + part * 1024 + (w4 * 4 + s) * 64 + lane) * 8) =
+                *(u32x4 *)(KTo + (ck * 2048 + part * 1024 + (w4 * 4 + s) * 64 + lane) * 8) =
                     u32x4{o[0], o[1], o[2], o[3]};
             }
         }
@@ -901,7 +897,7 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
         }
     }
     lds_barrier();
-    /* ---- 6. W in the fragment order of q e^G; U (fp32) as 16x16
+    /* ---- 6. W in the fragment order of Q; U (fp32) as 16x16
      * accumulator fragments: entry i = (32-column block i/256, row block
      * (i/64)%4, lane i%64) holds rows 16((i/64)%4) + 4((i/16)%4) + 0..3 of
      * columns 32(i/256) + i%16 (values 0..3) and +16 (values 4..7) ---- */
@@ -934,12 +930,12 @@ __global__ __launch_bounds__(PA_THREADS, 1) void gdn_chunk_a_kernel(
  *   tokens 16w..16w+15):
  *     S (bf16) -> LDS as S^T;                                   barrier 1
  *     V'_w = U_w - W_w S (16x16x32, 8 MFMAs), as hi + lo (bf16)
- *       -> LDS as V'^T;                                         barrier 2
- *     S_w = e^{G_last} S_w + (K e^{G_last-G})^T_w V' (32x32x16; hi.hi,
- *       hi.lo, lo.hi: 12 MFMAs)
+ *       -> LDS as V'^T, and e^{G_last-G} V'_w likewise as D^T;  barrier 2
+ *     S_w = e^{G_last} S_w + K^T_w D (32x32x16; hi.hi, hi.lo, lo.hi:
+ *       12 MFMAs)
  *   output wave w (chunk tokens 16w..16w+15):
  *                                                               barrier 1
- *     O_w = (Q e^G)_w S (8 MFMAs) from the same S^T;            barrier 2
+ *     O_w = e^G (Q_w S) (8 MFMAs) from the same S^T;            barrier 2
  *     O_w += QKm_w V' (12 MFMAs), O (fp32) out through a per-wave LDS tile.
  * The output waves keep their products off the recurrence's critical path:
  * each LDS buffer is written by the chain waves only after the barrier
@@ -959,22 +955,27 @@ constexpr int CB_THREADS = 512;
 struct ChainOps {
     bf16x8 w[4], kgh[4], kgl[4];
     float4 u[2];
+    float4 g; /* G of this lane's 4 V' rows */
     float gl;
 };
 struct OutOps {
     bf16x8 qg[4], qkh[2], qkl[2];
+    float4 g; /* G of this lane's 4 O rows */
 };
 
 __global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
-    const bf16x8 *__restrict__ Wi, const bf16x8 *__restrict__ Qgi, const bf16x8 *__restrict__ QKi,
-    const bf16x8 *__restrict__ KgTi, const float4 *__restrict__ Ui, const float *__restrict__ Gli,
+    const bf16x8 *__restrict__ Wi, const bf16x8 *__restrict__ Qi, const bf16x8 *__restrict__ QKi,
+    const bf16x8 *__restrict__ KTi, const float4 *__restrict__ Ui, const float *__restrict__ Gi,
     const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
     const int32_t *__restrict__ seg_chunk0, const int32_t *__restrict__ seg_nchunk,
-    const float *__restrict__ S_in, float *__restrict__ S_out, int Hv, int units,
+    const float *__restrict__ S_in, float *__restrict__ S_out, int Hv, int Hk, int units,
     float *__restrict__ o, TailJob tail) {
     __shared__ __attribute__((aligned(16))) bf16 sT[32][DK + 8];   /* S^T [column][dk]        */
     __shared__ __attribute__((aligned(16))) bf16 vTh[32][CH + 8];  /* V'^T hi [column][token] */
     __shared__ __attribute__((aligned(16))) bf16 vTl[32][CH + 8];  /* V'^T lo                 */
+    /* (e^{G_last-G} V')^T hi and lo: the S update's operand */
+    __shared__ __attribute__((aligned(16))) bf16 dTh[32][CH + 8];
+    __shared__ __attribute__((aligned(16))) bf16 dTl[32][CH + 8];
     __shared__ __attribute__((aligned(16))) float ost[4][16][36];  /* per output wave O tile  */
 
     const int bid = blockIdx.x;
@@ -998,7 +999,7 @@ __global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
     const int un = (bid & 7) + 8 * ((bid >> 3) / NCB), cbk = (bid >> 3) % NCB;
     if (un >= units)
         return;
-    const int seg = un / Hv, hv = un - seg * Hv;
+    const int seg = un / Hv, hv = un - seg * Hv, hk = hv / (Hv / Hk);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int w4 = wave & 3;
@@ -1039,15 +1040,15 @@ __global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
         struct Ptr {
             const bf16x8 *w, *kg;
             const float4 *u;
-            const float *gl;
+            const float *g;
         };
         auto ptrs = [&](int ch) {
-            const size_t cb = (size_t)ch * Hv + hv;
+            const size_t cb = (size_t)ch * Hv + hv, ck = (size_t)ch * Hk + hk;
             Ptr p;
             p.w = Wi + cb * 1024 + w4 * 256 + lane;
-            p.kg = KgTi + cb * 2048 + w4 * 256 + lane;
+            p.kg = KTi + ck * 2048 + w4 * 256 + lane;
             p.u = Ui + (cb * 1024 + (cbk * 4 + w4) * 64 + lane) * 2;
-            p.gl = Gli + cb * 64 + lane;
+            p.g = Gi + cb * 64;
             return p;
         };
         auto load_part = [&](const Ptr &p, ChainOps &op, int part) {
@@ -1058,7 +1059,8 @@ __global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
             } else if (part == 1) {
                 op.u[0] = p.u[0];
                 op.u[1] = p.u[1];
-                op.gl = p.gl[0];
+                op.g = *(const float4 *)(p.g + 16 * w4 + 4 * q4);
+                op.gl = p.g[63];
             } else {
 #pragma unroll
                 for (int s = 0; s < 4; s++) {
@@ -1088,17 +1090,30 @@ __global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
             __builtin_amdgcn_sched_barrier(0);
             const float uf[8] = {op.u[0].x, op.u[0].y, op.u[0].z, op.u[0].w,
                                  op.u[1].x, op.u[1].y, op.u[1].z, op.u[1].w};
+            /* each row's decay to the chunk's end: V' enters the S update as
+             * e^{G_last-G} V', and O as it is */
+            const float gv[4] = {op.g.x, op.g.y, op.g.z, op.g.w};
+            float dg[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                dg[i] = fast_exp(op.gl - gv[i]);
 #pragma unroll
             for (int jb = 0; jb < 2; jb++) {
-                bf16x4 ph, pl;
+                bf16x4 ph, pl, dh, dl;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const bfpair sp_ = split2(uf[4 * jb + i] - V[jb][i]);
+                    const float vp = uf[4 * jb + i] - V[jb][i];
+                    const bfpair sp_ = split2(vp);
                     ph[i] = sp_.hi;
                     pl[i] = sp_.lo;
+                    const bfpair sd_ = split2(vp * dg[i]);
+                    dh[i] = sd_.hi;
+                    dl[i] = sd_.lo;
                 }
                 *(bf16x4 *)&vTh[16 * jb + c16][16 * w4 + 4 * q4] = ph;
                 *(bf16x4 *)&vTl[16 * jb + c16][16 * w4 + 4 * q4] = pl;
+                *(bf16x4 *)&dTh[16 * jb + c16][16 * w4 + 4 * q4] = dh;
+                *(bf16x4 *)&dTl[16 * jb + c16][16 * w4 + 4 * q4] = dl;
             }
             __builtin_amdgcn_sched_barrier(0);
             load_part(np, nx, 1);
@@ -1107,8 +1122,8 @@ __global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
             bf16x8 vbh[4], vbl[4];
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                vbh[s] = *(const bf16x8 *)&vTh[c32][16 * s + 8 * h];
-                vbl[s] = *(const bf16x8 *)&vTl[c32][16 * s + 8 * h];
+                vbh[s] = *(const bf16x8 *)&dTh[c32][16 * s + 8 * h];
+                vbl[s] = *(const bf16x8 *)&dTl[c32][16 * s + 8 * h];
             }
             S = S * dec;
 #pragma unroll
@@ -1146,12 +1161,14 @@ __global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
     /* ---- output waves: O of chunk tokens 16 w4 .. +15 ---- */
     struct Ptr {
         const bf16x8 *qg, *qk;
+        const float *g;
     };
     auto ptrs = [&](int ch) {
-        const size_t cb = (size_t)ch * Hv + hv;
+        const size_t cb = (size_t)ch * Hv + hv, ck = (size_t)ch * Hk + hk;
         Ptr p;
-        p.qg = Qgi + cb * 1024 + w4 * 256 + lane;
+        p.qg = Qi + ck * 1024 + w4 * 256 + lane;
         p.qk = QKi + cb * 1024 + w4 * 128 + lane;
+        p.g = Gi + cb * 64 + 16 * w4 + 4 * q4;
         return p;
     };
     auto load_part = [&](const Ptr &p, OutOps &op, int part) {
@@ -1159,6 +1176,7 @@ __global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
 #pragma unroll
             for (int s = 0; s < 4; s++)
                 op.qg[s] = p.qg[64 * s];
+            op.g = *(const float4 *)p.g;
         } else {
 #pragma unroll
             for (int s = 0; s < 2; s++) {
@@ -1183,6 +1201,15 @@ __global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
         __builtin_amdgcn_sched_barrier(0);
         load_part(np, nx, 0);
         __builtin_amdgcn_sched_barrier(0);
+        { /* O = e^G (Q S) + QKm V' */
+            const float gv[4] = {op.g.x, op.g.y, op.g.z, op.g.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float eg = fast_exp(gv[i]);
+                O[0][i] *= eg;
+                O[1][i] *= eg;
+            }
+        }
         lds_barrier(); /* 2 */
         bf16x8 v2h[2][2], v2l[2][2];
 #pragma unroll
@@ -1241,7 +1268,7 @@ __global__ __launch_bounds__(CB_THREADS) void gdn_chunk_b_kernel(
  * since a few branches give few workgroups) owns state columns 16w..16w+15:
  * its S^T fragments (bf16) are read once into registers, then per segment it
  * computes those columns of
- *   V' = U - W S (hi + lo),  O = (Q e^G) S + QKm V'
+ *   V' = U - W S (hi + lo),  O = e^G (Q S) + QKm V'
  * for the 16-row blocks that hold tokens (the fragments and split products
  * of gdn_chunk_b_kernel), and the workgroup applies the gated RMSNorm of
  * gdn_norm_gate_kernel to the segment's fp32 rows. */
@@ -1249,12 +1276,12 @@ constexpr int SB_WGS = 512;
 constexpr int SB_THREADS = 512; /* 8 waves, 16 state columns each */
 
 __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
-    const bf16x8 *__restrict__ Wi, const bf16x8 *__restrict__ Qgi, const bf16x8 *__restrict__ QKi,
-    const float4 *__restrict__ Ui, const int32_t *__restrict__ chunk_tok0,
-    const int32_t *__restrict__ chunk_len, const int32_t *__restrict__ seg_chunk0,
-    const int32_t *__restrict__ seg_nchunk, int nseg, int spw, const float *__restrict__ S_in,
-    int Hv, const bf16 *__restrict__ z, int zs, const float *__restrict__ nw, float eps,
-    bf16 *__restrict__ y) {
+    const bf16x8 *__restrict__ Wi, const bf16x8 *__restrict__ Qi, const bf16x8 *__restrict__ QKi,
+    const float4 *__restrict__ Ui, const float *__restrict__ Gi,
+    const int32_t *__restrict__ chunk_tok0, const int32_t *__restrict__ chunk_len,
+    const int32_t *__restrict__ seg_chunk0, const int32_t *__restrict__ seg_nchunk, int nseg,
+    int spw, const float *__restrict__ S_in, int Hv, int Hk, const bf16 *__restrict__ z, int zs,
+    const float *__restrict__ nw, float eps, bf16 *__restrict__ y) {
     /* S^T staging at the start, then each segment's fp32 O rows */
     __shared__ __attribute__((aligned(16))) unsigned char so_raw[sizeof(bf16) * DV * (DK + 8)];
     __shared__ __attribute__((aligned(16))) bf16 vTh[DV][CH + 8]; /* V'^T hi [column][token] */
@@ -1263,7 +1290,7 @@ __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
     float(*ob)[DV + 4] = reinterpret_cast<float(*)[DV + 4]>(so_raw);
     static_assert(sizeof(float) * CH * (DV + 4) <= sizeof(bf16) * DV * (DK + 8), "O staging");
 
-    const int hv = blockIdx.y, sg0 = blockIdx.x * spw;
+    const int hv = blockIdx.y, sg0 = blockIdx.x * spw, hk = hv / (Hv / Hk);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q4 = lane >> 4, c16 = lane & 15;
@@ -1318,7 +1345,7 @@ __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
         const int ch = seg_chunk0 ? seg_chunk0[seg] : seg;
         const int t0 = chunk_tok0[ch], L = chunk_len[ch];
         const int nrb = (L + 15) >> 4, nks = (L + 31) >> 5;
-        const size_t cb = (size_t)ch * Hv + hv;
+        const size_t cb = (size_t)ch * Hv + hv, ck = (size_t)ch * Hk + hk;
 
         floatx4 O[4];
 #pragma unroll
@@ -1330,8 +1357,9 @@ __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 w[s] = Wi[cb * 1024 + rb * 256 + 64 * s + lane];
-                qg[s] = Qgi[cb * 1024 + rb * 256 + 64 * s + lane];
+                qg[s] = Qi[ck * 1024 + rb * 256 + 64 * s + lane];
             }
+            const float4 gq = *(const float4 *)(Gi + cb * 64 + 16 * rb + 4 * q4);
             /* U fragment of the 32-column block holding these 16 columns:
              * values 0..3 its first 16 columns, 4..7 the second */
             const float4 *up = Ui + (cb * 1024 + ((wave >> 1) * 4 + rb) * 64 + lane) * 2;
@@ -1342,6 +1370,11 @@ __global__ __launch_bounds__(SB_THREADS) void gdn_short_b_kernel(
                 V = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[s], sb[s], V, 0, 0, 0);
                 O[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qg[s], sb[s], O[rb], 0, 0, 0);
             }
+            /* O = e^G (Q S) + QKm V' */
+            O[rb][0] *= fast_exp(gq.x);
+            O[rb][1] *= fast_exp(gq.y);
+            O[rb][2] *= fast_exp(gq.z);
+            O[rb][3] *= fast_exp(gq.w);
             const float uf[4] = {uu.x, uu.y, uu.z, uu.w};
             bf16x4 ph, pl;
 #pragma unroll
@@ -1740,7 +1773,7 @@ extern "C" hipError_t k_gdn_conv_prep(const bf16_t *proj, int proj_stride, const
  * applies the norm itself either way (*o_pending = 0). */
 static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *S_out,
                               const bf16_t *z, int z_stride, const float *norm_w, float eps,
-                              int Hv, bf16_t *y, const cujev_gdn_scratch *ws, int N,
+                              int Hk, int Hv, bf16_t *y, const cujev_gdn_scratch *ws, int N,
                               const TailJob &tail, hipStream_t stream, bool norm = true,
                               int *o_pending = nullptr) {
     if (o_pending)
@@ -1755,10 +1788,10 @@ static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *
                                dim3(256), 0, stream, tail.proj, tail.ps, tail.conv_in,
                                tail.conv_out, tail.seg0_len, tail.C);
         hipLaunchKernelGGL(gdn_short_b_kernel, dim3((unsigned)CEIL_DIV(units, spw), (unsigned)Hv),
-                           dim3(SB_THREADS), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
-                           (const bf16x8 *)ws->QK, (const float4 *)ws->U, ck->chunk_tok0,
+                           dim3(SB_THREADS), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Q,
+                           (const bf16x8 *)ws->QK, (const float4 *)ws->U, ws->G, ck->chunk_tok0,
                            ck->chunk_len, packed ? nullptr : ck->seg_chunk0,
-                           packed ? nullptr : ck->seg_nchunk, units, spw, S_in, Hv,
+                           packed ? nullptr : ck->seg_nchunk, units, spw, S_in, Hv, Hk,
                            (const bf16 *)z, z_stride, norm_w, eps, (bf16 *)y);
         return hipGetLastError();
     }
@@ -1767,10 +1800,10 @@ static hipError_t gdn_phase_b(const cujev_chunks *ck, const float *S_in, float *
     const int units = ck->num_segments * Hv;
     const int ntail = tail.conv_out ? CEIL_DIV(tail.C, CB_THREADS) : 0;
     hipLaunchKernelGGL(gdn_chunk_b_kernel, dim3((unsigned)(NCB * CEIL_DIV(units, 8) * 8 + ntail)),
-                       dim3(CB_THREADS), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Qg,
-                       (const bf16x8 *)ws->QK, (const bf16x8 *)ws->KgT, (const float4 *)ws->U,
-                       ws->Glast, ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk,
-                       S_in, S_out, Hv, units, ws->O, tail);
+                       dim3(CB_THREADS), 0, stream, (const bf16x8 *)ws->W, (const bf16x8 *)ws->Q,
+                       (const bf16x8 *)ws->QK, (const bf16x8 *)ws->KT, (const float4 *)ws->U,
+                       ws->G, ck->chunk_tok0, ck->chunk_len, ck->seg_chunk0, ck->seg_nchunk,
+                       S_in, S_out, Hv, Hk, units, ws->O, tail);
     if (!norm) {
         if (o_pending)
             *o_pending = 1;
@@ -1791,9 +1824,9 @@ extern "C" hipError_t k_gdn_scan(const float *q, const float *k, const float *v,
     const int npairs = CEIL_DIV(Hv / Hk, 2);
     hipLaunchKernelGGL(gdn_chunk_a_kernel<0>, dim3((unsigned)ck->num_chunks, (unsigned)(Hk * npairs)),
                        dim3(PA_THREADS), 0, stream, q, k, v, g, beta, ConvSrc{}, ck->chunk_tok0,
-                       ck->chunk_len, ck->chunk_starts, Hk, Hv, npairs, (bf16 *)ws->W, (bf16 *)ws->Qg,
-                       (bf16 *)ws->QK, (bf16 *)ws->KgT, ws->U, ws->Glast);
-    return gdn_phase_b(ck, S_in, S_out, z, z_stride, norm_w, eps, Hv, y, ws, N, TailJob{},
+                       ck->chunk_len, ck->chunk_starts, Hk, Hv, npairs, (bf16 *)ws->W, (bf16 *)ws->Q,
+                       (bf16 *)ws->QK, (bf16 *)ws->KT, ws->U, ws->G);
+    return gdn_phase_b(ck, S_in, S_out, z, z_stride, norm_w, eps, Hk, Hv, y, ws, N, TailJob{},
                        stream);
 }
 
@@ -1885,8 +1918,8 @@ static hipError_t gdn_layer(const bf16_t *proj, int proj_stride, const float *co
                        (const float *)nullptr, (const float *)nullptr, (const float *)nullptr,
                        (const float *)nullptr, (const float *)nullptr, cv, ck->chunk_tok0,
                        ck->chunk_len, ck->chunk_starts, Hk, Hv, npairs, (bf16 *)ws->W,
-                       (bf16 *)ws->Qg, (bf16 *)ws->QK, (bf16 *)ws->KgT, ws->U, ws->Glast);
-    return gdn_phase_b(ck, S_in, S_out, proj + C, proj_stride, norm_w, eps, Hv, y, ws, N, tail,
+                       (bf16 *)ws->Q, (bf16 *)ws->QK, (bf16 *)ws->KT, ws->U, ws->G);
+    return gdn_phase_b(ck, S_in, S_out, proj + C, proj_stride, norm_w, eps, Hk, Hv, y, ws, N, tail,
                        stream, norm, o_pending);
 }
 

@@ -131,32 +131,37 @@ typedef struct cujev_chunks {
     int max_seg_len; /* longest segment in tokens (host-side); 0 = not known */
 } cujev_chunks;
 
-/* Scratch of the chunked scan. Per (chunk, v-head), written by the parallel
- * first phase in the MFMA operand-fragment order of the sequential second
- * phase, so each of its lanes reads 16 contiguous bytes per fragment and a
- * wave reads 1 KiB runs:
- *   W, q e^G   [64][128] as 16x16x32 A fragments (4 row blocks x 4 k-steps), bf16
+/* Scratch of the chunked scan, written by the parallel first phase in the
+ * MFMA operand-fragment order of the sequential second phase, so each of its
+ * lanes reads 16 contiguous bytes per fragment and a wave reads 1 KiB runs.
+ * Per (chunk, v-head):
+ *   W          [64][128] as 16x16x32 A fragments (4 row blocks x 4 k-steps), bf16
  *   QK^T masked [64][64] as 16x16x32 A fragments (4 x 2), bf16 hi then lo
- *   (k e^{Glast-G})^T [128][64] as 32x32x16 A fragments (4 x 4), bf16 hi then lo
  *   U          [64][128] as 16x16 accumulator fragments per 32-column block, fp32
- * plus the chunk's total log-decay (one copy per lane). O is the fp32 output
- * [N][Hv][128] before the gated norm. */
+ *   G          [64] cumulative log-decay of each token (restarting at segment
+ *              starts; past the chunk's end the last token's value)
+ * Per (chunk, k-head), shared by the k-head's v-heads (their decays are
+ * applied in the second phase):
+ *   Q          [64][128] as 16x16x32 A fragments, bf16
+ *   K^T        [128][64] as 32x32x16 A fragments (4 x 4), bf16 hi then lo
+ * O is the fp32 output [N][Hv][128] before the gated norm. The per-k-head
+ * arrays are sized per v-head (Hk <= Hv). */
 typedef struct cujev_gdn_scratch {
-    void *W;      /* bf16 [chunks][Hv][1024][8] */
-    void *Qg;     /* bf16 [chunks][Hv][1024][8] */
-    void *QK;     /* bf16 [chunks][Hv][2][512][8]  */
-    void *KgT;    /* bf16 [chunks][Hv][2][1024][8] */
-    float *U;     /* fp32 [chunks][Hv][1024][8] */
-    float *Glast; /* [chunks][Hv][64] (64 equal copies) */
-    float *O;     /* fp32 [N][Hv][128] */
+    void *W;  /* bf16 [chunks][Hv][1024][8] */
+    void *Q;  /* bf16 [chunks][Hk][1024][8] */
+    void *QK; /* bf16 [chunks][Hv][2][512][8]  */
+    void *KT; /* bf16 [chunks][Hk][2][1024][8] */
+    float *U; /* fp32 [chunks][Hv][1024][8] */
+    float *G; /* [chunks][Hv][64] */
+    float *O; /* fp32 [N][Hv][128] */
 } cujev_gdn_scratch;
 
 static inline size_t cujev_align256(size_t x) { return (x + 255) / 256 * 256; }
 static inline size_t cujev_gdn_scratch_bytes(int num_chunks, int Hv, int N) {
     const size_t ch = (size_t)num_chunks * Hv;
-    return 2 * cujev_align256(ch * 64 * 128 * 2) /* W, Qg */ +
+    return 2 * cujev_align256(ch * 64 * 128 * 2) /* W, Q */ +
            cujev_align256(ch * 64 * 64 * 2 * 2) /* QK hi + lo */ +
-           cujev_align256(ch * 64 * 128 * 2 * 2) /* KgT hi + lo */ +
+           cujev_align256(ch * 64 * 128 * 2 * 2) /* K^T hi + lo */ +
            cujev_align256(ch * 64 * 128 * 4) /* U */ + cujev_align256(ch * 64 * 4) +
            cujev_align256((size_t)N * Hv * 128 * 4);
 }
@@ -167,15 +172,15 @@ static inline cujev_gdn_scratch cujev_gdn_scratch_carve(void *base, int num_chun
     cujev_gdn_scratch s;
     s.W = p;
     p += cujev_align256(ch * 64 * 128 * 2);
-    s.Qg = p;
+    s.Q = p;
     p += cujev_align256(ch * 64 * 128 * 2);
     s.QK = p;
     p += cujev_align256(ch * 64 * 64 * 2 * 2);
-    s.KgT = p;
+    s.KT = p;
     p += cujev_align256(ch * 64 * 128 * 2 * 2);
     s.U = (float *)p;
     p += cujev_align256(ch * 64 * 128 * 4);
-    s.Glast = (float *)p;
+    s.G = (float *)p;
     p += cujev_align256(ch * 64 * 4);
     s.O = (float *)p;
     return s;

@@ -117,13 +117,14 @@ def gdn_chunk_emulated(q, k, v, g, beta, S0=None, chunk=64, split=()):
     already applied and rounded). Per chunk and head:
       A = tril(beta_i k_i.k_j e^{G_i-G_j}, -1);  T = (I + A)^-1   (fp32)
       W = bf16(bf16(T) bf16(beta e^G K)),  U = bf16(bf16(T) bf16(beta V))
-      Qg = bf16(q e^G), QKm = bf16(tril(q.k e^{G_i-G_j})), KgT = bf16(K e^{Gl-G})
-      V' = bf16(U - W bf16(S)),  O = Qg bf16(S) + QKm V'
-      S = e^{Gl} S + KgT^T V'     (S itself stays fp32)
+      Q = bf16(q), QKm = bf16(tril(q.k e^{G_i-G_j})), KT = bf16(K) (per k-head)
+      V' = bf16(U - W bf16(S)),  D = bf16(e^{Gl-G} (U - W bf16(S)))
+      O = e^G (Q bf16(S)) + QKm V'
+      S = e^{Gl} S + KT^T D       (S itself stays fp32)
     O is returned rounded to bf16, as the kernel stores it. `split` names
-    operands carried as hi + lo bf16 pairs instead: any of "S", "Vp", "T",
-    "W", "U", "Qg", "QK", "KgT", "O" (and, in request_logits, "qkv" for
-    the staged q, k, v).
+    operands carried as hi + lo bf16 pairs instead: any of "S", "Vp" (V' and
+    D), "T", "W", "U", "Q", "QK", "KT", "O" (and, in request_logits, "qkv"
+    for the staged q, k, v).
     Pinned by tests/test_request_oracle.py: with every operand split it
     matches gdn_chunked to ~1e-4, and each unsplit rounding point moves the
     result by the size a bf16 rounding implies.
@@ -147,14 +148,16 @@ def gdn_chunk_emulated(q, k, v, g, beta, S0=None, chunk=64, split=()):
             Tb = _rb(Tm, "T" in sp)
             W = _rb(Tb @ _rb(K * (bt * np.exp(G))[:, None], "W" in sp), "W" in sp)
             U = _rb(Tb @ _rb(Vv * bt[:, None], "U" in sp), "U" in sp)
-            Qg = _rb(Q * np.exp(G)[:, None], "Qg" in sp)
+            Qb = _rb(Q, "Q" in sp)
             QK = _rb(np.tril((Q @ K.T) * dec), "QK" in sp)
-            KgT = _rb(K * np.exp(G[-1] - G)[:, None], "KgT" in sp)
+            Kb = _rb(K, "KT" in sp)
             Sb = _rb(S[h], "S" in sp)
-            Vn = _rb(U - W @ Sb, "Vp" in sp)
-            oc = Qg @ Sb + QK @ Vn
+            Vx = U - W @ Sb
+            Vn = _rb(Vx, "Vp" in sp)
+            Vd = _rb(Vx * np.exp(G[-1] - G)[:, None], "Vp" in sp)
+            oc = np.exp(G)[:, None] * (Qb @ Sb) + QK @ Vn
             o[c0:c1, h] = _rb(oc, "O" in sp)
-            S[h] = np.exp(G[-1]) * S[h] + KgT.T @ Vn
+            S[h] = np.exp(G[-1]) * S[h] + Kb.T @ Vd
     return o, S
 
 

@@ -18,11 +18,7 @@ and RMS 0.021 from float64. Asserted:
     largest jitter seed's;
   * against float64, max |dp| and RMS within 1.5x of "engine"'s own: the
     engine is no further from the exact math than the reference engine is;
-  * max |dp| against "engine" within 3x the jitter floor. This build
-    differs from "engine" in more than summation order (the state
-    prefill's GDN scan runs the chunked form with split-bf16 products,
-    about 16 significant bits, where "engine" runs the recurrence in fp32;
-    GEMM sums are fp32, not float64); the figure is printed.
+  * max |dp| against "engine" within 1.5x the jitter floor.
 """
 import os
 import sys
@@ -94,4 +90,4 @@ def test_config5_numerics_against_oracle():
           flush=True)
     assert rms["engine"] <= FLOOR_FACTOR * floor_rms
     assert dp["f64"] <= FLOOR_FACTOR * ref_dp and rms["f64"] <= FLOOR_FACTOR * ref_rms
-    assert dp["engine"] <= 3.0 * floor_dp
+    assert dp["engine"] <= FLOOR_FACTOR * floor_dp
