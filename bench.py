@@ -427,7 +427,7 @@ def kernel_rooflines():
                        "traffic": kernel_bench.measured_traffic("attention"),
                        "traffic_source": "rocprofv3 --pmc FETCH_SIZE x2 + WRITE_SIZE x1 "
                                          "(copy-calibrated), bytes per launch, measured at "
-                                         + kernel_bench.MEASURED_AT,
+                                         + kernel_bench.MEASURED_AT["attention"],
                        "us_per_launch": round(att["us"], 2),
                        "flop_per_launch": att["flop"]}
     gdn = gdn_roofline()
@@ -440,7 +440,7 @@ def kernel_rooflines():
                            "us_per_layer": round(gdn["us"], 2),
                            "compulsory_bytes": gdn["bytes"],
                            "traffic": kernel_bench.measured_traffic("gdn"),
-                           "traffic_measured_at": kernel_bench.MEASURED_AT}
+                           "traffic_measured_at": kernel_bench.MEASURED_AT["gdn"]}
     gbr = gdn_roofline(case="gdn_branch")
     log(f"gdn config 2 branches: {gbr['us']:.1f} us, {gbr['gbs']:.1f} GB/s")
     res["gdn_branch_roofline"] = {"kernel": "gdn layer call: chunk_a (conv and gates inside, "
@@ -451,7 +451,7 @@ def kernel_rooflines():
                                   "us_per_layer": round(gbr["us"], 2),
                                   "compulsory_bytes": gbr["bytes"],
                                   "traffic": kernel_bench.measured_traffic("gdn_branch"),
-                                  "traffic_measured_at": kernel_bench.MEASURED_AT}
+                                  "traffic_measured_at": kernel_bench.MEASURED_AT["gdn_branch"]}
     return res
 
 

@@ -21,21 +21,20 @@ from __future__ import annotations
 import sys
 
 # HBM traffic per launch, measured with rocprofv3 --pmc on MI355X (one
-# counter group per run): FETCH_SIZE and WRITE_SIZE in KiB per dispatch,
-# summed over the kernels of the case. A plain 256 MiB device copy reads
-# 131085 KiB of FETCH_SIZE and 262144 KiB of WRITE_SIZE, so FETCH_SIZE is
-# scaled by 2 and WRITE_SIZE by 1. Measured at commit 386a920 (the kernel
-# reworks since fa3acd9 moved no bytes: same counts within 0.5 %); re-measure
-# after changing a kernel.
+# counter per run): FETCH_SIZE and WRITE_SIZE in KiB per dispatch, summed
+# over the kernels of the case. A plain 256 MiB device copy reads 131085 KiB
+# of FETCH_SIZE and writes 262144 KiB of WRITE_SIZE, so FETCH_SIZE is scaled
+# by 2 and WRITE_SIZE by 1. MEASURED_AT names the commit each case's counters
+# were taken at; re-measure after changing one of its kernels.
 COPY_SCALE = {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0}
-MEASURED_AT = "386a920"
+MEASURED_AT = {"attention": "06180c0", "gdn": "06180c0", "gdn_branch": "06180c0"}
 MEASURED_KIB = {
-    "attention": {"FETCH_SIZE": 115072.3, "WRITE_SIZE": 32800.1},
+    "attention": {"FETCH_SIZE": 115108.0, "WRITE_SIZE": 32807.7},
     # chunk_a<1>, chunk_b (with the conv-tail workgroups), norm_gate
-    "gdn": {"FETCH_SIZE": 18182.2 + 57560.9 + 24595.3,
-            "WRITE_SIZE": 115159.4 + 34912.0 + 16384.0},
+    "gdn": {"FETCH_SIZE": 18172.3 + 57601.8 + 24595.2,
+            "WRITE_SIZE": 90400.3 + 34912.0 + 16384.0},
     # chunk_a<2>, short_b
-    "gdn_branch": {"FETCH_SIZE": 9843.2 + 32824.4, "WRITE_SIZE": 57563.5 + 8192.0},
+    "gdn_branch": {"FETCH_SIZE": 9839.4 + 30838.9, "WRITE_SIZE": 45189.4 + 8192.0},
 }
 
 
