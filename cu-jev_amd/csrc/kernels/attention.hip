@@ -52,11 +52,14 @@ constexpr int V_BYTES = D * BK * 2; /* 32 KiB: V^T tile [256][64]  */
 /* LDS: V^T buffers first, K buffers after, so every ds_read offset of a
  * buffer fits the 16-bit immediate from one per-lane base register. */
 constexpr int V_OFF = 0, K_OFF = 2 * V_BYTES, LDS_BYTES = 2 * V_BYTES + 2 * K_BYTES;
-/* Shift of the base-2 softmax: p = 2^(s - mu) for any reference mu is exact
- * (mu cancels in o / l, and bf16/fp32 rounding of p commute with powers of
- * two), so mu only has to keep p in range. It stays 0 while the running max m
- * is within +-SHIFT_RANGE of it (p <= 2^64, the largest p >= 2^-64) and moves
- * to m when m leaves that window, rescaling o and l. */
+/* Shift of the base-2 softmax: mu cancels in o / l, so any reference mu
+ * gives the same softmax and only has to keep p = 2^(s - mu) in range. It
+ * stays 0 while the running max m is within +-SHIFT_RANGE of it (p <= 2^64,
+ * the largest p >= 2^-64) and moves to m when m leaves that window,
+ * rescaling o and l. The bf16 rounding of p then happens at other points
+ * than the reference's (which rounds 2^(s - m) against the running max): the
+ * two roundings agree only where m - mu is a whole number, and otherwise
+ * differ by up to one bf16 ulp of p, an equally valid rounding. */
 constexpr float SHIFT_RANGE = 64.f;
 
 /* 16-byte chunk swizzles: the 16 lanes of one ds_read_b128 phase hit 16
