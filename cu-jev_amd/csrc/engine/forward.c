@@ -57,16 +57,19 @@ typedef struct {
 
 /* Projection GEMMs Y[N,M] = X[N,K] W^T. For few tokens (the eval, N <= 96)
  * the hand-written weight-streaming kernel reads the pre-tiled copy of the
- * weight (its time is the HBM stream of W). Prefill token counts go to
- * hipBLASLt on the plain rows, except where the hand-tiled prefill kernel
- * (gemm_wide, same tiled copy) measured faster on MI355X: the fused
- * gate|up + silu_mul projection up to 2048 tokens and down_proj, split over
- * K into partials the residual add sums, up to 1000 tokens (hipBLASLt with
- * bf16 output measured faster at 1024: 4B prefill of 1024 tokens 10.20 ->
- * 10.02 ms, 9B 15.92 -> 15.39 ms; the kernel is faster at 530-640). Above
- * 2048 tokens hipBLASLt + silu_mul measured faster for gate|up: a 4B eval of
- * 2560 tokens 25.48 -> 25.09 ms, and the 9B request with its 4096-token eval
- * 155.6 -> 150.9 ms (about 150 us per layer off the kernel's 781 us).
+ * weight (its time is the HBM stream of W). Up to 1000 tokens the
+ * hand-tiled prefill kernel (gemm_wide, same tiled copy) takes every
+ * projection: measured on MI355X against hipBLASLt on the plain rows, with
+ * cold weights, for the 4B shapes at 256-800 tokens it took 0.69-0.89 of
+ * the time for qkv and in_proj, 0.55-0.69 for o_proj / out_proj and
+ * 0.52-0.61 for down_proj (the last two split over K into fp32 partials
+ * that the residual add sums), and 0.65-0.89 for the gated gate|up + silu.
+ * At 1024 tokens hipBLASLt was faster for in_proj (69 against 77 us), so
+ * above 1000 tokens the projections go to hipBLASLt, except gate|up, which
+ * stays on the kernel up to 2048 tokens (0.84-1.03 of hipBLASLt + silu_mul
+ * there); above that hipBLASLt + silu_mul measured faster for gate|up: a 4B
+ * eval of 2560 tokens 25.48 -> 25.09 ms, and the 9B request with its
+ * 4096-token eval 155.6 -> 150.9 ms.
  * CUJEV_SMALL_GEMM=0 / CUJEV_WIDE_GEMM=0 send those shapes to hipBLASLt. */
 static int env_on(const char *name) {
     const char *e = getenv(name);
@@ -81,7 +84,7 @@ static int small_gemm_ok(int N, int M, int K) {
 }
 
 #define CUJEV_WIDE_GATED_MAX_N 2048
-#define CUJEV_WIDE_RESID_MAX_N 1000
+#define CUJEV_WIDE_MAX_N 1000
 static int wide_gemm_on(void) {
     static int cached = -1;
     if (cached < 0)
@@ -93,15 +96,18 @@ static hipError_t proj_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, co
                             bf16_t *Y, int N, int M, int K) {
     if (Wt && small_gemm_ok(N, M, K))
         return k_gemm_small(X, K, Wt, N, M, K, 0, 1, Y, M, NULL, m->stream);
+    int rg, ng, sp;
+    if (Wt && wide_gemm_on() && N <= CUJEV_WIDE_MAX_N &&
+        cujev_gemm_wide_plan(N, M, K, 0, 1, &rg, &ng, &sp) == 0)
+        return k_gemm_wide(X, K, Wt, N, M, K, 0, rg, ng, 1, Y, M, NULL, m->stream);
     return k_gemm(m->gemm, X, W, Y, 0, N, M, K, m->stream);
 }
 
 /* A projection whose output feeds the residual add (o_proj, out_proj,
  * down_proj: M = H). Returns through *y / *yp / *splits what the following
- * k_add_rmsnorm reads: bf16 rows, or split-K fp32 partials in m->ypart.
- * `wide`: the prefill kernel may take it (down_proj). */
+ * k_add_rmsnorm reads: bf16 rows, or split-K fp32 partials in m->ypart. */
 static hipError_t resid_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, const bf16_t *Wt,
-                             int N, int M, int K, int wide, const bf16_t **y, const float **yp,
+                             int N, int M, int K, const bf16_t **y, const float **yp,
                              int *splits) {
     *y = m->y;
     *yp = NULL;
@@ -116,7 +122,7 @@ static hipError_t resid_gemm(cujev_model *m, const bf16_t *X, const bf16_t *W, c
         }
         return k_gemm_small(X, K, Wt, N, M, K, 0, 1, m->y, M, NULL, m->stream);
     }
-    if (Wt && wide && wide_gemm_on() && N <= CUJEV_WIDE_RESID_MAX_N) {
+    if (Wt && wide_gemm_on() && N <= CUJEV_WIDE_MAX_N) {
         size_t cap = m->ypart_bytes / ((size_t)N * M * 4);
         const int max_sp = cap > 8 ? 8 : (int)cap;
         int rg, ng, sp;
@@ -284,11 +290,11 @@ static cujev_status launch_all(cujev_model *m, cujev_state *st, const fwd_launch
                   "gather", l);
             n = B, mix = m->mixl, x = m->xl;
         }
-        K_TRY(resid_gemm(m, mix, w_res, wt_res, n, H, k_res, 0, &ry, &ryp, &rsp), "gemm o/out", l);
+        K_TRY(resid_gemm(m, mix, w_res, wt_res, n, H, k_res, &ry, &ryp, &rsp), "gemm o/out", l);
         K_TRY(k_add_rmsnorm(x, ry, ryp, rsp, ly->post_norm, m->xb, n, H, eps, NULL, 0, s),
               "add+norm", l);
         K_TRY(gate_up_gemm(m, ly, n, I, H), "gemm gate_up", l);
-        K_TRY(resid_gemm(m, m->act, ly->w_down, ly->wt_down, n, H, I, 1, &ry, &ryp, &rsp),
+        K_TRY(resid_gemm(m, m->act, ly->w_down, ly->wt_down, n, H, I, &ry, &ryp, &rsp),
               "gemm down", l);
         K_TRY(k_add_rmsnorm(x, ry, ryp, rsp, last ? m->final_norm : m->layers[l + 1].in_norm,
                             last ? m->hsel : m->xb, n, H, eps, NULL, 0, s),

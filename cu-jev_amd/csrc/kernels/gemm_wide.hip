@@ -20,14 +20,24 @@
  *    row group and step is one contiguous 1 KiB piece of the tiled W (one
  *    16-byte buffer load per lane), loaded one chunk ahead into a ring of 4
  *    register slots.
- *  - X goes through LDS, double buffered by chunk. Thread t stages NG
- *    16-byte pieces of chunk c+1 in registers while chunk c-1 computes, and
- *    writes them into the free buffer at the start of chunk c. The LDS image
- *    of a chunk is [token group][k step][lane] x 16 bytes, i.e. every B
- *    fragment is 1 KiB in lane order (conflict-free ds_read_b128), read one
- *    k step ahead of its MFMAs. Lane l of step i holds k = 64 (i/2) +
- *    16 (l/16) + 8 (i%2) + 0..7 of the chunk, the k assignment of the tiled
- *    W, so the product is the plain dot product.
+ *  - X goes through LDS, double buffered by chunk. Each wave loads its
+ *    share of chunk c+1 into registers while chunk c-1 computes and writes
+ *    it into the free buffer at the start of chunk c. Every load
+ *    instruction reads four whole 256-byte token rows (16 lanes per row):
+ *    loading the B fragments directly (16 tokens x 16 bytes at a 32-byte
+ *    stride per instruction) measured 10-15 % slower on the prefill shapes,
+ *    bound by the scattered addresses rather than the bytes. The LDS image
+ *    of a chunk is token-major, 256 bytes per token, with the 16-byte piece
+ *    p of token t in slot p ^ (t % 16), so that the B fragment reads (16
+ *    tokens at one k piece per quarter wave) hit 16 distinct 4-bank groups.
+ *    Lane l of step i reads k = 64 (i/2) + 16 (l/16) + 8 (i%2) + 0..7 of the
+ *    chunk, the k assignment of the tiled W, so the product is the plain
+ *    dot product.
+ *  - All loads go to registers, so the compiler's in-order vmcnt waits
+ *    hold. (Loading X with buffer_load ... lds measured faster still, but
+ *    those loads can complete out of order with the W loads to registers:
+ *    a partial vmcnt wait then does not cover the W operand, and on
+ *    multi-round grids the products came out wrong.)
  *  - One barrier per chunk. Loads are unconditional (chunk indices clamped,
  *    rows past N read as zero through the buffer range, row groups past M
  *    clamped and never stored).
@@ -132,33 +142,37 @@ __global__ __launch_bounds__(64 * WV, 1) void gemm_wide_kernel(
         return gw_load(wr, wlane, c * wchunk + wofs[r] + (uint32_t)i * 1024u);
     };
 
-    /* X staging: piece p = tid + 64 WV s (s < SPT) of a chunk is token group
-     * p / 256, step i = (p / 64) % 4 (= wave % 4), lane l: token nb BN +
-     * 16 (p / 256) + l%16, 16-byte piece 8 (i/2) + 2 (l/16) + i%2 of the
-     * chunk; it lands at LDS byte 16 p. */
+    /* X staging: instruction s of wave w loads local tokens 4 (w + WV s) +
+     * 0..3 into registers, one 256-byte row per 16 lanes (lane l: 16-byte
+     * piece l % 16 of token 4 (w + WV s) + l / 16), and writes piece p of
+     * token t to slot p ^ (t % 16) of that token's 256-byte LDS row. t % 16
+     * does not depend on s (4 WV is a multiple of 16). */
     const __amdgpu_buffer_rsrc_t xr = gw_rsrc(X, (uint32_t)((size_t)N * ldx * 2));
-    const int xi = wave & 3;
-    const int kpiece = 8 * (xi >> 1) + 2 * q + (xi & 1);
-    const uint32_t xrow0 = (uint32_t)(nb * BN + 16 * (wave >> 2) + c16) * (uint32_t)ldx * 2u +
-                           (uint32_t)kpiece * 16u;
-    const uint32_t xstride = (uint32_t)(16 * WV / 4) * (uint32_t)ldx * 2u; /* between pieces */
+    const int tl0 = 4 * wave + (lane >> 4);
+    const uint32_t xoff = (uint32_t)(nb * BN + tl0) * (uint32_t)ldx * 2u + (uint32_t)(c16 * 16);
+    const uint32_t xstride = (uint32_t)(4 * WV) * (uint32_t)ldx * 2u; /* between instructions */
+    const uint32_t xdst = (uint32_t)(tl0 * 256 + ((c16 ^ (tl0 & 15)) * 16));
     auto ldx_chunk = [&](int cl, bf16x8 (&xs)[SPT]) {
         const uint32_t kb = (uint32_t)(c0 + min(cl, nch - 1)) * (GW_KC * 2);
 #pragma unroll
         for (int s = 0; s < SPT; s++)
-            xs[s] = gw_load(xr, xrow0 + (uint32_t)s * xstride, kb);
+            xs[s] = gw_load(xr, xoff + (uint32_t)s * xstride, kb);
     };
     auto stx_chunk = [&](int buf, const bf16x8 (&xs)[SPT]) {
 #pragma unroll
         for (int s = 0; s < SPT; s++)
-            gw_lds_write(xl, (uint32_t)(buf * XBUF + (tid + 64 * WV * s) * 16), xs[s]);
+            gw_lds_write(xl, (uint32_t)(buf * XBUF + WV * s * 1024) + xdst, xs[s]);
     };
-    /* B fragment (token group j, step i) of buffer b: 1 KiB at
-     * b XBUF + (4 j + i) 1024, lane l at + 16 l */
+    /* B fragment (token group j, step i) of buffer b: lane l reads token
+     * 16 j + l%16, piece 8 (i/2) + 2 (l/16) + i%2, from its swizzled slot */
+    uint32_t boff[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        boff[i] = (uint32_t)(c16 * 256 + (((8 * (i >> 1) + 2 * q + (i & 1)) ^ c16) * 16));
     auto ldb = [&](int buf, int i, bf16x8 (&b)[NG]) {
 #pragma unroll
         for (int j = 0; j < NG; j++)
-            b[j] = gw_lds_read(xl, (uint32_t)(buf * XBUF + j * 4096 + i * 1024 + lane * 16));
+            b[j] = gw_lds_read(xl, (uint32_t)(buf * XBUF + j * 4096) + boff[i]);
     };
 
     floatx4 acc[RG][NG];
@@ -311,10 +325,14 @@ extern "C" int cujev_gemm_wide_supported(int RG, int NG, int gated) {
 }
 
 /* Estimated microseconds of a plan, a linear model fitted to measured
- * launches on MI355X (4B prefill shapes at 530 tokens, every tile and split;
- * mean error 5 %): per round of 256 workgroups, the MFMA cycles of one wave,
- * the bytes a workgroup loads (its W rows and X tokens over its K range) and
- * reads from LDS, plus the partial sums' write + read. */
+ * launches on MI355X (the 4B prefill shapes at 256-2048 tokens, every tile
+ * and split, cold weights; mean error 7 %; on the GEMM time alone its pick
+ * is the measured best in 32 of 35 shape/token cases and within 11 % in
+ * the rest): per
+ * round of 256 workgroups, the MFMA cycles of one wave, the W and X bytes a
+ * workgroup loads over its K range and the bytes its waves read from LDS,
+ * plus a fixed cost per round; with splits, the fp32 partials' write and
+ * the residual add's read of them (about 5 TB/s). */
 static double plan_us(int N, int M, int K, int gated, int RG, int NG, int S) {
     const int rows = gated ? M / 2 : M;
     const int bm = gated ? 32 * RG : 64 * RG;
@@ -323,11 +341,15 @@ static double plan_us(int N, int M, int K, int gated, int RG, int NG, int S) {
     const double rounds = (double)((items + 255) / 256);
     const double nch = (double)K / GW_KC / S;
     const double mfma = nch * 4 * RG * NG * 16;
-    const double l1 = nch * (16384.0 * RG + 256.0 * 16 * NG);
+    const double wbytes = nch * 16384.0 * RG;
+    const double xbytes = nch * 256.0 * 16 * NG;
     const double lds = nch * 16384.0 * NG;
-    double us = rounds * (2.835e-4 * mfma + 8.89e-6 * l1 + 7.40e-6 * lds - 0.67);
-    if (S > 1)
-        us += 0.149 * 2.0 * S * (double)N * M * 4 / 1e6;
+    double us = rounds * (2.667e-4 * mfma + 8.406e-6 * wbytes + 1.016e-6 * xbytes +
+                          4.065e-6 * lds + 4.685);
+    if (S > 1) {
+        const double mb_part = (double)S * N * M * 4 / 1e6;
+        us += 0.1863 * mb_part + 0.2 * mb_part;
+    }
     return us;
 }
 
