@@ -60,11 +60,11 @@ typedef struct {
  * weight (its time is the HBM stream of W). Up to 1000 tokens the
  * hand-tiled prefill kernel (gemm_wide, same tiled copy) takes every
  * projection: measured on MI355X against hipBLASLt on the plain rows, with
- * cold weights, for the 4B shapes at 256-800 tokens it took 0.69-0.89 of
- * the time for qkv and in_proj, 0.55-0.69 for o_proj / out_proj and
+ * cold weights, for the 4B shapes at 256-800 tokens it took 0.69-0.98 of
+ * the time for qkv and in_proj, 0.55-0.74 for o_proj / out_proj and
  * 0.52-0.61 for down_proj (the last two split over K into fp32 partials
  * that the residual add sums), and 0.65-0.89 for the gated gate|up + silu.
- * At 1024 tokens hipBLASLt was faster for in_proj (69 against 77 us), so
+ * At 1024 tokens hipBLASLt was faster for in_proj (69-72 against 77 us), so
  * above 1000 tokens the projections go to hipBLASLt, except gate|up, which
  * stays on the kernel up to 2048 tokens (0.84-1.03 of hipBLASLt + silu_mul
  * there); above that hipBLASLt + silu_mul measured faster for gate|up: a 4B

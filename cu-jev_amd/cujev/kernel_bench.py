@@ -13,6 +13,9 @@ gdn_branch config 2 branches: 64 branches x 16 tokens continuing one state
 gdn_split, gdn_branch_split: the same through conv_prep + scan (two calls)
 gemm_<p>    the few-token kernel on projection p (qkv, in, gate_up, down, o) at
            N = 80 with cold weights; blas_<p> the same on hipBLASLt
+wide_sweep the prefill GEMM: for each 4B projection and token count (argv[2],
+           comma-separated, default 610), hipBLASLt and every tile and split
+           of the hand-tiled kernel, cold weights; one line per launch kind
 copy       a plain device-to-device copy of 256 MiB (scale factor for the
            FETCH_SIZE / WRITE_SIZE counters)
 """
@@ -237,6 +240,62 @@ def time_launches(launch, iters=20, warmup=3):
     return e0.elapsed_time(e1) / iters * 1e3
 
 
+WIDE_TILES = [(2, 8), (2, 12), (3, 8), (3, 12), (4, 6), (4, 8), (4, 10), (4, 12), (6, 4),
+              (6, 6), (6, 8), (8, 4), (8, 6)]
+
+
+def wide_sweep(token_counts, reps=15):
+    """Prefill GEMM timings behind the engine's routing and the plan model's
+    fit: `ROW <projection> <N> blas 0 0 0 <us>` for hipBLASLt on the plain
+    rows and `ROW <projection> <N> wide <RG> <NG> <splits> <us>` for each
+    tile and split of the hand-tiled kernel (fp32 partials where splits >
+    1, the fused silu(gate) * up for gate_up), cold weights (> 800 MB of
+    copies, launched in turn)."""
+    import torch
+    from . import ops
+    ops.load()
+    shapes = [("qkv", 10240, 2560, False, 1), ("in", 12352, 2560, False, 1),
+              ("gate_up", 18432, 2560, True, 1), ("o", 2560, 4096, False, 8),
+              ("down", 2560, 9216, False, 8)]
+    for N in token_counts:
+        for name, M, K, gated, max_splits in shapes:
+            g = torch.Generator(device="cuda").manual_seed(7)
+            X = torch.randn(N, K, device="cuda", generator=g).to(torch.bfloat16)
+            ncopy = max(2, int(800e6 // (M * K * 2)) + 1)
+            W = [(torch.randn(M, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+                 for _ in range(ncopy)]
+            Wt = [ops.gemm_small_tile(w) for w in W]
+            Y = torch.empty(N, M, dtype=torch.bfloat16, device="cuda")
+            act = torch.empty(N, M // 2, dtype=torch.bfloat16, device="cuda")
+            P = torch.empty(min(max_splits, max(1, int(2e9 // (N * M * 4)))), N, M,
+                            dtype=torch.float32, device="cuda")
+            it = [0]
+
+            def timed(fn):
+                def launch():
+                    fn(it[0] % ncopy)
+                    it[0] += 1
+                return time_launches(launch, reps, 3)
+
+            print(f"ROW {name} {N} blas 0 0 0 {timed(lambda i: ops.gemm(X, W[i], Y)):.2f}",
+                  flush=True)
+            for rg, ng in WIDE_TILES:
+                if gated and rg % 2:
+                    continue
+                for sp in range(1, max_splits + 1):
+                    if (K // 128) % sp or sp > P.shape[0]:
+                        continue
+                    if sp == 1:
+                        fn = (lambda i, rg=rg, ng=ng: ops.gemm_wide(
+                            X, Wt[i], Y=act if gated else Y, gated=gated, rg=rg, ng=ng))
+                    else:
+                        fn = (lambda i, rg=rg, ng=ng, sp=sp: ops.gemm_wide(
+                            X, Wt[i], P=P, splits=sp, rg=rg, ng=ng))
+                    print(f"ROW {name} {N} wide {rg} {ng} {sp} {timed(fn):.2f}", flush=True)
+            del W, Wt, P
+            torch.cuda.empty_cache()
+
+
 CASES = {"attention": attention_case, "gdn": gdn_case, "gdn_branch": gdn_branch_case,
          "gdn_split": lambda: gdn_case(fused=False),
          "gdn_branch_split": lambda: gdn_branch_case(fused=False), "copy": copy_case}
@@ -246,6 +305,9 @@ for _g in GEMM_SHAPES:
 
 if __name__ == "__main__":
     name = sys.argv[1]
+    if name == "wide_sweep":
+        wide_sweep([int(n) for n in (sys.argv[2] if len(sys.argv) > 2 else "610").split(",")])
+        sys.exit(0)
     iters = int(sys.argv[2]) if len(sys.argv) > 2 else 20
     warmup = int(sys.argv[3]) if len(sys.argv) > 3 else 3
     launch, info = CASES[name]()
