@@ -219,6 +219,53 @@ def run_recur(o, L, proj, seg_lens, conv_in, S_in):
     return y.float().cpu().numpy()
 
 
+@pytest.mark.parametrize("seg_lens,Hk,Hv,config2", [([70], 2, 4, False), ([5, 64, 1, 33], 16, 32, True),
+                                                     ([3, 9], 1, 3, False)])
+def test_gdn_conv_prep_matches_oracle(seg_lens, Hk, Hv, config2):
+    """The prep stage on its own (gdn_conv_prep, the two-call path's first
+    call): causal conv + SiLU with every segment continuing the state's conv
+    tail, the l2-norms of q and k with q * 128^-1/2, v, g = -e^A softplus(a +
+    dt_bias) and beta = sigmoid(b), per token, against oracle.gdn_conv and
+    oracle.gdn_prep (float64) on the same bf16 inputs; the conv tail after
+    the first segment exactly (REF src/kernels/gdn.cu:4-96)."""
+    o = ops()
+    print(f"conv_prep seg_lens={seg_lens} Hk={Hk} Hv={Hv}", flush=True)
+    L = Layer(31, Hk, Hv, config2=config2)
+    N = sum(seg_lens)
+    proj = L.proj(N)
+    tail = orc.bf16_round(L.rng.standard_normal((L.C, 3)).astype(np.float32)).astype(np.float32)
+    dev = "cuda"
+    t = lambda a: torch.as_tensor(a).to(dev)
+    own_base = np.repeat(np.cumsum([0] + list(seg_lens[:-1])), seg_lens).astype(np.int32)
+    q = torch.empty(N, Hk, DK, dtype=torch.float32, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty(N, Hv, DV, dtype=torch.float32, device=dev)
+    g = torch.empty(N, Hv, dtype=torch.float32, device=dev)
+    beta = torch.empty_like(g)
+    cout = torch.zeros(L.C, 3, dtype=torch.float32, device=dev)
+    o.gdn_conv_prep(bf(proj).to(dev), t(L.conv_w), t(tail), cout, seg_lens[0], t(own_base),
+                    t(L.A_neg), t(L.dt_bias), Hk, Hv, q, k, v, g, beta)
+    torch.cuda.synchronize()
+    x, _, b, a = orc.gdn_split_proj(proj.astype(np.float64), Hk, Hv)
+    rep, start, worst = Hv // Hk, 0, {}
+    for Ls in seg_lens:
+        sl = slice(start, start + Ls)
+        xc = orc.gdn_conv(x[sl], L.conv_w, tail)
+        rq, rk, rv, rg, rb = orc.gdn_prep(xc, b[sl], a[sl], L.A_log, L.dt_bias, Hk, Hv)
+        for name, got, ref in (("q", q[sl].cpu().numpy(), rq[:, ::rep]),
+                               ("k", k[sl].cpu().numpy(), rk[:, ::rep]),
+                               ("v", v[sl].cpu().numpy(), rv), ("g", g[sl].cpu().numpy(), rg),
+                               ("beta", beta[sl].cpu().numpy(), rb)):
+            e = float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+            worst[name] = max(worst.get(name, 0.0), e)
+        start += Ls
+    print("  worst relative error: " + ", ".join(f"{n} {e:.2e}" for n, e in worst.items()))
+    for name, e in worst.items():
+        assert e <= 1e-5, (name, e)
+    np.testing.assert_array_equal(cout.cpu().numpy(),
+                                  orc.gdn_conv_tail(x[: seg_lens[0]], tail).astype(np.float32))
+
+
 @pytest.mark.parametrize("seg_lens,Hk,Hv", [([1, 2, 3, 5, 16, 17, 31, 32], 2, 4),
                                             ([7] * 19, 1, 4), ([20] * 4, 16, 32)])
 def test_gdn_recur_branches(seg_lens, Hk, Hv):
