@@ -2,7 +2,7 @@
 bench.py (timed with HIP events on the launch stream) and runnable on their
 own for profilers:
 
-    python -m cujev.kernel_bench attention|gdn|gdn_branch|gemm_*|blas_*|copy [iters [warmup]]
+    python -m cujev.kernel_bench attention|gdn|gdn_branch|gemm_*|blas_*|wide_*|copy [iters [warmup]]
 
 attention  config 3: Hq 16 / Hkv 4, D 256, state 8192 keys, 256 branches x 16
 gdn        config 2: Hk 16 / Hv 32, T = 2048 prefill through the one-call GDN
@@ -12,7 +12,9 @@ gdn_branch config 2 branches: 64 branches x 16 tokens continuing one state
            (S and the conv tail read, nothing written back), packed chunks
 gdn_split, gdn_branch_split: the same through conv_prep + scan (two calls)
 gemm_<p>    the few-token kernel on projection p (qkv, in, gate_up, down, o) at
-           N = 80 with cold weights; blas_<p> the same on hipBLASLt
+           N = 80 with cold weights; blas_<p> the same on hipBLASLt; wide_<p>
+           the prefill kernel at the deferred pass's 610 tokens on the
+           engine's plan (tile, splits), cold weights
 wide_sweep the prefill GEMM: for each 4B projection and token count (argv[2],
            comma-separated, default 610), hipBLASLt and every tile and split
            of the hand-tiled kernel, cold weights; one line per launch kind
@@ -212,6 +214,38 @@ def gemm_case(name, small=True, N=80):
     return launch, {"bytes": M * K * 2, "copies": ncopy}
 
 
+def wide_case(name, N=610):
+    """One projection of the deferred config-4 pass (610 tokens) on the
+    prefill kernel with the engine's plan (tile and, for the residual
+    projections, split count), cold weights (> 800 MB of copies, launched
+    in turn)."""
+    import torch
+    from . import ops
+    ops.load()
+    M, K, gated = GEMM_SHAPES[name]
+    residual = M <= 4096
+    rg, ng, sp = ops.gemm_wide_plan(N, M, K, gated, 8 if residual else 1)
+    dev = "cuda"
+    ncopy = max(2, int(800e6 // (M * K * 2)) + 1)
+    g = torch.Generator(device=dev).manual_seed(7)
+    X = torch.randn(N, K, device=dev, generator=g).to(torch.bfloat16)
+    Wt = [ops.gemm_small_tile((torch.randn(M, K, device=dev, generator=g) * 0.02)
+                              .to(torch.bfloat16)) for _ in range(ncopy)]
+    Y = torch.empty(N, M // 2 if gated else M, dtype=torch.bfloat16, device=dev)
+    P = torch.empty(sp, N, M, dtype=torch.float32, device=dev)
+    if sp > 1:
+        run = lambda W: ops.gemm_wide(X, W, P=P, splits=sp, rg=rg, ng=ng)
+    else:
+        run = lambda W: ops.gemm_wide(X, W, Y=Y, gated=gated, rg=rg, ng=ng)
+    state = {"i": 0}
+
+    def launch():
+        run(Wt[state["i"] % ncopy])
+        state["i"] += 1
+
+    return launch, {"N": N, "plan": (rg, ng, sp), "copies": ncopy}
+
+
 def copy_case(nbytes=256 << 20):
     import torch
     a = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
@@ -302,6 +336,7 @@ CASES = {"attention": attention_case, "gdn": gdn_case, "gdn_branch": gdn_branch_
 for _g in GEMM_SHAPES:
     CASES["gemm_" + _g] = lambda _g=_g: gemm_case(_g, small=True)
     CASES["blas_" + _g] = lambda _g=_g: gemm_case(_g, small=False)
+    CASES["wide_" + _g] = lambda _g=_g: wide_case(_g)
 
 if __name__ == "__main__":
     name = sys.argv[1]
